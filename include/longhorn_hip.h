@@ -1,0 +1,185 @@
+/*
+ * longhorn_hip.h -- C ABI of liblonghorn_hip.so, the MI355X (gfx950) backend
+ * of LonghornAI's quantized-GEMM path.
+ *
+ * Conventions for every entry point:
+ *   - All array arguments are DEVICE pointers (hipMalloc'd or equivalent),
+ *     row-major, tightly packed, unless stated otherwise.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *     Work is enqueued on it; nothing synchronises.  No entry point
+ *     allocates device memory.
+ *   - Return value: LHQ_OK (0) or an LHQ_ERR_* code; lhq_last_error()
+ *     returns a per-thread message for the last failure.  Nothing throws,
+ *     nothing aborts, and nothing falls back to the CPU.
+ *   - dims are int (int64_t for flat element counts), as in the reference.
+ *
+ * Each entry point names the reference function it replaces (file:line in
+ * the LonghornAI tree).  The reference functions take host pointers and run
+ * on the CPU; the lh:: drop-in library (the kernels/ headers) keeps those
+ * signatures and forwards here.
+ */
+#ifndef LONGHORN_HIP_H
+#define LONGHORN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status ------------------------------------------------------------ */
+#define LHQ_OK 0
+#define LHQ_ERR_INVALID 1     /* null pointer, negative or inconsistent dims */
+#define LHQ_ERR_UNSUPPORTED 2 /* valid for the reference, not for this kernel */
+#define LHQ_ERR_HIP 3         /* the HIP runtime reported an error */
+
+const char* lhq_status_string(int status);
+const char* lhq_last_error(void);
+int lhq_version(void); /* major*10000 + minor*100 + patch */
+
+/* ---- int8 symmetric quantizers: quant.hpp:28-48 / quant.cpp:34-105 ------ */
+/* Per-tensor (quant.hpp:31-34).  The scale lives in device memory. */
+int lhq_q8_quantize_per_tensor(const float* src, int8_t* dst, float* scale_out,
+                               int64_t n, void* stream);
+int lhq_q8_dequantize_per_tensor(const int8_t* src, const float* scale, float* dst,
+                                 int64_t n, void* stream);
+/* Per-row / per-token (quant.hpp:38-41). */
+int lhq_q8_quantize_per_row(const float* src, int8_t* dst, float* scales_out,
+                            int rows, int dim, void* stream);
+int lhq_q8_dequantize_per_row(const int8_t* src, const float* scales, float* dst,
+                              int rows, int dim, void* stream);
+/* Per-token quantization of bfloat16 activations: quant.cpp:52-63 applied to
+ * the exact fp32 widening of each bf16 value (benchmark config 3). */
+int lhq_q8_quantize_per_row_bf16(const uint16_t* src, int8_t* dst, float* scales_out,
+                                 int rows, int dim, void* stream);
+/* Per-column / per-output-channel (quant.hpp:45-48). */
+int lhq_q8_quantize_per_col(const float* src, int8_t* dst, float* scales_out,
+                            int rows, int cols, void* stream);
+int lhq_q8_dequantize_per_col(const int8_t* src, const float* scales, float* dst,
+                              int rows, int cols, void* stream);
+
+/* ---- int4 group quantizers: quant.hpp:50-75 / quant.cpp:111-172 --------- */
+/* Reference layout: packed u8 [K/2, N] (row 2i low nibble, 2i+1 high,
+ * two's-complement int4 in [-7,7]); scales fp32 [K/G, N]. */
+int lhq_q4_quantize_groupwise(const float* src, uint8_t* packed, float* scales_out,
+                              int K, int N, int group_size, void* stream);
+int lhq_q4_dequantize_groupwise(const uint8_t* packed, const float* scales, float* dst,
+                                int K, int N, int group_size, void* stream);
+/* Asymmetric int4 (no reference counterpart; benchmark configs 2, 4, 5):
+ * unsigned codes u in [0,15] packed like the reference, fp16 scale and one
+ * zero-point byte per (group, column); w = (u - z) * s. */
+int lhq_q4a_quantize_groupwise(const float* src, uint8_t* packed, uint16_t* scales_f16,
+                               uint8_t* zeros, int K, int N, int group_size, void* stream);
+int lhq_q4a_dequantize_groupwise(const uint8_t* packed, const uint16_t* scales_f16,
+                                 const uint8_t* zeros, float* dst, int K, int N,
+                                 int group_size, void* stream);
+
+/* ---- FP8 E4M3 quantizers: quant.hpp:77-94 / quant.cpp:176-249 ----------- */
+int lhq_fp8_quantize_per_tensor(const float* src, uint8_t* dst, float* scale_out,
+                                int64_t n, void* stream);
+int lhq_fp8_dequantize_per_tensor(const uint8_t* src, const float* scale, float* dst,
+                                  int64_t n, void* stream);
+int lhq_fp8_quantize_per_row(const float* src, uint8_t* dst, float* scales_out,
+                             int rows, int dim, void* stream);
+int lhq_fp8_dequantize_per_row(const uint8_t* src, const float* scales, float* dst,
+                               int rows, int dim, void* stream);
+int lhq_fp8_quantize_per_col(const float* src, uint8_t* dst, float* scales_out,
+                             int rows, int cols, void* stream);
+int lhq_fp8_dequantize_per_col(const uint8_t* src, const float* scales, float* dst,
+                               int rows, int cols, void* stream);
+
+/* ---- prepacked weight layouts (no reference counterpart: the reference
+ * reads [K/2,N] / [K,N] row-major directly, gemm_quant.cpp:42,66) --------- */
+/* W4 prepacked layout (Nt = ceil(N/16), Kt = ceil(K/128), NG = K/G):
+ *   qweight [Nt][Kt][64][16 B]: a 1 KiB tile holds 16 columns x 128 k; the
+ *     16 bytes of lane l are the B operands of four 16x16x32 MFMAs for column
+ *     16*nt + (l & 15): dword j covers k = 128*kt + 32*j + 8*(l >> 4) + e,
+ *     e = 0..7, element e in nibble (e & 1) ? 4 + e/2 : e/2; codes are
+ *     unsigned (symmetric q is stored as q + 8).
+ *   scales  [Nt][NG][16] fp32 (symmetric) or fp16 (asymmetric).
+ *   zeros   [Nt][ceil(NG/8)][16] u32, group g in nibble g % 8.
+ * Sizes in bytes: */
+int64_t lhq_w4_qweight_bytes(int K, int N);
+int64_t lhq_w4_scales_bytes(int K, int N, int group_size, int fp16_scales);
+int64_t lhq_w4_zeros_bytes(int K, int N, int group_size);
+/* From the reference layout (quant.hpp:52-59; q4_get quant.hpp:68-75):
+ * fp32 scales kept as fp32, implied zero point 8. */
+int lhq_w4_prepack_sym(const uint8_t* packed, const float* scales, int K, int N,
+                       int group_size, uint8_t* qweight, float* scales_out, void* stream);
+/* From the asymmetric layout written by lhq_q4a_quantize_groupwise. */
+int lhq_w4_prepack_asym(const uint8_t* packed, const uint16_t* scales_f16,
+                        const uint8_t* zeros, int K, int N, int group_size,
+                        uint8_t* qweight, uint16_t* scales_out, uint32_t* zeros_out,
+                        void* stream);
+/* 8-bit B operand (int8 or fp8 e4m3) [K, N] -> k-contiguous Bt [Np][Kp]
+ * with Np = N rounded up to 256 and Kp = K rounded up to 128, zero padded. */
+int64_t lhq_b8_prepacked_bytes(int K, int N);
+int lhq_b8_prepack(const uint8_t* B, int K, int N, uint8_t* Bt, void* stream);
+
+/* ---- W4A16 GEMM: gemm_quant.hpp:47-57 / gemm_quant.cpp:54-82 ----------- */
+/* Reference semantics: fp32 A [M,K]; symmetric W4 prepacked by
+ * lhq_w4_prepack_sym; C fp32 [M,N] = beta*C + alpha*A@W (beta == 0 never
+ * reads C).  group_size must be a multiple of 32 that divides K. */
+int lhq_gemm_w4a16(const float* A, const uint8_t* qweight, const float* scales,
+                   float* C, int M, int N, int K, int group_size, float alpha, float beta,
+                   void* stream);
+/* Benchmark configs 2/5: bf16 A [M,K]; asymmetric W4 (fp16 scales, u4
+ * zeros) prepacked by lhq_w4_prepack_asym; bf16 C [M,N] = A@W, fp32 accumulate. */
+int lhq_gemm_w4a16_bf16(const uint16_t* A, const uint8_t* qweight, const uint16_t* scales,
+                        const uint32_t* zeros, uint16_t* C, int M, int N, int K,
+                        int group_size, void* stream);
+/* Uniform batch of independent W4A16 GEMMs (the gemm_batched contract,
+ * gemm.cpp:59-67): A [batch,M,K], weights stacked with the per-matrix
+ * strides lhq_w4_*_bytes, C [batch,M,N]. */
+int lhq_gemm_w4a16_bf16_batched(const uint16_t* A, const uint8_t* qweight,
+                                const uint16_t* scales, const uint32_t* zeros, uint16_t* C,
+                                int batch, int M, int N, int K, int group_size, void* stream);
+/* Ragged grouped W4A16 for MoE experts in ONE launch (benchmark config 4).
+ * Group e owns rows [offsets[e], offsets[e+1]) of A [rows, K] and C [rows, N]
+ * (the expert_offsets table of moe.cpp:111-123, device-resident); its
+ * weights are at qweights[e], scales[e], zeros[e] (device arrays of device
+ * pointers).  row_capacity bounds offsets[E] (the rows A and C hold). */
+int lhq_gemm_w4a16_bf16_grouped(const uint16_t* A, const int32_t* offsets,
+                                const uint8_t* const* qweights,
+                                const uint16_t* const* scales,
+                                const uint32_t* const* zeros, uint16_t* C,
+                                int num_groups, int row_capacity, int N, int K,
+                                int group_size, void* stream);
+
+/* ---- W8A8 GEMM: gemm_quant.hpp:34-45 / gemm_quant.cpp:29-49 ------------ */
+/* Reference semantics, bit-exact: Aq int8 [M,K]; Bt = lhq_b8_prepack(Bq);
+ * C[m,n] = beta-applied C + ((alpha*A_s[m])*B_s[n])*float(acc). */
+int lhq_gemm_w8a8(const int8_t* Aq, const int8_t* Bt, const float* A_scales,
+                  const float* B_scales, float* C, int M, int N, int K, float alpha,
+                  float beta, void* stream);
+/* Benchmark config 3: same, alpha = 1, beta = 0, output rounded to bf16. */
+int lhq_gemm_w8a8_bf16(const int8_t* Aq, const int8_t* Bt, const float* A_scales,
+                       const float* B_scales, uint16_t* C, int M, int N, int K,
+                       void* stream);
+/* Debug: the raw int32 accumulator of gemm_quant.cpp:38-43, [M,N]. */
+int lhq_gemm_w8a8_i32(const int8_t* Aq, const int8_t* Bt, int32_t* acc, int M, int N,
+                      int K, void* stream);
+
+/* ---- FP8 E4M3 GEMM: gemm_quant.hpp:59-70 / gemm_quant.cpp:87-104 ------- */
+/* A e4m3 [M,K]; Bt = lhq_b8_prepack(B e4m3 [K,N]); per-tensor scales in
+ * device memory; C = beta-applied C + ((alpha*sA)*sB)*acc, fp32 acc. */
+int lhq_gemm_fp8_e4m3(const uint8_t* A, const uint8_t* Bt, const float* A_scale,
+                      const float* B_scale, float* C, int M, int N, int K, float alpha,
+                      float beta, void* stream);
+
+/* ---- fp32 GEMM: gemm.hpp:13-29 / gemm.cpp:5-75 -------------------------- */
+/* lh::gemm semantics (beta first; beta == 0 never reads C). */
+int lhq_gemm_f32(const float* A, const float* B, float* C, int M, int N, int K,
+                 float alpha, float beta, void* stream);
+/* lh::gemm_ref semantics: C = alpha*acc + beta*C, C always read. */
+int lhq_gemm_f32_ref(const float* A, const float* B, float* C, int M, int N, int K,
+                     float alpha, float beta, void* stream);
+int lhq_gemm_f32_batched(const float* A, const float* B, float* C, int batch, int M,
+                         int N, int K, float alpha, float beta, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LONGHORN_HIP_H */

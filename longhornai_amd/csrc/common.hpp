@@ -1,0 +1,170 @@
+// common.hpp -- shared device helpers for the gfx950 quantized-GEMM kernels.
+//
+// Everything here is written for CDNA4 (gfx950) wave64 execution: MFMA
+// operand vector types, bit-exact bf16/fp16/e4m3 conversions that reproduce
+// the reference's software dtypes (dtypes.hpp:17-196), and the status
+// plumbing of the C ABI (include/longhorn_hip.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "longhorn_hip.h"
+
+namespace lhq {
+
+// ---------------------------------------------------------------------------
+// MFMA operand types (verified lane layouts, gfx950):
+//   16x16xK: lane l holds row/col (l & 15), K-slice (l >> 4);
+//            D element j of lane l is D[4*(l>>4) + j][l & 15].
+//   32x32xK: lane l holds row/col (l & 31), K-slice (l >> 5);
+//            D element j of lane l is D[8*(j>>2) + 4*(l>>5) + (j&3)][l & 31].
+// ---------------------------------------------------------------------------
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(16))) float f32x16_t;
+typedef __attribute__((ext_vector_type(4))) int i32x4_t;
+typedef __attribute__((ext_vector_type(16))) int i32x16_t;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4_t;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2_t;
+
+__device__ __forceinline__ f32x4_t mfma_bf16_16x16x32(u32x4_t a, u32x4_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16_t mfma_bf16_32x32x16(u32x4_t a, u32x4_t b, f32x16_t c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ i32x16_t mfma_i8_32x32x32(u32x4_t a, u32x4_t b, i32x16_t c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4_t, a),
+                                                 __builtin_bit_cast(i32x4_t, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ i32x4_t mfma_i8_16x16x64(u32x4_t a, u32x4_t b, i32x4_t c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4_t, a),
+                                                 __builtin_bit_cast(i32x4_t, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4_t mfma_fp8_16x16x32(u32x2_t a, u32x2_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(__builtin_bit_cast(long, a),
+                                                      __builtin_bit_cast(long, b), c, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
+// Bit-exact conversions (same results as the reference software dtypes).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+    return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+// RNE on the dropped 16 bits; NaN keeps its payload with the quiet bit set
+// (dtypes.hpp:87-98).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t x = __float_as_uint(f);
+    if ((x & 0x7f800000u) == 0x7f800000u && (x & 0x7fffffu))
+        return static_cast<uint16_t>((x >> 16) | 0x40u);
+    x += 0x7fffu + ((x >> 16) & 1u);
+    return static_cast<uint16_t>(x >> 16);
+}
+// Two fp32 -> packed bf16 pair with the same rounding (low half = a).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    return static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+}
+// binary16 -> fp32 (exact for every encoding; dtypes.hpp:57-85).
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+// fp32 -> E4M3 with the reference's rules (dtypes.hpp:111-158): NaN/inf ->
+// 0x7f, saturation to 0x7e above 448, flush to zero below 2^-9.
+__device__ __forceinline__ uint32_t rne_shift_u32(uint32_t v, int sh) {
+    uint32_t kept = v >> sh;
+    uint32_t dropped = v & ((1u << sh) - 1u);
+    uint32_t half = 1u << (sh - 1);
+    if (dropped > half || (dropped == half && (kept & 1u))) kept += 1u;
+    return kept;
+}
+__device__ __forceinline__ uint8_t f32_to_e4m3(float value) {
+    uint32_t x = __float_as_uint(value);
+    uint32_t s = (x >> 24) & 0x80u;
+    uint32_t e8 = (x >> 23) & 0xffu;
+    uint32_t m = x & 0x7fffffu;
+    if (e8 == 0xffu) return static_cast<uint8_t>(s | 0x7fu);
+    int e = static_cast<int>(e8) - 120;
+    if (e > 15 || (e == 15 && m > 0x600000u)) return static_cast<uint8_t>(s | 0x7eu);
+    if (e >= 1) {
+        uint32_t code = (static_cast<uint32_t>(e) << 3) | (m >> 20);
+        uint32_t low = m & 0xfffffu;
+        if (low > 0x80000u || (low == 0x80000u && (code & 1u))) {
+            code += 1u;
+            if (code >= 0x80u && (code >> 3) > 15u) return static_cast<uint8_t>(s | 0x7eu);
+        }
+        return static_cast<uint8_t>(s | (code & 0x7fu));
+    }
+    if (e < -2) return static_cast<uint8_t>(s);
+    return static_cast<uint8_t>(s | (rne_shift_u32(m | 0x800000u, 21 - e) & 0x7fu));
+}
+// E4M3 -> fp32 (dtypes.hpp:160-196).
+__device__ __forceinline__ float e4m3_to_f32(uint8_t b) {
+    uint32_t s = (b & 0x80u) ? 0x80000000u : 0u;
+    uint32_t e = (b >> 3) & 0xfu;
+    uint32_t m = b & 7u;
+    if (e == 0xfu && m == 7u) return __uint_as_float(s | 0x7fc00000u);
+    if (e == 0) return __uint_as_float(s | __float_as_uint(static_cast<float>(m) * 0x1p-9f));
+    return __uint_as_float(s | ((e + 120u) << 23) | (m << 20));
+}
+
+// Saturating round to a symmetric integer range (quant.cpp:12-19, 117-124):
+// clamp first, then round-to-nearest-even; NaN converts to 0 on both sides.
+__device__ __forceinline__ int sat_rint(float v, int lim) {
+    if (v >= static_cast<float>(lim)) return lim;
+    if (v <= static_cast<float>(-lim)) return -lim;
+    return static_cast<int>(__builtin_rintf(v));
+}
+
+// ---------------------------------------------------------------------------
+// Prepacked W4 layout (shared by prepack and GEMM kernels).
+//
+//   qweight  [Nt][Kt][64 lanes][16 B]       Nt = ceil(N/16), Kt = ceil(K/128)
+//     A 1 KiB tile covers 16 columns x 128 k.  Lane l owns column
+//     16*nt + (l & 15) and, in dword j (0..3), the eight k values
+//     128*kt + 32*j + 8*(l >> 4) + e (e = 0..7): exactly the B operand of one
+//     16x16x32 MFMA.  Element e sits in nibble slot (e & 1) ? 4 + e/2 : e/2,
+//     so elements (2p, 2p+1) are nibbles p and p+4 (bits 4p and 4p+16).
+//   scales   [Nt][NG][16]  fp32 (symmetric) or fp16 (asymmetric), NG = K/G
+//   zeros    [Nt][ceil(NG/8)][16] u32, group g in nibble g % 8 (asymmetric)
+// Codes are unsigned: symmetric int4 q in [-7,7] is stored as q + 8 with an
+// implied zero point of 8.
+// ---------------------------------------------------------------------------
+constexpr int kW4TileN = 16;
+constexpr int kW4TileK = 128;
+constexpr int kW4TileBytes = 1024;
+
+__host__ __device__ inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+__host__ __device__ inline int64_t ceil_div64(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// bf16 bits of (16 + u) for nibbles p and p+4 of `d`, packed low/high: the
+// nibble lands on mantissa bits 3..6 of a bf16 whose exponent encodes 16.
+__device__ __forceinline__ uint32_t w4_pair_16pu(uint32_t d, int p) {
+    uint32_t sh = (p == 0) ? (d << 3) : (d >> (4 * p - 3));
+    return (sh & 0x00780078u) | 0x41804180u;
+}
+
+}  // namespace lhq
+
+// ---------------------------------------------------------------------------
+// Host-side status plumbing (defined in capi.cpp).
+// ---------------------------------------------------------------------------
+namespace lhq {
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+}  // namespace lhq
+
+#define LHQ_REQUIRE(cond, ...)                                              \
+    do {                                                                    \
+        if (!(cond)) return ::lhq::set_error(LHQ_ERR_INVALID, __VA_ARGS__); \
+    } while (0)
+#define LHQ_SUPPORTED(cond, ...)                                                \
+    do {                                                                        \
+        if (!(cond)) return ::lhq::set_error(LHQ_ERR_UNSUPPORTED, __VA_ARGS__); \
+    } while (0)

@@ -1,0 +1,179 @@
+// prepack.hip -- one-time re-tiling of quantized weights into the layouts the
+// gfx950 GEMM kernels stream.
+//
+// The reference keeps int4 weights as [K/2, N] bytes (quant.hpp:52-59) and
+// int8 weights as [K, N] (gemm_quant.hpp:37), and reads them with a stride of
+// N bytes per k step (gemm_quant.cpp:42, quant.hpp:71).  On the GPU that
+// stride would make every wave touch K/2 separate rows for one column; these
+// kernels rewrite the weights once so each wave reads contiguous 1 KiB runs
+// that are already in MFMA operand order.
+#include "common.hpp"
+
+namespace lhq {
+namespace {
+
+// One thread per (tile, lane): assemble the 16 bytes lane `l` of tile
+// (nt, kt) will load -- the four 16x16x32 B operands of column 16*nt + (l&15).
+template <bool ASYM>
+__global__ void w4_prepack_qweight_kernel(const uint8_t* __restrict__ packed,
+                                          uint8_t* __restrict__ qweight, int K, int N,
+                                          int Kt, int64_t total_lanes) {
+    int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= total_lanes) return;
+    const int lane = static_cast<int>(t & 63);
+    const int64_t tile = t >> 6;
+    const int kt = static_cast<int>(tile % Kt);
+    const int nt = static_cast<int>(tile / Kt);
+    const int n = nt * kW4TileN + (lane & 15);
+    u32x4_t out;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        uint32_t d = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int k = kt * kW4TileK + 32 * j + 8 * (lane >> 4) + e;
+            uint32_t u = 0;
+            if (n < N && k < K) {
+                const uint8_t b = packed[static_cast<int64_t>(k >> 1) * N + n];
+                const uint32_t nib = (k & 1) ? (b >> 4) : (b & 0xfu);
+                // symmetric: two's-complement q in [-8,7] -> q + 8 (quant.hpp:73-74)
+                u = ASYM ? nib : ((nib ^ 8u) & 0xfu);
+            }
+            const int slot = (e & 1) ? 4 + (e >> 1) : (e >> 1);
+            d |= u << (4 * slot);
+        }
+        out[j] = d;
+    }
+    *reinterpret_cast<u32x4_t*>(qweight + t * 16) = out;
+}
+
+template <typename S>
+__global__ void w4_prepack_scales_kernel(const S* __restrict__ scales, S* __restrict__ out,
+                                         int N, int NG, int64_t total) {
+    int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= total) return;
+    const int c = static_cast<int>(t & 15);
+    const int64_t r = t >> 4;
+    const int g = static_cast<int>(r % NG);
+    const int nt = static_cast<int>(r / NG);
+    const int n = nt * kW4TileN + c;
+    out[t] = (n < N) ? scales[static_cast<int64_t>(g) * N + n] : S(0);
+}
+
+__global__ void w4_prepack_zeros_kernel(const uint8_t* __restrict__ zeros,
+                                        uint32_t* __restrict__ out, int N, int NG, int NG8,
+                                        int64_t total) {
+    int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (t >= total) return;
+    const int c = static_cast<int>(t & 15);
+    const int64_t r = t >> 4;
+    const int g8 = static_cast<int>(r % NG8);
+    const int nt = static_cast<int>(r / NG8);
+    const int n = nt * kW4TileN + c;
+    uint32_t v = 0;
+    if (n < N) {
+        for (int i = 0; i < 8; ++i) {
+            const int g = g8 * 8 + i;
+            if (g < NG) v |= (static_cast<uint32_t>(zeros[static_cast<int64_t>(g) * N + n]) & 0xfu) << (4 * i);
+        }
+    }
+    out[t] = v;
+}
+
+// Bt[n][k] = B[k][n] for n < N, k < K, zero elsewhere: a 64x64-byte tile is
+// transposed through LDS so both the reads and the writes are coalesced.
+__global__ __launch_bounds__(256) void b8_prepack_kernel(const uint8_t* __restrict__ B,
+                                                        uint8_t* __restrict__ Bt, int K, int N,
+                                                        int Kp) {
+    __shared__ uint8_t tile[64][65];
+    const int k0 = blockIdx.x * 64, n0 = blockIdx.y * 64;
+    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+        const int kk = i >> 6, nn = i & 63;
+        const int k = k0 + kk, n = n0 + nn;
+        tile[kk][nn] = (k < K && n < N) ? B[static_cast<int64_t>(k) * N + n] : 0;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+        const int nn = i >> 6, kk = i & 63;
+        Bt[static_cast<int64_t>(n0 + nn) * Kp + k0 + kk] = tile[kk][nn];
+    }
+}
+
+bool w4_dims_ok(int K, int N, int G) {
+    return K > 0 && N > 0 && G > 0 && (K % G) == 0 && (K % 2) == 0;
+}
+
+}  // namespace
+
+}  // namespace lhq
+
+using namespace lhq;
+
+extern "C" {
+
+int64_t lhq_w4_qweight_bytes(int K, int N) {
+    if (K <= 0 || N <= 0) return 0;
+    return static_cast<int64_t>(ceil_div(N, kW4TileN)) * ceil_div(K, kW4TileK) * kW4TileBytes;
+}
+
+int64_t lhq_w4_scales_bytes(int K, int N, int G, int fp16_scales) {
+    if (!w4_dims_ok(K, N, G)) return 0;
+    return static_cast<int64_t>(ceil_div(N, kW4TileN)) * (K / G) * kW4TileN * (fp16_scales ? 2 : 4);
+}
+
+int64_t lhq_w4_zeros_bytes(int K, int N, int G) {
+    if (!w4_dims_ok(K, N, G)) return 0;
+    return static_cast<int64_t>(ceil_div(N, kW4TileN)) * ceil_div(K / G, 8) * kW4TileN * 4;
+}
+
+int lhq_w4_prepack_sym(const uint8_t* packed, const float* scales, int K, int N, int G,
+                       uint8_t* qweight, float* scales_out, void* stream) {
+    LHQ_REQUIRE(packed && scales && qweight && scales_out, "w4_prepack_sym: null pointer");
+    LHQ_REQUIRE(w4_dims_ok(K, N, G), "w4_prepack_sym: need K,N,G > 0, K even, G | K (K=%d N=%d G=%d)", K, N, G);
+    const int Nt = ceil_div(N, kW4TileN), Kt = ceil_div(K, kW4TileK), NG = K / G;
+    const int64_t lanes = static_cast<int64_t>(Nt) * Kt * 64;
+    hipStream_t s = as_stream(stream);
+    w4_prepack_qweight_kernel<false><<<static_cast<unsigned>(ceil_div64(lanes, 256)), 256, 0, s>>>(
+        packed, qweight, K, N, Kt, lanes);
+    const int64_t ns = static_cast<int64_t>(Nt) * NG * 16;
+    w4_prepack_scales_kernel<float><<<static_cast<unsigned>(ceil_div64(ns, 256)), 256, 0, s>>>(
+        scales, scales_out, N, NG, ns);
+    return check_launch("w4_prepack_sym");
+}
+
+int lhq_w4_prepack_asym(const uint8_t* packed, const uint16_t* scales_f16, const uint8_t* zeros,
+                        int K, int N, int G, uint8_t* qweight, uint16_t* scales_out,
+                        uint32_t* zeros_out, void* stream) {
+    LHQ_REQUIRE(packed && scales_f16 && zeros && qweight && scales_out && zeros_out,
+                "w4_prepack_asym: null pointer");
+    LHQ_REQUIRE(w4_dims_ok(K, N, G), "w4_prepack_asym: need K,N,G > 0, K even, G | K (K=%d N=%d G=%d)", K, N, G);
+    const int Nt = ceil_div(N, kW4TileN), Kt = ceil_div(K, kW4TileK), NG = K / G;
+    const int NG8 = ceil_div(NG, 8);
+    const int64_t lanes = static_cast<int64_t>(Nt) * Kt * 64;
+    hipStream_t s = as_stream(stream);
+    w4_prepack_qweight_kernel<true><<<static_cast<unsigned>(ceil_div64(lanes, 256)), 256, 0, s>>>(
+        packed, qweight, K, N, Kt, lanes);
+    const int64_t ns = static_cast<int64_t>(Nt) * NG * 16;
+    w4_prepack_scales_kernel<uint16_t><<<static_cast<unsigned>(ceil_div64(ns, 256)), 256, 0, s>>>(
+        scales_f16, scales_out, N, NG, ns);
+    const int64_t nz = static_cast<int64_t>(Nt) * NG8 * 16;
+    w4_prepack_zeros_kernel<<<static_cast<unsigned>(ceil_div64(nz, 256)), 256, 0, s>>>(
+        zeros, zeros_out, N, NG, NG8, nz);
+    return check_launch("w4_prepack_asym");
+}
+
+int64_t lhq_b8_prepacked_bytes(int K, int N) {
+    if (K <= 0 || N <= 0) return 0;
+    return static_cast<int64_t>(ceil_div(N, 256)) * 256 * (static_cast<int64_t>(ceil_div(K, 128)) * 128);
+}
+
+int lhq_b8_prepack(const uint8_t* B, int K, int N, uint8_t* Bt, void* stream) {
+    LHQ_REQUIRE(B && Bt, "b8_prepack: null pointer");
+    LHQ_REQUIRE(K > 0 && N > 0, "b8_prepack: need K, N > 0 (K=%d N=%d)", K, N);
+    const int Kp = ceil_div(K, 128) * 128, Np = ceil_div(N, 256) * 256;
+    dim3 grid(Kp / 64, Np / 64);
+    b8_prepack_kernel<<<grid, 256, 0, as_stream(stream)>>>(B, Bt, K, N, Kp);
+    return check_launch("b8_prepack");
+}
+
+}  // extern "C"

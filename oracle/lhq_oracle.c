@@ -1,0 +1,680 @@
+/*
+ * lhq_oracle.c -- CPU restatement of LonghornAI's quantized-GEMM path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the parity checker for the HIP
+ * backend: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg may load it.  The product path (liblonghorn_hip.so and the lh::
+ * drop-in library) never links or calls it.
+ *
+ * Every function restates the semantics of one reference function, in the
+ * reference's loop order and rounding, in plain C99.  Citations are
+ * file:line into the reference tree (src/kernels/...).  Build with
+ * -ffp-contract=off so no multiply-add is fused: the reference is built for
+ * baseline x86-64 (no FMA), so each product and sum is rounded separately.
+ *
+ * Functions marked "BASELINE extension" have no reference counterpart: they
+ * define the asymmetric int4 / bf16 variants the benchmark configs ask for,
+ * and are pinned by closed forms and by reduction to the reference functions
+ * (see the tests), not by the reference itself.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define EXPORT __attribute__((visibility("default")))
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* ---------------------------------------------------------------------- */
+/* Scalar conversions: dtypes.hpp:17-269                                    */
+/* ---------------------------------------------------------------------- */
+
+/* Round-to-nearest-even of `v >> sh` using the dropped bits (sh >= 1). */
+static inline uint32_t rne_shift(uint32_t v, int sh) {
+    uint32_t kept = v >> sh;
+    uint32_t dropped = v & ((1u << sh) - 1u);
+    uint32_t half = 1u << (sh - 1);
+    if (dropped > half || (dropped == half && (kept & 1u))) kept += 1u;
+    return kept;
+}
+
+/* fp32 -> binary16, RNE, NaN quieted to 0x7e00 (dtypes.hpp:17-55). */
+EXPORT uint16_t lho_f32_to_f16(float value) {
+    uint32_t x = f2u(value);
+    uint32_t s = (x >> 16) & 0x8000u;
+    uint32_t e8 = (x >> 23) & 0xffu;
+    uint32_t m = x & 0x7fffffu;
+    if (e8 == 0xffu) return (uint16_t)(s | (m ? 0x7e00u : 0x7c00u));
+    int e = (int)e8 - 112;                 /* rebias 127 -> 15 */
+    if (e >= 31) return (uint16_t)(s | 0x7c00u);
+    if (e <= 0) {                          /* subnormal half or zero */
+        if (e < -10) return (uint16_t)s;
+        return (uint16_t)(s | rne_shift(m | 0x800000u, 14 - e));
+    }
+    /* Normal: the carry out of the mantissa walks into the exponent. */
+    uint32_t body = ((uint32_t)e << 10) | (m >> 13);
+    uint32_t low = m & 0x1fffu;
+    if (low > 0x1000u || (low == 0x1000u && (body & 1u))) body += 1u;
+    return (uint16_t)(s | body);
+}
+
+/* binary16 -> fp32, exact (dtypes.hpp:57-85). */
+EXPORT float lho_f16_to_f32(uint16_t h) {
+    uint32_t s = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1fu;
+    uint32_t m = h & 0x3ffu;
+    if (e == 0x1fu) return u2f(s | 0x7f800000u | (m << 13));
+    if (e == 0) {
+        if (m == 0) return u2f(s);
+        /* subnormal: value = m * 2^-24, exact in fp32 */
+        float v = (float)m * 0x1p-24f;
+        return u2f(s | f2u(v));
+    }
+    return u2f(s | ((e + 112u) << 23) | (m << 13));
+}
+
+/* fp32 -> bfloat16, RNE on the low 16 bits, NaN keeps payload + quiet bit
+ * (dtypes.hpp:87-98). */
+EXPORT uint16_t lho_f32_to_bf16(float value) {
+    uint32_t x = f2u(value);
+    if ((x & 0x7f800000u) == 0x7f800000u && (x & 0x7fffffu))
+        return (uint16_t)((x >> 16) | 0x40u);
+    x += 0x7fffu + ((x >> 16) & 1u);
+    return (uint16_t)(x >> 16);
+}
+
+EXPORT float lho_bf16_to_f32(uint16_t b) { return u2f((uint32_t)b << 16); }
+
+/* fp32 -> FP8 E4M3 (dtypes.hpp:111-158).  Quirks kept on purpose:
+ *  - NaN and +-inf map to the NaN code 0x7f|sign;
+ *  - any |x| > 448 saturates to 0x7e|sign;
+ *  - |x| < 2^-9 flushes to signed zero (new_exp < -2), even where RNE
+ *    would round up to the smallest subnormal. */
+EXPORT uint8_t lho_f32_to_e4m3(float value) {
+    uint32_t x = f2u(value);
+    uint32_t s = (x >> 24) & 0x80u;
+    uint32_t e8 = (x >> 23) & 0xffu;
+    uint32_t m = x & 0x7fffffu;
+    if (e8 == 0xffu) return (uint8_t)(s | 0x7fu);
+    int e = (int)e8 - 120;                 /* rebias 127 -> 7 */
+    if (e > 15 || (e == 15 && m > 0x600000u)) return (uint8_t)(s | 0x7eu);
+    if (e >= 1) {
+        uint32_t code = ((uint32_t)e << 3) | (m >> 20);
+        uint32_t low = m & 0xfffffu;
+        if (low > 0x80000u || (low == 0x80000u && (code & 1u))) {
+            code += 1u;
+            if (code >= 0x80u && (code >> 3) > 15u) return (uint8_t)(s | 0x7eu);
+        }
+        return (uint8_t)(s | (code & 0x7fu));
+    }
+    if (e < -2) return (uint8_t)s;
+    return (uint8_t)(s | (rne_shift(m | 0x800000u, 21 - e) & 0x7fu));
+}
+
+/* FP8 E4M3 -> fp32 (dtypes.hpp:160-196): 0x7f/0xff is NaN, no infinities. */
+EXPORT float lho_e4m3_to_f32(uint8_t b) {
+    uint32_t s = (b & 0x80u) ? 0x80000000u : 0u;
+    uint32_t e = (b >> 3) & 0xfu;
+    uint32_t m = b & 7u;
+    if (e == 0xfu && m == 7u) return u2f(s | 0x7fc00000u);
+    if (e == 0) {
+        if (m == 0) return u2f(s);
+        float v = (float)m * 0x1p-9f;      /* subnormal: m/8 * 2^-6 */
+        return u2f(s | f2u(v));
+    }
+    return u2f(s | ((e + 120u) << 23) | (m << 20));
+}
+
+/* fp32 -> FP8 E5M2 (dtypes.hpp:201-237): overflow -> inf, |x| < 2^-17 -> 0. */
+EXPORT uint8_t lho_f32_to_e5m2(float value) {
+    uint32_t x = f2u(value);
+    uint32_t s = (x >> 24) & 0x80u;
+    uint32_t e8 = (x >> 23) & 0xffu;
+    uint32_t m = x & 0x7fffffu;
+    if (e8 == 0xffu) return (uint8_t)(s | (m ? 0x7fu : 0x7cu));
+    int e = (int)e8 - 112;                 /* rebias 127 -> 15 */
+    if (e >= 31) return (uint8_t)(s | 0x7cu);
+    if (e >= 1) {
+        uint32_t code = ((uint32_t)e << 2) | (m >> 21);
+        uint32_t low = m & 0x1fffffu;
+        if (low > 0x100000u || (low == 0x100000u && (code & 1u))) code += 1u;
+        if (code >= 0x7cu) return (uint8_t)(s | 0x7cu);
+        return (uint8_t)(s | (code & 0x7fu));
+    }
+    if (e < -1) return (uint8_t)s;
+    return (uint8_t)(s | (rne_shift(m | 0x800000u, 22 - e) & 0x7fu));
+}
+
+/* FP8 E5M2 -> fp32 (dtypes.hpp:239-269). */
+EXPORT float lho_e5m2_to_f32(uint8_t b) {
+    uint32_t s = (b & 0x80u) ? 0x80000000u : 0u;
+    uint32_t e = (b >> 2) & 0x1fu;
+    uint32_t m = b & 3u;
+    if (e == 0x1fu) return u2f(s | 0x7f800000u | (m << 21));
+    if (e == 0) {
+        if (m == 0) return u2f(s);
+        float v = (float)m * 0x1p-16f;     /* m/4 * 2^-14 */
+        return u2f(s | f2u(v));
+    }
+    return u2f(s | ((e + 112u) << 23) | (m << 21));
+}
+
+/* Array forms of the conversions, for the Python tests. */
+EXPORT void lho_f32_to_f16_n(const float* x, uint16_t* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = lho_f32_to_f16(x[i]);
+}
+EXPORT void lho_f16_to_f32_n(const uint16_t* x, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = lho_f16_to_f32(x[i]);
+}
+EXPORT void lho_f32_to_bf16_n(const float* x, uint16_t* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = lho_f32_to_bf16(x[i]);
+}
+EXPORT void lho_f32_to_e4m3_n(const float* x, uint8_t* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = lho_f32_to_e4m3(x[i]);
+}
+EXPORT void lho_e4m3_to_f32_n(const uint8_t* x, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = lho_e4m3_to_f32(x[i]);
+}
+EXPORT void lho_f32_to_e5m2_n(const float* x, uint8_t* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = lho_f32_to_e5m2(x[i]);
+}
+EXPORT void lho_e5m2_to_f32_n(const uint8_t* x, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = lho_e5m2_to_f32(x[i]);
+}
+
+/* ---------------------------------------------------------------------- */
+/* Quantizers: quant.cpp                                                    */
+/* ---------------------------------------------------------------------- */
+
+/* Saturate, then round with the current (nearest-even) mode
+ * (quant.cpp:12-19).  The clamp is applied before lrintf so huge inputs
+ * never overflow the conversion. */
+static inline int8_t sat_rint(float v, int lim) {
+    if (v >= (float)lim) return (int8_t)lim;
+    if (v <= (float)-lim) return (int8_t)-lim;
+    long r = lrintf(v);
+    int ri = (int)r;
+    if (ri > lim) ri = lim;
+    if (ri < -lim) ri = -lim;
+    return (int8_t)ri;
+}
+
+/* max |x| over n values, starting from 0; NaN never wins (quant.cpp:21-28). */
+static inline float max_abs_n(const float* x, int64_t n, int64_t stride) {
+    float m = 0.0f;
+    for (int64_t i = 0; i < n; ++i) {
+        float a = fabsf(x[i * stride]);
+        if (a > m) m = a;
+    }
+    return m;
+}
+
+/* quant.cpp:34-45: one scale, quantize by multiplying with 1/scale. */
+EXPORT void lho_q8_quantize_per_tensor(const float* src, int8_t* dst,
+                                       float* scale_out, int64_t n) {
+    float m = max_abs_n(src, n, 1);
+    float scale = (m > 0.0f) ? m / 127.0f : 1.0f;
+    float inv = 1.0f / scale;
+    for (int64_t i = 0; i < n; ++i) dst[i] = sat_rint(src[i] * inv, 127);
+    *scale_out = scale;
+}
+
+/* quant.cpp:47-50 */
+EXPORT void lho_q8_dequantize_per_tensor(const int8_t* src, float scale,
+                                         float* dst, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) dst[i] = (float)src[i] * scale;
+}
+
+/* quant.cpp:52-63: per-row scale, reciprocal multiply. */
+EXPORT void lho_q8_quantize_per_row(const float* src, int8_t* dst,
+                                    float* scales_out, int rows, int dim) {
+    for (int r = 0; r < rows; ++r) {
+        const float* x = src + (int64_t)r * dim;
+        int8_t* q = dst + (int64_t)r * dim;
+        float m = max_abs_n(x, dim, 1);
+        float scale = (m > 0.0f) ? m / 127.0f : 1.0f;
+        float inv = 1.0f / scale;
+        for (int i = 0; i < dim; ++i) q[i] = sat_rint(x[i] * inv, 127);
+        scales_out[r] = scale;
+    }
+}
+
+/* quant.cpp:65-73 */
+EXPORT void lho_q8_dequantize_per_row(const int8_t* src, const float* scales,
+                                      float* dst, int rows, int dim) {
+    for (int r = 0; r < rows; ++r)
+        for (int i = 0; i < dim; ++i)
+            dst[(int64_t)r * dim + i] = (float)src[(int64_t)r * dim + i] * scales[r];
+}
+
+/* quant.cpp:75-96: per-column scale, quantize by DIVIDING by the scale. */
+EXPORT void lho_q8_quantize_per_col(const float* src, int8_t* dst,
+                                    float* scales_out, int rows, int cols) {
+    for (int c = 0; c < cols; ++c) {
+        float m = max_abs_n(src + c, rows, cols);
+        scales_out[c] = (m > 0.0f) ? m / 127.0f : 1.0f;
+    }
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < cols; ++c)
+            dst[(int64_t)r * cols + c] =
+                sat_rint(src[(int64_t)r * cols + c] / scales_out[c], 127);
+}
+
+/* quant.cpp:98-105 */
+EXPORT void lho_q8_dequantize_per_col(const int8_t* src, const float* scales,
+                                      float* dst, int rows, int cols) {
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < cols; ++c)
+            dst[(int64_t)r * cols + c] = (float)src[(int64_t)r * cols + c] * scales[c];
+}
+
+/* quant.hpp:68-75: nibble k&1 of byte (k/2)*N + n, sign-extended from bit 3. */
+EXPORT int8_t lho_q4_get(const uint8_t* packed, int k, int n, int N) {
+    uint8_t b = packed[(int64_t)(k / 2) * N + n];
+    int v = (k & 1) ? (b >> 4) : (b & 0xf);
+    return (int8_t)(v >= 8 ? v - 16 : v);
+}
+
+/* quant.cpp:128-160: symmetric int4 in [-7,7], fp32 scale max|w|/7 per
+ * (K-group, column), division by the scale, two K-adjacent rows per byte. */
+EXPORT void lho_q4_quantize_groupwise(const float* src, uint8_t* packed,
+                                      float* scales_out, int K, int N, int G) {
+    int groups = K / G;
+    for (int g = 0; g < groups; ++g)
+        for (int n = 0; n < N; ++n) {
+            float m = max_abs_n(src + (int64_t)g * G * N + n, G, N);
+            scales_out[(int64_t)g * N + n] = (m > 0.0f) ? m / 7.0f : 1.0f;
+        }
+    for (int k = 0; k < K; k += 2)
+        for (int n = 0; n < N; ++n) {
+            float s0 = scales_out[(int64_t)(k / G) * N + n];
+            float s1 = scales_out[(int64_t)((k + 1) / G) * N + n];
+            int8_t q0 = sat_rint(src[(int64_t)k * N + n] / s0, 7);
+            int8_t q1 = sat_rint(src[(int64_t)(k + 1) * N + n] / s1, 7);
+            packed[(int64_t)(k / 2) * N + n] =
+                (uint8_t)((q0 & 0xf) | ((q1 & 0xf) << 4));
+        }
+}
+
+/* quant.cpp:162-172 */
+EXPORT void lho_q4_dequantize_groupwise(const uint8_t* packed,
+                                        const float* scales, float* dst,
+                                        int K, int N, int G) {
+    for (int k = 0; k < K; ++k)
+        for (int n = 0; n < N; ++n)
+            dst[(int64_t)k * N + n] =
+                (float)lho_q4_get(packed, k, n, N) * scales[(int64_t)(k / G) * N + n];
+}
+
+/* quant.cpp:176-188: FP8 per-tensor, scale max/448, reciprocal multiply. */
+EXPORT void lho_fp8_quantize_per_tensor(const float* src, uint8_t* dst,
+                                        float* scale_out, int64_t n) {
+    float m = max_abs_n(src, n, 1);
+    float scale = (m > 0.0f) ? m / 448.0f : 1.0f;
+    float inv = 1.0f / scale;
+    for (int64_t i = 0; i < n; ++i) dst[i] = lho_f32_to_e4m3(src[i] * inv);
+    *scale_out = scale;
+}
+
+/* quant.cpp:190-193 */
+EXPORT void lho_fp8_dequantize_per_tensor(const uint8_t* src, float scale,
+                                          float* dst, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) dst[i] = lho_e4m3_to_f32(src[i]) * scale;
+}
+
+/* quant.cpp:195-206 */
+EXPORT void lho_fp8_quantize_per_row(const float* src, uint8_t* dst,
+                                     float* scales_out, int rows, int dim) {
+    for (int r = 0; r < rows; ++r) {
+        const float* x = src + (int64_t)r * dim;
+        float m = max_abs_n(x, dim, 1);
+        float scale = (m > 0.0f) ? m / 448.0f : 1.0f;
+        float inv = 1.0f / scale;
+        for (int i = 0; i < dim; ++i)
+            dst[(int64_t)r * dim + i] = lho_f32_to_e4m3(x[i] * inv);
+        scales_out[r] = scale;
+    }
+}
+
+/* quant.cpp:208-216 */
+EXPORT void lho_fp8_dequantize_per_row(const uint8_t* src, const float* scales,
+                                       float* dst, int rows, int dim) {
+    for (int r = 0; r < rows; ++r)
+        for (int i = 0; i < dim; ++i)
+            dst[(int64_t)r * dim + i] =
+                lho_e4m3_to_f32(src[(int64_t)r * dim + i]) * scales[r];
+}
+
+/* quant.cpp:218-238: per-column, division by the scale. */
+EXPORT void lho_fp8_quantize_per_col(const float* src, uint8_t* dst,
+                                     float* scales_out, int rows, int cols) {
+    for (int c = 0; c < cols; ++c) {
+        float m = max_abs_n(src + c, rows, cols);
+        scales_out[c] = (m > 0.0f) ? m / 448.0f : 1.0f;
+    }
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < cols; ++c)
+            dst[(int64_t)r * cols + c] =
+                lho_f32_to_e4m3(src[(int64_t)r * cols + c] / scales_out[c]);
+}
+
+/* quant.cpp:240-249 */
+EXPORT void lho_fp8_dequantize_per_col(const uint8_t* src, const float* scales,
+                                       float* dst, int rows, int cols) {
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < cols; ++c)
+            dst[(int64_t)r * cols + c] =
+                lho_e4m3_to_f32(src[(int64_t)r * cols + c]) * scales[c];
+}
+
+/* ---------------------------------------------------------------------- */
+/* GEMMs: gemm_quant.cpp, gemm.cpp                                          */
+/* ---------------------------------------------------------------------- */
+
+/* gemm_quant.cpp:12-21: beta == 0 writes zeros without reading C; beta == 1
+ * leaves C untouched; otherwise C *= beta. */
+static void apply_beta(float* C, int M, int N, float beta) {
+    if (beta == 1.0f) return;
+    for (int64_t i = 0; i < (int64_t)M * N; ++i)
+        C[i] = (beta == 0.0f) ? 0.0f : C[i] * beta;
+}
+
+/* gemm_quant.cpp:29-49: int32 accumulate, then
+ * C += ((alpha * a_s) * b_s) * float(acc), each product rounded. */
+EXPORT void lho_gemm_w8a8(const int8_t* Aq, const int8_t* Bq,
+                          const float* A_s, const float* B_s, float* C,
+                          int M, int N, int K, float alpha, float beta) {
+    apply_beta(C, M, N, beta);
+    for (int i = 0; i < M; ++i) {
+        const int8_t* a = Aq + (int64_t)i * K;
+        for (int j = 0; j < N; ++j) {
+            int32_t acc = 0;
+            for (int k = 0; k < K; ++k)
+                acc += (int32_t)a[k] * (int32_t)Bq[(int64_t)k * N + j];
+            float f = alpha * A_s[i];
+            f = f * B_s[j];
+            f = f * (float)acc;
+            C[(int64_t)i * N + j] += f;
+        }
+    }
+}
+
+/* The int32 accumulator of gemm_quant.cpp:38-43, exposed (the reference
+ * keeps it internal; the build's debug entry point writes it out). */
+EXPORT void lho_gemm_w8a8_i32acc(const int8_t* Aq, const int8_t* Bq,
+                                 int32_t* acc_out, int M, int N, int K) {
+    for (int i = 0; i < M; ++i)
+        for (int j = 0; j < N; ++j) {
+            int32_t acc = 0;
+            for (int k = 0; k < K; ++k)
+                acc += (int32_t)Aq[(int64_t)i * K + k] * (int32_t)Bq[(int64_t)k * N + j];
+            acc_out[(int64_t)i * N + j] = acc;
+        }
+}
+
+/* BASELINE extension (config 3): the gemm_w8a8 epilogue with alpha = 1,
+ * beta = 0, rounded to bfloat16: out = bf16(((1*a_s)*b_s)*float(acc)). */
+EXPORT void lho_gemm_w8a8_bf16out(const int8_t* Aq, const int8_t* Bq,
+                                  const float* A_s, const float* B_s,
+                                  uint16_t* C, int M, int N, int K) {
+    for (int i = 0; i < M; ++i)
+        for (int j = 0; j < N; ++j) {
+            int32_t acc = 0;
+            for (int k = 0; k < K; ++k)
+                acc += (int32_t)Aq[(int64_t)i * K + k] * (int32_t)Bq[(int64_t)k * N + j];
+            float f = 1.0f * A_s[i];
+            f = f * B_s[j];
+            f = f * (float)acc;
+            C[(int64_t)i * N + j] = lho_f32_to_bf16(0.0f + f);
+        }
+}
+
+/* gemm_quant.cpp:54-82: per K-group, dequantize the [G, N] panel
+ * (float(q) * s), then C[i,:] += (alpha * A[i,k]) * panel[k,:] in k order. */
+EXPORT void lho_gemm_w4a16_groupwise(const float* A, const uint8_t* Bp,
+                                     const float* Bs, float* C,
+                                     int M, int N, int K, int G,
+                                     float alpha, float beta) {
+    apply_beta(C, M, N, beta);
+    float* panel = (float*)malloc(sizeof(float) * (size_t)G * (size_t)N);
+    for (int k0 = 0; k0 < K; k0 += G) {
+        int g = k0 / G;
+        for (int kk = 0; kk < G; ++kk)
+            for (int n = 0; n < N; ++n)
+                panel[(int64_t)kk * N + n] =
+                    (float)lho_q4_get(Bp, k0 + kk, n, N) * Bs[(int64_t)g * N + n];
+        for (int i = 0; i < M; ++i) {
+            float* c = C + (int64_t)i * N;
+            for (int kk = 0; kk < G; ++kk) {
+                float a = alpha * A[(int64_t)i * K + k0 + kk];
+                const float* b = panel + (int64_t)kk * N;
+                for (int n = 0; n < N; ++n) c[n] += a * b[n];
+            }
+        }
+    }
+    free(panel);
+}
+
+/* gemm_quant.cpp:87-104: fp32 accumulate of decoded e4m3 products, then
+ * C += ((alpha * sA) * sB) * acc. */
+EXPORT void lho_gemm_fp8_e4m3(const uint8_t* A, const uint8_t* B,
+                              float A_scale, float B_scale, float* C,
+                              int M, int N, int K, float alpha, float beta) {
+    apply_beta(C, M, N, beta);
+    float combined = alpha * A_scale;
+    combined = combined * B_scale;
+    for (int i = 0; i < M; ++i)
+        for (int j = 0; j < N; ++j) {
+            float acc = 0.0f;
+            for (int k = 0; k < K; ++k) {
+                float p = lho_e4m3_to_f32(A[(int64_t)i * K + k]) *
+                          lho_e4m3_to_f32(B[(int64_t)k * N + j]);
+                acc = acc + p;
+            }
+            C[(int64_t)i * N + j] += combined * acc;
+        }
+}
+
+/* gemm.cpp:5-16: naive fp32, C = alpha*acc + beta*C (always reads C). */
+EXPORT void lho_gemm_ref(const float* A, const float* B, float* C,
+                         int M, int N, int K, float alpha, float beta) {
+    for (int i = 0; i < M; ++i)
+        for (int j = 0; j < N; ++j) {
+            float acc = 0.0f;
+            for (int k = 0; k < K; ++k) acc += A[(int64_t)i * K + k] * B[(int64_t)k * N + j];
+            float t = alpha * acc;
+            C[(int64_t)i * N + j] = t + beta * C[(int64_t)i * N + j];
+        }
+}
+
+/* gemm.cpp:21-57: beta first, then C[i,j] += (alpha*A[i,k]) * B[k,j] with k
+ * ascending for every element (the 64^3 blocking does not change the
+ * per-element order, so an i-k-j loop is bit-identical). */
+EXPORT void lho_gemm(const float* A, const float* B, float* C,
+                     int M, int N, int K, float alpha, float beta) {
+    apply_beta(C, M, N, beta);
+    for (int i = 0; i < M; ++i) {
+        float* c = C + (int64_t)i * N;
+        for (int k = 0; k < K; ++k) {
+            float a = alpha * A[(int64_t)i * K + k];
+            const float* b = B + (int64_t)k * N;
+            for (int j = 0; j < N; ++j) c[j] += a * b[j];
+        }
+    }
+}
+
+/* gemm.cpp:59-67 */
+EXPORT void lho_gemm_batched(const float* A, const float* B, float* C,
+                             int batch, int M, int N, int K,
+                             float alpha, float beta) {
+    for (int b = 0; b < batch; ++b)
+        lho_gemm(A + (int64_t)b * M * K, B + (int64_t)b * K * N,
+                 C + (int64_t)b * M * N, M, N, K, alpha, beta);
+}
+
+/* gemm.cpp:69-75 */
+EXPORT void lho_gemm_grouped(const float* const* A, const float* const* B,
+                             float* const* C, const int* M, const int* N,
+                             const int* K, int groups, float alpha, float beta) {
+    for (int g = 0; g < groups; ++g)
+        lho_gemm(A[g], B[g], C[g], M[g], N[g], K[g], alpha, beta);
+}
+
+/* ---------------------------------------------------------------------- */
+/* BASELINE extensions: asymmetric int4 (u4 code, fp16 scale, u4 zero),     */
+/* bf16 activations / outputs, per-token quant of bf16 rows, MoE grouping.  */
+/* ---------------------------------------------------------------------- */
+
+/* Per-token int8 quantization of bf16 rows: quant.cpp:52-63 applied to the
+ * exact fp32 widening of each bf16 value. */
+EXPORT void lho_q8_quantize_per_row_bf16(const uint16_t* src, int8_t* dst,
+                                         float* scales_out, int rows, int dim) {
+    for (int r = 0; r < rows; ++r) {
+        const uint16_t* x = src + (int64_t)r * dim;
+        float m = 0.0f;
+        for (int i = 0; i < dim; ++i) {
+            float a = fabsf(lho_bf16_to_f32(x[i]));
+            if (a > m) m = a;
+        }
+        float scale = (m > 0.0f) ? m / 127.0f : 1.0f;
+        float inv = 1.0f / scale;
+        for (int i = 0; i < dim; ++i)
+            dst[(int64_t)r * dim + i] = sat_rint(lho_bf16_to_f32(x[i]) * inv, 127);
+        scales_out[r] = scale;
+    }
+}
+
+/* Asymmetric int4 quantizer (the build's own definition, no reference):
+ * per (K-group g, column n), with the range widened to contain 0:
+ *   lo = min(0, min w), hi = max(0, max w)
+ *   s  = fp16((hi - lo) / 15); s = 1 if hi == lo; s >= 2^-14 (fp16 normal)
+ *   z  = clamp(rint(-lo / s), 0, 15)
+ *   u  = clamp(rint(w / s) + z, 0, 15)       (s is the fp16-rounded value)
+ * Codes are packed like quant.hpp:52-59 (row 2i low nibble, 2i+1 high) but
+ * unsigned; zeros are one byte per (g, n); dequant is (u - z) * s. */
+EXPORT void lho_q4a_quantize_groupwise(const float* src, uint8_t* packed,
+                                       uint16_t* scales_f16, uint8_t* zeros,
+                                       int K, int N, int G) {
+    int groups = K / G;
+    for (int g = 0; g < groups; ++g)
+        for (int n = 0; n < N; ++n) {
+            float lo = 0.0f, hi = 0.0f;
+            for (int kk = 0; kk < G; ++kk) {
+                float w = src[(int64_t)(g * G + kk) * N + n];
+                if (w < lo) lo = w;
+                if (w > hi) hi = w;
+            }
+            float s = (hi - lo) / 15.0f;
+            if (!(s > 0.0f)) s = 1.0f;
+            uint16_t sh = lho_f32_to_f16(s);
+            float sq = lho_f16_to_f32(sh);
+            if (sq < 0x1p-14f) { sh = lho_f32_to_f16(0x1p-14f); sq = 0x1p-14f; }
+            float zf = rintf(-lo / sq);
+            if (zf < 0.0f) zf = 0.0f;
+            if (zf > 15.0f) zf = 15.0f;
+            scales_f16[(int64_t)g * N + n] = sh;
+            zeros[(int64_t)g * N + n] = (uint8_t)zf;
+        }
+    for (int k = 0; k < K; ++k)
+        for (int n = 0; n < N; ++n) {
+            int64_t gi = (int64_t)(k / G) * N + n;
+            float sq = lho_f16_to_f32(scales_f16[gi]);
+            float t = rintf(src[(int64_t)k * N + n] / sq) + (float)zeros[gi];
+            if (t < 0.0f) t = 0.0f;
+            if (t > 15.0f) t = 15.0f;
+            uint8_t u = (uint8_t)t;
+            uint8_t* b = &packed[(int64_t)(k / 2) * N + n];
+            if (k & 1) *b = (uint8_t)((*b & 0x0f) | (u << 4));
+            else       *b = (uint8_t)((*b & 0xf0) | u);
+        }
+}
+
+static inline int q4a_code(const uint8_t* packed, int k, int n, int N) {
+    uint8_t b = packed[(int64_t)(k / 2) * N + n];
+    return (k & 1) ? (b >> 4) : (b & 0xf);
+}
+
+/* w[k,n] = float(u - z) * s  (one rounding, like quant.cpp:162-172). */
+EXPORT void lho_q4a_dequantize_groupwise(const uint8_t* packed,
+                                         const uint16_t* scales_f16,
+                                         const uint8_t* zeros, float* dst,
+                                         int K, int N, int G) {
+    for (int k = 0; k < K; ++k)
+        for (int n = 0; n < N; ++n) {
+            int64_t gi = (int64_t)(k / G) * N + n;
+            dst[(int64_t)k * N + n] =
+                (float)(q4a_code(packed, k, n, N) - (int)zeros[gi]) *
+                lho_f16_to_f32(scales_f16[gi]);
+        }
+}
+
+/* W4A16 with asymmetric weights and bf16 activations, fp32 result, in the
+ * loop order of gemm_quant.cpp:54-82 (panel dequant, then k-ordered axpy).
+ * A is bf16 [M,K] (widened exactly); C is fp32 [M,N]; alpha = 1, beta = 0. */
+EXPORT void lho_gemm_w4a16_asym(const uint16_t* A, const uint8_t* Bp,
+                                const uint16_t* Bs, const uint8_t* Bz,
+                                float* C, int M, int N, int K, int G) {
+    for (int64_t i = 0; i < (int64_t)M * N; ++i) C[i] = 0.0f;
+    float* panel = (float*)malloc(sizeof(float) * (size_t)G * (size_t)N);
+    for (int k0 = 0; k0 < K; k0 += G) {
+        int g = k0 / G;
+        for (int kk = 0; kk < G; ++kk)
+            for (int n = 0; n < N; ++n) {
+                int64_t gi = (int64_t)g * N + n;
+                panel[(int64_t)kk * N + n] =
+                    (float)(q4a_code(Bp, k0 + kk, n, N) - (int)Bz[gi]) *
+                    lho_f16_to_f32(Bs[gi]);
+            }
+        for (int i = 0; i < M; ++i) {
+            float* c = C + (int64_t)i * N;
+            for (int kk = 0; kk < G; ++kk) {
+                float a = lho_bf16_to_f32(A[(int64_t)i * K + k0 + kk]);
+                const float* b = panel + (int64_t)kk * N;
+                for (int n = 0; n < N; ++n) c[n] += a * b[n];
+            }
+        }
+    }
+    free(panel);
+}
+
+/* Ragged grouped W4A16: group e owns rows
+ * [offsets[e], offsets[e+1]) of A and C (the expert_offsets contract of
+ * moe.cpp:111-123) and weight set e of the stacked arrays
+ * Bp[E][K/2][N], Bs[E][K/G][N], Bz[E][K/G][N].  Each group is the
+ * gemm_w4a16_asym above -- the gemm_grouped loop of gemm.cpp:69-75. */
+EXPORT void lho_gemm_w4a16_asym_grouped(const uint16_t* A, const int32_t* offsets,
+                                        const uint8_t* Bp, const uint16_t* Bs,
+                                        const uint8_t* Bz, float* C,
+                                        int E, int N, int K, int G) {
+    int64_t wq = (int64_t)K / 2 * N, wg = (int64_t)(K / G) * N;
+    for (int e = 0; e < E; ++e) {
+        int r0 = offsets[e], r1 = offsets[e + 1];
+        if (r1 <= r0) continue;
+        lho_gemm_w4a16_asym(A + (int64_t)r0 * K, Bp + e * wq, Bs + e * wg,
+                            Bz + e * wg, C + (int64_t)r0 * N, r1 - r0, N, K, G);
+    }
+}
+
+/* moe.cpp:102-140 steps 1-3 without the activation copy: counts per expert,
+ * exclusive prefix sum into offsets[E+1], then a stable placement that keeps
+ * token order inside each expert.  token_idx/slot_idx have T*topk entries. */
+EXPORT void lho_moe_dispatch_table(const int32_t* expert_ids, int T, int topk,
+                                   int E, int32_t* offsets, int32_t* token_idx,
+                                   int32_t* slot_idx) {
+    int32_t* cursor = (int32_t*)calloc((size_t)E, sizeof(int32_t));
+    for (int t = 0; t < T; ++t)
+        for (int k = 0; k < topk; ++k) cursor[expert_ids[t * topk + k]]++;
+    offsets[0] = 0;
+    for (int e = 0; e < E; ++e) offsets[e + 1] = offsets[e] + cursor[e];
+    for (int e = 0; e < E; ++e) cursor[e] = 0;
+    for (int t = 0; t < T; ++t)
+        for (int k = 0; k < topk; ++k) {
+            int e = expert_ids[t * topk + k];
+            int pos = offsets[e] + cursor[e]++;
+            token_idx[pos] = t;
+            slot_idx[pos] = k;
+        }
+    free(cursor);
+}

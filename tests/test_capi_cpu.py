@@ -1,0 +1,74 @@
+"""C ABI checks that need no GPU: the library loads, exports every entry point
+include/longhorn_hip.h declares, and rejects bad arguments on the host with
+the documented status codes before any device work is queued."""
+import ctypes as C
+
+import pytest
+
+from longhornai_amd import capi
+
+
+@pytest.fixture(scope="module")
+def L():
+    return capi.load()
+
+
+def test_exports_every_declared_symbol(L):
+    declared = capi.header_symbols()
+    assert len(declared) >= 38
+    missing = [s for s in declared if not hasattr(L.cdll, s)]
+    assert not missing, missing
+    assert set(declared) == set(capi.SIGNATURES), "ctypes table out of sync with the header"
+
+
+def test_status_strings(L):
+    assert L.lhq_status_string(0) == b"ok"
+    assert L.lhq_status_string(capi.LHQ_ERR_UNSUPPORTED) == b"unsupported configuration"
+    assert L.lhq_version() >= 100
+
+
+def test_size_queries(L):
+    # Nt = 28672/16 tiles x Kt = 64 tiles x 1 KiB
+    assert L.lhq_w4_qweight_bytes(8192, 28672) == 1792 * 64 * 1024 == 8192 * 28672 // 2
+    assert L.lhq_w4_scales_bytes(8192, 28672, 128, 1) == 1792 * 64 * 16 * 2
+    assert L.lhq_w4_zeros_bytes(8192, 28672, 128) == 1792 * 8 * 16 * 4
+    assert L.lhq_w4_qweight_bytes(64, 32) == 2 * 1 * 1024           # padded to 16 x 128 tiles
+    assert L.lhq_b8_prepacked_bytes(4096, 14336) == 14336 * 4096
+    assert L.lhq_b8_prepacked_bytes(4, 4) == 256 * 128
+    assert L.lhq_w4_scales_bytes(100, 16, 3, 0) == 0               # G does not divide K
+
+
+FAKE = C.c_void_p(0x1000)  # never dereferenced: validation fails first
+
+
+@pytest.mark.parametrize("name,args,code", [
+    ("lhq_gemm_w4a16", (None, FAKE, FAKE, FAKE, 1, 64, 128, 32, 1.0, 0.0, None), capi.LHQ_ERR_INVALID),
+    ("lhq_gemm_w4a16", (FAKE, FAKE, FAKE, FAKE, 1, 64, 128, 48, 1.0, 0.0, None), capi.LHQ_ERR_INVALID),
+    ("lhq_gemm_w4a16", (FAKE, FAKE, FAKE, FAKE, 1, 64, 96, 96, 1.0, 0.0, None), capi.LHQ_ERR_UNSUPPORTED),
+    ("lhq_gemm_w4a16", (FAKE, FAKE, FAKE, FAKE, 1, 64, 64, 16, 1.0, 0.0, None), capi.LHQ_ERR_UNSUPPORTED),
+    ("lhq_gemm_w4a16_bf16", (FAKE, FAKE, FAKE, None, FAKE, 1, 64, 128, 128, None), capi.LHQ_ERR_INVALID),
+    ("lhq_gemm_w4a16_bf16", (FAKE, FAKE, FAKE, FAKE, FAKE, -1, 64, 128, 128, None), capi.LHQ_ERR_INVALID),
+    ("lhq_gemm_w8a8", (FAKE, FAKE, FAKE, FAKE, FAKE, 4, 4, 4, 1.0, 0.0, None), capi.LHQ_ERR_UNSUPPORTED),
+    ("lhq_gemm_w8a8", (FAKE, FAKE, None, FAKE, FAKE, 4, 4, 16, 1.0, 0.0, None), capi.LHQ_ERR_INVALID),
+    ("lhq_gemm_w8a8_i32", (FAKE, FAKE, FAKE, 4, 0, 16, None), capi.LHQ_ERR_INVALID),
+    ("lhq_w4_prepack_sym", (FAKE, FAKE, 63, 16, 7, FAKE, FAKE, None), capi.LHQ_ERR_INVALID),
+    ("lhq_q4_quantize_groupwise", (FAKE, FAKE, FAKE, 64, 16, 48, None), capi.LHQ_ERR_INVALID),
+    ("lhq_q8_quantize_per_row", (None, FAKE, FAKE, 4, 4, None), capi.LHQ_ERR_INVALID),
+    ("lhq_q8_quantize_per_tensor", (FAKE, FAKE, FAKE, -5, None), capi.LHQ_ERR_INVALID),
+    ("lhq_gemm_w4a16_bf16_grouped", (FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, -1, 16, 64, 128, 128, None),
+     capi.LHQ_ERR_INVALID),
+    ("lhq_gemm_w4a16_bf16_batched", (FAKE, FAKE, FAKE, FAKE, FAKE, 70000, 1, 64, 128, 128, None),
+     capi.LHQ_ERR_INVALID),
+    ("lhq_gemm_f32", (FAKE, FAKE, FAKE, -1, 4, 4, 1.0, 0.0, None), capi.LHQ_ERR_INVALID),
+])
+def test_host_validation(L, name, args, code):
+    st = L.status(name, *args)
+    assert st == code, (st, L.last_error())
+    assert L.last_error()
+
+
+def test_empty_problems_are_noops(L):
+    # M == 0 returns OK without touching memory
+    assert L.status("lhq_gemm_w4a16_bf16", None, FAKE, FAKE, FAKE, FAKE, 0, 64, 128, 128, None) == 0
+    assert L.status("lhq_gemm_w8a8_i32", None, FAKE, FAKE, 0, 16, 16, None) == 0
+    assert L.status("lhq_q8_quantize_per_row", FAKE, FAKE, FAKE, 0, 16, None) == 0

@@ -1,0 +1,164 @@
+"""W4A16 GEMM on the GPU vs the CPU oracle (gemm_quant.cpp:54-82).
+
+Tolerances (north star): relative Frobenius error <= 1e-4 for fp32 outputs,
+<= 1e-2 for bf16 outputs.  The fp32 path is the reference drop-in (fp32
+activations, symmetric int4, fp32 scales); the bf16 path is the benchmark
+configs' asymmetric int4 with fp16 scales and u4 zero points.
+"""
+import numpy as np
+import pytest
+
+from oracle import rel_frobenius
+from tests import _data as D
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-4
+TOL_BF16 = 1e-2
+
+
+@pytest.fixture(scope="module")
+def ops(lib):
+    from longhornai_amd import ops as _ops
+    return _ops
+
+
+def _sym_case(oracle, ops, M, K, N, G, seed, alpha=1.0, beta=0.0):
+    A = D.uniform((M, K), -1, 1, seed)
+    W = D.uniform((K, N), -1, 1, seed + 1)
+    Bp, Bs = oracle.q4_quantize_groupwise(W, G)
+    C0 = D.uniform((M, N), -1, 1, seed + 2)
+    want = oracle.gemm_w4a16_groupwise(A, Bp, Bs, N, G, C0, alpha, beta)
+    w = ops.prepack_w4_sym(ops.dev(Bp), ops.dev(Bs), K, N, G)
+    C = ops.dev(C0)
+    ops.gemm_w4a16(ops.dev(A), w, C, alpha, beta)
+    got = ops.host(C)
+    return got, want
+
+
+@pytest.mark.parametrize("M,K,N,G", [
+    (16, 64, 32, 32),        # test_gemm_quant.cpp:56-57 shape
+    (1, 4096, 4096, 128),
+    (4, 4096, 11008, 128),
+    (16, 11008, 4096, 128),
+    (3, 256, 48, 64),
+    (17, 512, 100, 32),
+    (40, 1024, 272, 256),
+    (1, 8192, 28672, 128),   # decode target shape, fp32 API
+])
+def test_w4a16_f32_matches_oracle(oracle, ops, M, K, N, G):
+    got, want = _sym_case(oracle, ops, M, K, N, G, seed=100 + M + K // 64)
+    err = rel_frobenius(got, want)
+    assert err <= TOL_F32, f"rel Frobenius {err:.3e}"
+
+
+@pytest.mark.parametrize("alpha,beta", [(0.5, 2.0), (1.0, 1.0), (-1.25, 0.0), (2.0, -0.5)])
+def test_w4a16_f32_alpha_beta(oracle, ops, alpha, beta):
+    got, want = _sym_case(oracle, ops, 8, 256, 64, 32, seed=7, alpha=alpha, beta=beta)
+    assert rel_frobenius(got, want) <= TOL_F32
+
+
+def test_w4a16_f32_beta0_ignores_nan_in_c(oracle, ops):
+    """apply_beta with beta == 0 writes zeros without reading C (gemm_quant.cpp:15-16)."""
+    M, K, N, G = 4, 128, 32, 32
+    A = D.uniform((M, K), -1, 1, 1)
+    W = D.uniform((K, N), -1, 1, 2)
+    Bp, Bs = oracle.q4_quantize_groupwise(W, G)
+    want = oracle.gemm_w4a16_groupwise(A, Bp, Bs, N, G)
+    w = ops.prepack_w4_sym(ops.dev(Bp), ops.dev(Bs), K, N, G)
+    C = ops.dev(np.full((M, N), np.nan, np.float32))
+    ops.gemm_w4a16(ops.dev(A), w, C, 1.0, 0.0)
+    got = ops.host(C)
+    assert np.isfinite(got).all()
+    assert rel_frobenius(got, want) <= TOL_F32
+
+
+def _asym_case(oracle, ops, M, K, N, G, seed):
+    A = D.to_bf16_bits(oracle, D.normal((M, K), 1.0, seed))
+    W = D.normal((K, N), 0.02, seed + 1)
+    p, s, z = oracle.q4a_quantize_groupwise(W, G)
+    want_f32 = oracle.gemm_w4a16_asym(A, p, s, z, N, G)
+    w = ops.prepack_w4_asym(ops.dev(p), ops.dev(s), ops.dev(z), K, N, G)
+    C = ops.gemm_w4a16_bf16(ops.dev(A), w)
+    got = D.bf16_bits_to_f32(ops.host(C, np.uint16))
+    return got, want_f32
+
+
+@pytest.mark.parametrize("M,K,N", [
+    (1, 4096, 4096), (4, 4096, 11008), (16, 11008, 4096),      # config 2
+    (1, 8192, 10240), (8, 8192, 8192), (1, 28672, 8192),       # config 5 (decode M)
+    (1, 8192, 28672),                                          # decode target
+    (5, 384, 40),
+])
+def test_w4a16_bf16_matches_oracle(oracle, ops, M, K, N):
+    got, want = _asym_case(oracle, ops, M, K, N, 128, seed=300 + M)
+    err = rel_frobenius(got, want)
+    # bf16 output rounding alone is ~2^-9 relative; the bound is the north star's.
+    assert err <= TOL_BF16, f"rel Frobenius {err:.3e}"
+    # and the result must be the correctly rounded value up to one bf16 ulp
+    want_b = D.bf16_bits_to_f32(D.to_bf16_bits(oracle, want))
+    ulp = np.abs(want_b) * 2.0 ** -7 + 1e-30
+    assert (np.abs(got - want_b) <= ulp).mean() > 0.999
+
+
+@pytest.mark.parametrize("G", [32, 64, 256])
+def test_w4a16_bf16_group_sizes(oracle, ops, G):
+    got, want = _asym_case(oracle, ops, 3, 1024, 96, G, seed=G)
+    assert rel_frobenius(got, want) <= TOL_BF16
+
+
+def test_w4a16_bf16_batched(oracle, ops):
+    import torch
+    B, M, K, N, G = 3, 5, 512, 80, 128
+    As, Ws, wants = [], [], []
+    for b in range(B):
+        A = D.to_bf16_bits(oracle, D.normal((M, K), 1.0, 10 + b))
+        p, s, z = oracle.q4a_quantize_groupwise(D.normal((K, N), 0.02, 20 + b), G)
+        As.append(A)
+        Ws.append(ops.prepack_w4_asym(ops.dev(p), ops.dev(s), ops.dev(z), K, N, G))
+        wants.append(oracle.gemm_w4a16_asym(A, p, s, z, N, G))
+    A_all = ops.dev(np.stack(As))
+    q = torch.cat([w.qweight for w in Ws])
+    s = torch.cat([w.scales for w in Ws])
+    z = torch.cat([w.zeros for w in Ws])
+    C = ops.empty((B, M, N), np.int16)
+    ops.run("lhq_gemm_w4a16_bf16_batched", A_all, q, s, z, C, B, M, N, K, G)
+    got = D.bf16_bits_to_f32(ops.host(C, np.uint16))
+    for b in range(B):
+        assert rel_frobenius(got[b], wants[b]) <= TOL_BF16
+
+
+def _grouped(oracle, ops, T, E, topk, K, N, G, seed, empty_expert=None):
+    import torch
+    ids = D.moe_routing(T, E, topk, seed)
+    if empty_expert is not None:
+        ids[ids == empty_expert] = (empty_expert + 1) % E
+    off, tok, _ = oracle.moe_dispatch_table(ids, E)
+    X = D.to_bf16_bits(oracle, D.normal((T, K), 1.0, seed + 1))
+    A = X[tok]  # dispatched rows, expert-major, token order kept (moe.cpp:124-139)
+    P_, S_, Z_ = [], [], []
+    for e in range(E):
+        p, s, z = oracle.q4a_quantize_groupwise(D.normal((K, N), 0.02, seed + 10 + e), G)
+        P_.append(p); S_.append(s); Z_.append(z)
+    want = oracle.gemm_w4a16_asym_grouped(A, off, np.stack(P_), np.stack(S_), np.stack(Z_), N, G)
+    Ws = [ops.prepack_w4_asym(ops.dev(P_[e]), ops.dev(S_[e]), ops.dev(Z_[e]), K, N, G) for e in range(E)]
+    qptr = torch.tensor([w.qweight.data_ptr() for w in Ws], dtype=torch.int64, device="cuda")
+    sptr = torch.tensor([w.scales.data_ptr() for w in Ws], dtype=torch.int64, device="cuda")
+    zptr = torch.tensor([w.zeros.data_ptr() for w in Ws], dtype=torch.int64, device="cuda")
+    rows = A.shape[0]
+    C = ops.zeros((rows, N), np.int16)
+    ops.run("lhq_gemm_w4a16_bf16_grouped", A, off, qptr, sptr, zptr, C, E, rows, N, K, G)
+    got = D.bf16_bits_to_f32(ops.host(C, np.uint16))
+    return got, want, off
+
+
+def test_w4a16_grouped_small(oracle, ops):
+    got, want, off = _grouped(oracle, ops, T=37, E=5, topk=2, K=256, N=64, G=128, seed=1)
+    assert off[-1] == 74
+    assert rel_frobenius(got, want) <= TOL_BF16
+
+
+def test_w4a16_grouped_empty_expert(oracle, ops):
+    got, want, off = _grouped(oracle, ops, T=20, E=4, topk=1, K=128, N=48, G=64, seed=3, empty_expert=2)
+    assert off[3] == off[2]
+    assert rel_frobenius(got, want) <= TOL_BF16
