@@ -1,0 +1,392 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X quantized-GEMM path (one GPU).
+
+Headline metric: "W4A16 decode GB/s (% HBM peak) + W8A8
+prefill TOPS (% MFMA peak), 1 GPU".
+
+* ``value`` -- W4A16 decode GEMV, M=1, K=8192, N=28672, asymmetric int4
+  group 128 (fp16 scales, u4 zero points), bf16 activations and output: the
+  north-star shape.  One step = one GEMM launch over one weight matrix; the
+  launches rotate over enough distinct weight sets (> 2x the 256 MB Infinity
+  Cache) that every step streams its weights from HBM.  Throughput is the
+  algorithmic bytes of one call (packed weights + scales + zeros + activations
+  + output) times K steps over the timed region.
+* ``w8a8_prefill`` -- int8 x int8 -> int32 -> fp32 scale -> bf16, M=4096,
+  K=4096, N=14336 (north-star target) and M=2048 (config 3): TOPS = 2*M*K*N
+  per call over the measured launch time.
+* ``roofline`` -- the W4A16 decode kernel against the 8 TB/s HBM peak, with
+  HBM traffic per launch from the committed rocprofv3 PMC summary.
+* ``cpu_baseline`` -- the reference's own gemm_w4a16_groupwise
+  (gemm_quant.cpp:54-82, compiled from its sources into oracle/_ref) or, where
+  that library is absent, the C restatement in oracle/, timed on the host on
+  the same M=1, K=8192, N=28672 shape (fp32 API, symmetric int4 -- the only
+  form the reference has), single thread as the reference runs.
+
+Timing: launches are captured into HIP graphs (torch.cuda.CUDAGraph drives
+hipStreamBeginCapture on the stream the kernels are launched on) so the
+timed region measures the GPU, not Python; HIP events bracket the region on
+that same stream.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, published
+INT8_PEAK_TOPS = 5000.0     # MI355X dense int8 MFMA, published
+BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA, published
+INFINITY_CACHE_BYTES = 256 << 20
+
+
+def w4a16_bytes(M: int, K: int, N: int, G: int) -> int:
+    """Algorithmic bytes of one asymmetric W4A16 call (u4 weights, fp16
+    scales, u4 zeros, bf16 activations and output)."""
+    return K * N // 2 + (K // G) * N * 2 + (K // G) * N // 2 + M * K * 2 + M * N * 2
+
+
+def w4a16_sym_f32_bytes(M: int, K: int, N: int, G: int) -> int:
+    """Algorithmic bytes of the reference's fp32-API call (int4 weights, fp32
+    scales, fp32 activations and output)."""
+    return K * N // 2 + (K // G) * N * 4 + M * K * 4 + M * N * 4
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# GPU legs
+# ---------------------------------------------------------------------------
+
+class GraphTimer:
+    """Times exactly `steps` launches of `launch(i)` captured in HIP graphs."""
+
+    def __init__(self, launch, period: int, chunk: int):
+        import torch
+        self.torch = torch
+        self.launch = launch
+        self.period = period
+        self.chunk = max(1, chunk)
+        self._graphs = {}
+
+    def _graph(self, n: int, start: int):
+        key = (n, start % self.period)
+        g = self._graphs.get(key)
+        if g is None:
+            torch = self.torch
+            g = torch.cuda.CUDAGraph()
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                with torch.cuda.graph(g, stream=s):
+                    for i in range(n):
+                        self.launch(start + i)
+            torch.cuda.current_stream().wait_stream(s)
+            torch.cuda.synchronize()
+            self._graphs[key] = g
+        return g
+
+    def run(self, steps: int) -> None:
+        done = 0
+        while done < steps:
+            n = min(self.chunk, steps - done)
+            self._graph(n, done).replay()
+            done += n
+
+    def prepare(self, steps: int) -> None:
+        done = 0
+        while done < steps:
+            n = min(self.chunk, steps - done)
+            self._graph(n, done)
+            done += n
+
+    def time(self, steps: int, warmup: int):
+        """Returns (elapsed ms of the timed region by HIP events, wall ms)."""
+        torch = self.torch
+        self.prepare(steps)
+        if warmup:
+            self.prepare(warmup)
+            self.run(warmup)
+        torch.cuda.synchronize()
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        ev0.record()
+        self.run(steps)
+        ev1.record()
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) * 1e3
+        return ev0.elapsed_time(ev1), wall
+
+
+def make_w4_sets(ops, K: int, N: int, G: int, nsets: int, seed: int):
+    """`nsets` distinct asymmetric int4 weight sets quantized on the device
+    from N(0, 0.02), prepacked; plus bf16 N(0,1) activation rows."""
+    import numpy as np
+    import torch
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    sets = []
+    for _ in range(nsets):
+        W = torch.randn((K, N), generator=gen, device="cuda", dtype=torch.float32) * 0.02
+        packed = ops.empty((K // 2, N), np.uint8)
+        sc = ops.empty((K // G, N), np.uint16)
+        zp = ops.empty((K // G, N), np.uint8)
+        ops.lib().call("lhq_q4a_quantize_groupwise", W.data_ptr(), packed.data_ptr(), sc.data_ptr(),
+                       zp.data_ptr(), K, N, G, ops.stream())
+        del W
+        sets.append(ops.prepack_w4_asym(packed, sc, zp, K, N, G))
+        del packed, sc, zp
+    torch.cuda.synchronize()
+    return sets
+
+
+def bench_w4a16(ops, M, K, N, G, steps, warmup, seed=0, min_rotate_bytes=2 * INFINITY_CACHE_BYTES + (1 << 26)):
+    import numpy as np
+    import torch
+    per = w4a16_bytes(M, K, N, G)
+    nsets = max(2, -(-min_rotate_bytes // per))
+    sets = make_w4_sets(ops, K, N, G, nsets, seed)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed + 1)
+    A = [(torch.randn((M, K), generator=gen, device="cuda") .to(torch.bfloat16)).view(torch.int16)
+         for _ in range(nsets)]
+    C = [ops.empty((M, N), np.int16) for _ in range(nsets)]
+    fn = ops.lib().cdll.lhq_gemm_w4a16_bf16
+    args = [(A[i].data_ptr(), sets[i].qweight.data_ptr(), sets[i].scales.data_ptr(),
+             sets[i].zeros.data_ptr(), C[i].data_ptr()) for i in range(nsets)]
+
+    def launch(i):
+        a = args[i % nsets]
+        st = fn(a[0], a[1], a[2], a[3], a[4], M, N, K, G, ops.stream())
+        if st:
+            raise RuntimeError(f"lhq_gemm_w4a16_bf16: {ops.lib().last_error()}")
+
+    timer = GraphTimer(launch, nsets, chunk=nsets * max(1, 64 // nsets))
+    ms, wall = timer.time(steps, warmup)
+    us = ms * 1e3 / steps
+    res = {"M": M, "K": K, "N": N, "G": G, "bytes_per_call": per, "weight_sets": nsets,
+           "rotate_bytes": per * nsets, "us_per_call": us, "gbs": per / (us * 1e-6) / 1e9,
+           "elapsed_ms": ms, "wall_ms": wall}
+    res["hbm_frac"] = res["gbs"] / HBM_PEAK_GBS
+    del timer, sets, A, C
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_w8a8(ops, M, K, N, steps, warmup, seed=0):
+    import numpy as np
+    import torch
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    W = torch.randn((K, N), generator=gen, device="cuda") * 0.02
+    Bq = ops.empty((K, N), np.int8)
+    Bs = ops.empty((N,), np.float32)
+    ops.lib().call("lhq_q8_quantize_per_col", W.data_ptr(), Bq.data_ptr(), Bs.data_ptr(), K, N, ops.stream())
+    del W
+    Bt = ops.prepack_b8(Bq, K, N)
+    del Bq
+    X = torch.randn((M, K), generator=gen, device="cuda")
+    # 0.1 % of the activations replaced by +-20 outliers (config 3)
+    n_out = max(1, (M * K) // 1000)
+    pos = torch.randint(0, M * K, (n_out,), generator=gen, device="cuda")
+    sign = torch.where(torch.rand((n_out,), generator=gen, device="cuda") < 0.5, -20.0, 20.0)
+    X.view(-1)[pos] = sign
+    Xb = X.to(torch.bfloat16).view(torch.int16)
+    del X
+    Aq = ops.empty((M, K), np.int8)
+    As = ops.empty((M,), np.float32)
+    C = ops.empty((M, N), np.int16)
+    fn = ops.lib().cdll.lhq_gemm_w8a8_bf16
+    qfn = ops.lib().cdll.lhq_q8_quantize_per_row_bf16
+
+    def launch(_i):
+        st = fn(Aq.data_ptr(), Bt.data_ptr(), As.data_ptr(), Bs.data_ptr(), C.data_ptr(), M, N, K, ops.stream())
+        if st:
+            raise RuntimeError(f"lhq_gemm_w8a8_bf16: {ops.lib().last_error()}")
+
+    def qlaunch(_i):
+        st = qfn(Xb.data_ptr(), Aq.data_ptr(), As.data_ptr(), M, K, ops.stream())
+        if st:
+            raise RuntimeError(f"lhq_q8_quantize_per_row_bf16: {ops.lib().last_error()}")
+
+    qlaunch(0)
+    torch.cuda.synchronize()
+    ms, _ = GraphTimer(launch, 1, chunk=16).time(steps, warmup)
+    us = ms * 1e3 / steps
+    ops_per = 2 * M * K * N
+    qms, _ = GraphTimer(qlaunch, 1, chunk=16).time(steps, warmup)
+    qus = qms * 1e3 / steps
+    qbytes = M * K * 2 + M * K + M * 4
+    res = {"M": M, "K": K, "N": N, "us_per_call": us, "tops": ops_per / (us * 1e-6) / 1e12,
+           "act_quant_us": qus, "act_quant_gbs": qbytes / (qus * 1e-6) / 1e9}
+    res["mfma_frac"] = res["tops"] / INT8_PEAK_TOPS
+    del Bt, Xb, Aq, As, C
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return res
+
+
+def copy_probe(nbytes: int = 1 << 30, reps: int = 5) -> None:
+    """A plain device copy of known size: the calibration kernel for the
+    FETCH_SIZE / WRITE_SIZE counters (each launch reads and writes nbytes)."""
+    import torch
+    a = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    a.fill_(1)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline (test infrastructure: the reference's path or its restatement)
+# ---------------------------------------------------------------------------
+
+def cpu_baseline(M: int, K: int, N: int, G: int, budget_s: float):
+    import numpy as np
+    from oracle import Oracle, Ref, ref_available
+    kind = "reference" if ref_available() else "port"
+    impl = Ref() if kind == "reference" else Oracle()
+    rng = np.random.default_rng(0)
+    W = (rng.standard_normal((K, N), dtype=np.float32) * np.float32(0.02))
+    Bp, Bs = impl.q4_quantize_groupwise(W, G)
+    del W
+    A = rng.standard_normal((M, K), dtype=np.float32)
+    times = []
+    impl.gemm_w4a16_groupwise(A, Bp, Bs, N, G)  # warm-up
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 20):
+        t0 = time.perf_counter()
+        impl.gemm_w4a16_groupwise(A, Bp, Bs, N, G)
+        times.append(time.perf_counter() - t0)
+    p50 = statistics.median(times)
+    per = w4a16_sym_f32_bytes(M, K, N, G)
+    return {
+        "value": per / p50 / 1e9,
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": kind,
+        "sample": (f"gemm_w4a16_groupwise (gemm_quant.cpp:54-82) M={M} K={K} N={N} G={G}, fp32 A/C, "
+                   f"symmetric int4 + fp32 scales ({per} algorithmic B/call); p50 of {len(times)} calls, "
+                   f"{p50 * 1e3:.1f} ms/call, 1 thread; host nproc={os.cpu_count()}"),
+        "ms_per_call": p50 * 1e3,
+        "speedup_gpu_over_cpu": None,
+    }
+
+
+# ---------------------------------------------------------------------------
+# traffic from the committed PMC summary
+# ---------------------------------------------------------------------------
+
+def committed_traffic(kernel_key: str):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE +
+    WRITE_SIZE, calibrated against a plain copy), as recorded in
+    profiles/<kernel_key>_pmc.md on a line `traffic_bytes_per_launch: <int>`."""
+    path = os.path.join(ROOT, "profiles", f"{kernel_key}_pmc.md")
+    try:
+        text = open(path).read()
+    except OSError:
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", text)
+    return int(m.group(1)) if m else None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline timing")
+    ap.add_argument("--no-w8a8", action="store_true", help="skip the W8A8 prefill leg")
+    ap.add_argument("--w8a8-steps", type=int, default=200)
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run a 1 GiB device copy (PMC calibration kernel)")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}): "
+              "this build has no multi-GPU path; the kernels shard along N with no collective "
+              "(see the design notes).", file=sys.stderr)
+        return 2
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    torch.cuda.set_device(0)
+    from longhornai_amd import ops
+    ops.lib()  # fails loudly when the HIP library is missing
+
+    if args.copy_probe:
+        copy_probe()
+
+    M, K, N, G = 1, 8192, 28672, 128
+    log(f"w4a16 decode M={M} K={K} N={N} G={G}: {args.warmup} warmup + {args.steps} timed steps")
+    w4 = bench_w4a16(ops, M, K, N, G, args.steps, args.warmup)
+    log(f"  {w4['us_per_call']:.2f} us/call  {w4['gbs']:.1f} GB/s  ({100 * w4['hbm_frac']:.1f}% of HBM peak), "
+        f"{w4['weight_sets']} rotating sets = {w4['rotate_bytes'] / 2**20:.0f} MiB")
+
+    w8 = []
+    if not args.no_w8a8:
+        for m in (4096, 2048):
+            log(f"w8a8 prefill M={m} K=4096 N=14336: {args.w8a8_steps} steps")
+            r = bench_w8a8(ops, m, 4096, 14336, args.w8a8_steps, max(10, args.w8a8_steps // 10))
+            log(f"  {r['us_per_call']:.1f} us/call  {r['tops']:.0f} TOPS ({100 * r['mfma_frac']:.1f}% of int8 peak); "
+                f"act quant {r['act_quant_us']:.1f} us ({r['act_quant_gbs']:.0f} GB/s)")
+            w8.append(r)
+
+    cpu = None
+    if not args.no_cpu:
+        log(f"cpu baseline: ~{args.cpu_budget:.0f} s")
+        cpu = cpu_baseline(M, K, N, G, args.cpu_budget)
+        cpu["speedup_gpu_over_cpu"] = (cpu["ms_per_call"] * 1e3) / w4["us_per_call"]
+        log(f"  {cpu['kind']}: {cpu['ms_per_call']:.1f} ms/call, {cpu['value']:.2f} GB/s")
+
+    traffic = committed_traffic("w4a16_decode")
+    line = {
+        "metric": "W4A16 decode GB/s (% HBM peak) + W8A8 prefill TOPS (% MFMA peak), 1 GPU",
+        "value": round(w4["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": w4["elapsed_ms"] / args.steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u4xbf16->f32",
+        "data": "synthetic (seeded N(0,0.02) weights quantized on device, N(0,1) bf16 activations)",
+        "config": {"workload": "w4a16_decode_gemv", "M": M, "K": K, "N": N, "group_size": G,
+                   "weights": "asymmetric int4, fp16 scale + u4 zero per group",
+                   "rotating_weight_sets": w4["weight_sets"], "rotate_bytes": w4["rotate_bytes"],
+                   "bytes_per_step": w4["bytes_per_call"]},
+        "roofline": {"bound": "hbm", "achieved": round(w4["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(w4["hbm_frac"], 4), "traffic": traffic,
+                     "kernel": "w4_gemv_kernel", "algorithmic_bytes": w4["bytes_per_call"],
+                     "us_per_launch": round(w4["us_per_call"], 3)},
+        "w8a8_prefill": [
+            {"M": r["M"], "K": r["K"], "N": r["N"], "us_per_call": round(r["us_per_call"], 2),
+             "value": round(r["tops"], 1), "unit": "TOPS", "peak": INT8_PEAK_TOPS,
+             "frac": round(r["mfma_frac"], 4), "act_quant_us": round(r["act_quant_us"], 2)}
+            for r in w8],
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
