@@ -313,6 +313,8 @@ def main() -> int:
     ap.add_argument("--w8a8-steps", type=int, default=200)
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a 1 GiB device copy (PMC calibration kernel)")
+    ap.add_argument("--only", choices=["w4a16", "w8a8"], default=None,
+                    help="run one leg only (profiling); prints that leg's summary, not the bench line")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -334,10 +336,19 @@ def main() -> int:
         copy_probe()
 
     M, K, N, G = 1, 8192, 28672, 128
+    if args.only == "w8a8":
+        for m in (4096, 2048):
+            r = bench_w8a8(ops, m, 4096, 14336, args.w8a8_steps, max(10, args.w8a8_steps // 10))
+            print(json.dumps({"leg": "w8a8_prefill", **r}), flush=True)
+        return 0
     log(f"w4a16 decode M={M} K={K} N={N} G={G}: {args.warmup} warmup + {args.steps} timed steps")
     w4 = bench_w4a16(ops, M, K, N, G, args.steps, args.warmup)
     log(f"  {w4['us_per_call']:.2f} us/call  {w4['gbs']:.1f} GB/s  ({100 * w4['hbm_frac']:.1f}% of HBM peak), "
         f"{w4['weight_sets']} rotating sets = {w4['rotate_bytes'] / 2**20:.0f} MiB")
+
+    if args.only == "w4a16":
+        print(json.dumps({"leg": "w4a16_decode", **w4}), flush=True)
+        return 0
 
     w8 = []
     if not args.no_w8a8:
@@ -375,7 +386,7 @@ def main() -> int:
                    "bytes_per_step": w4["bytes_per_call"]},
         "roofline": {"bound": "hbm", "achieved": round(w4["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(w4["hbm_frac"], 4), "traffic": traffic,
-                     "kernel": "w4_gemv_kernel", "algorithmic_bytes": w4["bytes_per_call"],
+                     "kernel": "w4_decode_kernel", "algorithmic_bytes": w4["bytes_per_call"],
                      "us_per_launch": round(w4["us_per_call"], 3)},
         "w8a8_prefill": [
             {"M": r["M"], "K": r["K"], "N": r["N"], "us_per_call": round(r["us_per_call"], 2),

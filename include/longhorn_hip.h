@@ -95,7 +95,7 @@ int lhq_fp8_dequantize_per_col(const uint8_t* src, const float* scales, float* d
  *   qweight [Nt][Kt][64][16 B]: a 1 KiB tile holds 16 columns x 128 k; the
  *     16 bytes of lane l are the B operands of four 16x16x32 MFMAs for column
  *     16*nt + (l & 15): dword j covers k = 128*kt + 32*j + 8*(l >> 4) + e,
- *     e = 0..7, element e in nibble (e & 1) ? 4 + e/2 : e/2; codes are
+ *     e = 0..7, element e in nibble e < 4 ? 2e : 2(e-4)+1; codes are
  *     unsigned (symmetric q is stored as q + 8).
  *   scales  [Nt][NG][16] fp32 (symmetric) or fp16 (asymmetric).
  *   zeros   [Nt][ceil(NG/8)][16] u32, group g in nibble g % 8.

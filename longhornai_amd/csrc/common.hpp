@@ -128,8 +128,9 @@ __device__ __forceinline__ int sat_rint(float v, int lim) {
 //     A 1 KiB tile covers 16 columns x 128 k.  Lane l owns column
 //     16*nt + (l & 15) and, in dword j (0..3), the eight k values
 //     128*kt + 32*j + 8*(l >> 4) + e (e = 0..7): exactly the B operand of one
-//     16x16x32 MFMA.  Element e sits in nibble slot (e & 1) ? 4 + e/2 : e/2,
-//     so elements (2p, 2p+1) are nibbles p and p+4 (bits 4p and 4p+16).
+//     16x16x32 MFMA.  Element e sits in nibble w4_slot(e): elements 0..3 in
+//     the low nibbles of bytes 0..3, elements 4..7 in their high nibbles, so
+//     one mask exposes four codes as whole bytes (see w4_operand).
 //   scales   [Nt][NG][16]  fp32 (symmetric) or fp16 (asymmetric), NG = K/G
 //   zeros    [Nt][ceil(NG/8)][16] u32, group g in nibble g % 8 (asymmetric)
 // Codes are unsigned: symmetric int4 q in [-7,7] is stored as q + 8 with an
@@ -142,11 +143,28 @@ constexpr int kW4TileBytes = 1024;
 __host__ __device__ inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 __host__ __device__ inline int64_t ceil_div64(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// bf16 bits of (16 + u) for nibbles p and p+4 of `d`, packed low/high: the
-// nibble lands on mantissa bits 3..6 of a bf16 whose exponent encodes 16.
-__device__ __forceinline__ uint32_t w4_pair_16pu(uint32_t d, int p) {
-    uint32_t sh = (p == 0) ? (d << 3) : (d >> (4 * p - 3));
-    return (sh & 0x00780078u) | 0x41804180u;
+// Nibble index (bits 4*slot .. 4*slot+3 of the lane's dword) of operand
+// element e of a prepacked W4 dword.
+__host__ __device__ constexpr int w4_slot(int e) { return e < 4 ? 2 * e : 2 * (e - 4) + 1; }
+
+// The codes enter the MFMA as the exact bf16 integers 128 + u: high byte
+// 0x43 (exponent 2^7), code in mantissa bits 0..3.
+constexpr float kW4Bias = 128.0f;
+
+// One prepacked dword (eight 4-bit codes) -> the four bf16 pairs of a
+// 16x16x32 MFMA B operand: 2 masks, 1 shift and 4 byte permutes.
+// __builtin_amdgcn_perm(hi, lo, sel) picks result byte i from the eight
+// bytes {lo: 0..3, hi: 4..7} named by byte i of sel.
+__device__ __forceinline__ u32x4_t w4_operand(uint32_t d) {
+    const uint32_t lo = d & 0x0F0F0F0Fu;         // codes of elements 0..3
+    const uint32_t hi = (d >> 4) & 0x0F0F0F0Fu;  // codes of elements 4..7
+    constexpr uint32_t kExp = 0x43434343u;
+    u32x4_t b;
+    b[0] = __builtin_amdgcn_perm(kExp, lo, 0x04010400u);  // {e0, e1}
+    b[1] = __builtin_amdgcn_perm(kExp, lo, 0x04030402u);  // {e2, e3}
+    b[2] = __builtin_amdgcn_perm(kExp, hi, 0x04010400u);  // {e4, e5}
+    b[3] = __builtin_amdgcn_perm(kExp, hi, 0x04030402u);  // {e6, e7}
+    return b;
 }
 
 }  // namespace lhq

@@ -39,8 +39,7 @@ __global__ void w4_prepack_qweight_kernel(const uint8_t* __restrict__ packed,
                 // symmetric: two's-complement q in [-8,7] -> q + 8 (quant.hpp:73-74)
                 u = ASYM ? nib : ((nib ^ 8u) & 0xfu);
             }
-            const int slot = (e & 1) ? 4 + (e >> 1) : (e >> 1);
-            d |= u << (4 * slot);
+            d |= u << (4 * w4_slot(e));
         }
         out[j] = d;
     }

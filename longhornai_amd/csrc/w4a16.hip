@@ -3,18 +3,26 @@
 //
 // Reference: gemm_w4a16_groupwise (gemm_quant.hpp:47-57, gemm_quant.cpp:54-82)
 // dequantizes a [G, N] fp32 panel per K-group and runs an fp32 axpy over it.
-// Here nothing is dequantized to memory.  The decode/skinny kernel below
-// (M <= 16 per row block) streams each 1 KiB weight tile once with 128-bit
-// loads and feeds the MFMA the EXACT integers 16 + u as bf16 (one shift and
-// one and-or per pair of nibbles).  Per K-segment of the group it forms
-//     t  = sum_k x[m,k] * (16 + u[k,n])          (MFMA, fp32 accumulate)
-//     xs = sum_k x[m,k]                           (MFMA against a ones operand)
-// and adds s[g,n] * (t - (16 + z[g,n]) * xs) to the fp32 accumulator, which is
-// sum_k x * (u - z) * s up to fp32 reassociation -- the reference's value.
+// Here nothing is dequantized to memory.  Each 1 KiB weight tile is streamed
+// once with 128-bit loads and fed to the MFMA as the EXACT integers 128 + u
+// (bf16; w4_operand).  Per K-segment of a group the kernels form
+//     t  = sum_k x[m,k] * (128 + u[k,n])          (MFMA, fp32 accumulate)
+//     xs = sum_k x[m,k]                            (MFMA against a ones operand)
+// and add s[g,n] * (t - (128 + z[g,n]) * xs) to an fp32 accumulator: that is
+// sum_k x * (u - z) * s up to fp32 reassociation, the reference's value.
 // fp32 activations are split into bf16 hi + lo (two MFMAs), which keeps the
-// product error near 2^-17 relative.  K is split across the waves of a
-// workgroup and reduced through LDS in a fixed order (deterministic).
+// product error near 2^-17 relative.
+//
+// Two kernels share that arithmetic:
+//   w4_decode_kernel -- M <= 16 with the activations small enough to stage in
+//     LDS: a streaming GEMV whose only global loads in the main loop are the
+//     weight tiles and their scales / zero points (a D-deep ring per wave).
+//   w4_gemv_kernel   -- any M in 16-row blocks, uniform batches and ragged
+//     grouped launches (device-side group table).
+// Both split K over the waves of a workgroup and reduce through LDS in wave
+// order, so results are deterministic.
 #include <cstdlib>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -30,6 +38,9 @@ struct W4Args {
     const uint32_t* zeros;
     void* C;
     int M, N, K, G, Nt, Kt, NG, NG8;
+    // group of tile kt when G > 128: __umulhi(kt, gmul), gmul = ceil(2^32 / (G/128))
+    // (exact for kt, G/128 < 2^16); 0 when G <= 128
+    uint32_t gmul;
     float alpha, beta;
     // per-matrix strides for uniform batches (grid.z): elements of A / C,
     // bytes of qweight, elements of scales / zeros
@@ -42,6 +53,21 @@ struct W4Args {
     const uint32_t* const* zss;
     int num_groups, row_capacity;
 };
+
+// Scale group of segment s of K tile kt; a segment is BPS 32-wide k blocks
+// (min(G,128) k values), so G <= 128 needs no division at all.
+template <int BPS>
+__device__ __forceinline__ int group_of(int kt, int s, uint32_t gmul) {
+    if constexpr (BPS < 4) return kt * (4 / BPS) + s;
+    else return gmul ? static_cast<int>(__umulhi(static_cast<uint32_t>(kt), gmul)) : kt;
+}
+// The same with G > 128 known at compile time (GBIG) or known false.
+template <int BPS, bool GBIG>
+__device__ __forceinline__ int group_of_c(int kt, int s, uint32_t gmul) {
+    if constexpr (BPS < 4) return kt * (4 / BPS) + s;
+    else if constexpr (GBIG) return static_cast<int>(__umulhi(static_cast<uint32_t>(kt), gmul));
+    else return kt;
+}
 
 // Map blockIdx.y of a grouped launch to (group, first row, row end): groups
 // take ceil(rows/16) row blocks each, in order.  Offsets are clamped to
@@ -86,15 +112,30 @@ __device__ __forceinline__ void load_a8(const void* A, int64_t off, bool ok, u32
     }
 }
 
-// Decode / skinny W4A16.  grid = (ceil(Nt/T), ceil(M/16), batch); a
-// workgroup of WAVES waves owns T column tiles and 16 rows; wave w walks its
-// share of the K tiles.  BPS = 32-wide k blocks per scale segment
-// (min(G,128)/32).
+// Output element (row r, column c) of a W4 GEMM: fp32 with the reference's
+// alpha / beta (beta == 0 never reads C, gemm_quant.cpp:12-21) or bf16 RNE.
+template <bool F32C>
+__device__ __forceinline__ void w4_store(const W4Args& p, int64_t o, float v) {
+    if constexpr (F32C) {
+        float* Cp = static_cast<float*>(p.C);
+        float out = p.alpha * v;
+        if (p.beta != 0.0f) out = p.beta * Cp[o] + out;
+        Cp[o] = out;
+    } else {
+        static_cast<uint16_t*>(p.C)[o] = f32_to_bf16(v);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Generic kernel.  grid = (ceil(Nt/T), row blocks, batch); a workgroup of
+// WAVES waves owns T column tiles and 16 rows; wave w walks its share of the
+// K tiles.  BPS = 32-wide k blocks per scale segment (min(G,128)/32).
+// ---------------------------------------------------------------------------
 template <bool F32A, bool ASYM, bool F32C, int T, int WAVES, int BPS, bool GROUPED>
 __global__ __launch_bounds__(64 * WAVES) void w4_gemv_kernel(W4Args p) {
     constexpr int SEGS = 4 / BPS;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nt0 = blockIdx.x * T;
     int m0 = blockIdx.y * 16, m_end = p.M;
     const int z = blockIdx.z;
@@ -149,16 +190,14 @@ __global__ __launch_bounds__(64 * WAVES) void w4_gemv_kernel(W4Args p) {
                 xs = mfma_bf16_16x16x32(ah[j], ones, xs);
                 if constexpr (F32A) xs = mfma_bf16_16x16x32(al[j], ones, xs);
             }
-            const int g = min((kt * kW4TileK + s * BPS * 32) / p.G, p.NG - 1);
+            const int g = group_of<BPS>(kt, s, p.gmul);
 #pragma unroll
             for (int t = 0; t < T; ++t) {
                 f32x4_t acc_t = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int jj = 0; jj < BPS; ++jj) {
                     const int j = s * BPS + jj;
-                    u32x4_t b;
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) b[q] = w4_pair_16pu(w[t][j], q);
+                    const u32x4_t b = w4_operand(w[t][j]);
                     acc_t = mfma_bf16_16x16x32(ah[j], b, acc_t);
                     if constexpr (F32A) acc_t = mfma_bf16_16x16x32(al[j], b, acc_t);
                 }
@@ -167,10 +206,10 @@ __global__ __launch_bounds__(64 * WAVES) void w4_gemv_kernel(W4Args p) {
                 if constexpr (ASYM) {
                     sc = f16_to_f32(static_cast<const uint16_t*>(scales)[si]);
                     const uint32_t zw = zeros[(static_cast<int64_t>(ntc[t]) * p.NG8 + (g >> 3)) * 16 + col];
-                    zc = 16.0f + static_cast<float>((zw >> (4 * (g & 7))) & 15u);
+                    zc = kW4Bias + static_cast<float>((zw >> (4 * (g & 7))) & 15u);
                 } else {
                     sc = static_cast<const float*>(scales)[si];
-                    zc = 24.0f;  // 16 + implied zero point 8
+                    zc = kW4Bias + 8.0f;  // implied zero point 8
                 }
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
@@ -183,15 +222,7 @@ __global__ __launch_bounds__(64 * WAVES) void w4_gemv_kernel(W4Args p) {
         const int r = m0 + 4 * (ln >> 4) + i;
         const int c = (nt0 + t) * kW4TileN + (ln & 15);
         if (r >= m_end || c >= p.N || nt0 + t >= p.Nt) return;
-        const int64_t o = z * p.c_bs + static_cast<int64_t>(r) * p.N + c;
-        if constexpr (F32C) {
-            float* Cp = static_cast<float*>(p.C);
-            float out = p.alpha * v;
-            if (p.beta != 0.0f) out = p.beta * Cp[o] + out;
-            Cp[o] = out;
-        } else {
-            static_cast<uint16_t*>(p.C)[o] = f32_to_bf16(v);
-        }
+        w4_store<F32C>(p, z * p.c_bs + static_cast<int64_t>(r) * p.N + c, v);
     };
 
     if constexpr (WAVES == 1) {
@@ -216,15 +247,293 @@ __global__ __launch_bounds__(64 * WAVES) void w4_gemv_kernel(W4Args p) {
     }
 }
 
-// Tuning knobs (read once): LHQ_W4_TILES (1|2) and LHQ_W4_WAVES (2|4|8)
-// override the shape heuristic; unset = heuristic.
+// ---------------------------------------------------------------------------
+// Decode kernel (M <= 16 rows, one 16-row block).  The workgroup stages its
+// activation rows [min(M,16), Kp] in LDS once (fp32 activations as bf16
+// hi / lo planes), so the main loop's only global loads are weight tiles and
+// their scales / zero points.  Vector-memory loads complete in order: an
+// activation fetch queued behind weight tiles would wait for all of them.
+//
+// Each wave owns NPW consecutive K tiles of T column tiles per pass; a pass
+// issues all of its loads first and then consumes them in issue order, so
+// the wave waits for the memory system once per pass and nothing loaded is
+// carried across a loop edge.  Overlap comes from the many resident waves.
+// grid = (ceil(Nt/T), 1, batch), blockDim = 64*S: the S waves cover S*NPW
+// consecutive tiles per pass (passes repeat until Kt is covered) and are
+// reduced through LDS in wave order (deterministic).
+// ---------------------------------------------------------------------------
+
+// Every load a wave issues is unconditional (out-of-range addresses are
+// clamped to valid ones, the values discarded): the compiler counts
+// outstanding loads per path, and a load that only some paths issue would
+// turn each later wait into a wait for everything.
+template <bool F32A, bool ASYM, bool F32C, int T, int NPW, int BPS, bool GBIG>
+__global__ __launch_bounds__(T == 1 ? 1024 : 512) void w4_decode_kernel(W4Args p) {
+    static_assert(NPW == 4 || NPW == 8, "passes start at multiples of NPW tiles");
+    constexpr int SEGS = 4 / BPS;
+    // zero words (8 groups each) per pass: G < 128 -> the pass's words
+    // (passes start at multiples of 8 tiles); G == 128 -> one shared word;
+    // G > 128 -> one per tile
+    constexpr int NZW = (BPS < 4) ? (NPW * SEGS + 7) / 8 : (GBIG ? NPW : 1);
+    // [F32A ? 2 : 1 planes][Ml rows][Kp], bf16 (fp32 activations: hi, lo)
+    extern __shared__ __attribute__((aligned(16))) uint16_t a_lds[];
+    __shared__ float red[T == 1 ? 16 : 8][T][4][64];
+
+    const int S = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int z = blockIdx.z;
+    const int Ml = min(p.M, 16);
+    const int col = lane & 15;
+    const int Kp = p.Kt * kW4TileK;
+
+    // Column tiles past Nt (odd Nt with T = 2) alias the last one; their
+    // outputs are never stored.  Bases are wave-uniform; the per-lane parts
+    // of every address below are 32-bit offsets.
+    const uint8_t* qwb[T];
+    const char* scb[T];
+    const char* zwb[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        const int64_t nt = min(static_cast<int>(blockIdx.x) * T + t, p.Nt - 1);
+        qwb[t] = p.qw + z * p.qw_bs + nt * p.Kt * kW4TileBytes;
+        scb[t] = static_cast<const char*>(p.scales) + (z * p.s_bs + nt * p.NG * 16) * (ASYM ? 2 : 4);
+        zwb[t] = ASYM ? reinterpret_cast<const char*>(p.zeros + z * p.z_bs + nt * p.NG8 * 16) : nullptr;
+    }
+    // fp16 scales are fetched as the aligned dword holding columns
+    // (col & ~1, col | 1); the lane's half is selected at use
+    const uint32_t s_half = ASYM ? 16u * (col & 1) : 0u;
+    const uint32_t s_col = ASYM ? static_cast<uint32_t>((col & ~1) * 2) : static_cast<uint32_t>(col * 4);
+
+    // one pass worth of loaded operands; two of them alternate so the next
+    // pass's loads are in flight while the current pass is consumed
+    struct Pass {
+        u32x4_t w[NPW][T];
+        uint32_t sw[NPW][T][SEGS];
+        uint32_t zw[NZW][T];
+    };
+    // All loads of the pass starting at tile kt0, in consumption order (zero
+    // words first: the first tile needs them); tiles past Kt re-read the
+    // last tile (the same lines, never consumed).
+    auto issue = [&](Pass& P, int kt0) {
+        if constexpr (ASYM) {
+#pragma unroll
+            for (int q = 0; q < NZW; ++q) {
+                const int g = (BPS < 4) ? group_of_c<BPS, GBIG>(min(kt0, p.Kt - 1), 0, 0) + 8 * q
+                                        : group_of_c<BPS, GBIG>(min(kt0 + q, p.Kt - 1), 0, p.gmul);
+                const uint32_t off = static_cast<uint32_t>((min(g >> 3, p.NG8 - 1) * 16 + col) * 4);
+#pragma unroll
+                for (int t = 0; t < T; ++t) P.zw[q][t] = *reinterpret_cast<const uint32_t*>(zwb[t] + off);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NPW; ++i) {
+            const int kt = min(kt0 + i, p.Kt - 1);
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+#pragma unroll
+                for (int s = 0; s < SEGS; ++s) {
+                    const uint32_t off = static_cast<uint32_t>(group_of_c<BPS, GBIG>(kt, s, p.gmul) * 16 * (ASYM ? 2 : 4)) + s_col;
+                    P.sw[i][t][s] = *reinterpret_cast<const uint32_t*>(scb[t] + off);
+                }
+                P.w[i][t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(
+                    qwb[t] + static_cast<uint32_t>(kt * kW4TileBytes + lane * 16)));
+            }
+        }
+    };
+
+    // 1. activation loads first, then the first pass's weights: the wait
+    //    for the activations then covers nothing behind them
+    const int span = S * NPW;  // tiles per pass over the workgroup
+    const int rc = Kp >> 3;    // 8-element chunks per padded row
+    const int chunks = Ml * rc;
+    const char* A = static_cast<const char*>(p.A) + z * p.a_bs * (F32A ? 4 : 2);
+    constexpr int B = 4;  // chunks per thread per staging batch
+    u32x4_t av[B], av2[B];
+    auto stage_load = [&](int c0) {
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const int c = c0 + b * 64 * S;
+            const int r = c / rc, k = (c - r * rc) * 8;
+            const bool ok = c < chunks && k < p.K;
+            const int64_t e = ok ? static_cast<int64_t>(r) * p.K + k : 0;  // element 0 always exists
+            if constexpr (F32A) {
+                av[b] = *reinterpret_cast<const u32x4_t*>(A + e * 4);
+                av2[b] = *reinterpret_cast<const u32x4_t*>(A + e * 4 + 16);
+            } else {
+                av[b] = *reinterpret_cast<const u32x4_t*>(A + e * 2);
+            }
+        }
+    };
+    auto stage_store = [&](int c0) {
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const int c = c0 + b * 64 * S;
+            const int r = c / rc, k = (c - r * rc) * 8;
+            const bool ok = c < chunks && k < p.K;
+            if (c < chunks) {
+                const u32x4_t zero = {0, 0, 0, 0};
+                if constexpr (F32A) {
+                    const u32x4_t x0 = ok ? av[b] : zero, x1 = ok ? av2[b] : zero;
+                    const float f[8] = {__uint_as_float(x0[0]), __uint_as_float(x0[1]),
+                                        __uint_as_float(x0[2]), __uint_as_float(x0[3]),
+                                        __uint_as_float(x1[0]), __uint_as_float(x1[1]),
+                                        __uint_as_float(x1[2]), __uint_as_float(x1[3])};
+                    u32x4_t hi, lo;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint16_t h0 = f32_to_bf16(f[2 * i]), h1 = f32_to_bf16(f[2 * i + 1]);
+                        hi[i] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
+                        lo[i] = pack_bf16x2(f[2 * i] - bf16_to_f32(h0), f[2 * i + 1] - bf16_to_f32(h1));
+                    }
+                    *reinterpret_cast<u32x4_t*>(a_lds + static_cast<uint32_t>(c) * 8) = hi;
+                    *reinterpret_cast<u32x4_t*>(a_lds + static_cast<uint32_t>(Ml * Kp + c * 8)) = lo;
+                } else {
+                    *reinterpret_cast<u32x4_t*>(a_lds + static_cast<uint32_t>(c) * 8) = ok ? av[b] : zero;
+                }
+            }
+        }
+    };
+    const int kb0 = wave * NPW;
+    stage_load(threadIdx.x);
+    Pass pa, pb;
+    issue(pa, kb0);
+    stage_store(threadIdx.x);
+    // activations beyond the first batch (large M*K): staged after the
+    // first pass's loads are out
+    for (int c0 = threadIdx.x + B * 64 * S; c0 < chunks; c0 += B * 64 * S) {
+        stage_load(c0);
+        stage_store(c0);
+    }
+    __syncthreads();
+
+    // rows >= M read row M-1 (their outputs are discarded), so every LDS
+    // read stays inside the staged rows
+    const uint16_t* arow = a_lds + static_cast<uint32_t>(min(col, Ml - 1) * Kp + 8 * (lane >> 4));
+    const u32x4_t ones = {kOnesBf16x2, kOnesBf16x2, kOnesBf16x2, kOnesBf16x2};
+    f32x4_t acc[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    auto consume = [&](const Pass& P, int kb) {
+        const int n = min(NPW, p.Kt - kb);
+#pragma unroll
+        for (int i = 0; i < NPW; ++i) {
+            if (i < n) {
+                const int kt = kb + i;
+                u32x4_t ah[4], al[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    ah[j] = *reinterpret_cast<const u32x4_t*>(arow + kt * kW4TileK + 32 * j);
+                    if constexpr (F32A)
+                        al[j] = *reinterpret_cast<const u32x4_t*>(arow + Ml * Kp + kt * kW4TileK + 32 * j);
+                }
+#pragma unroll
+                for (int s = 0; s < SEGS; ++s) {
+                    f32x4_t xs = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int jj = 0; jj < BPS; ++jj) {
+                        xs = mfma_bf16_16x16x32(ah[s * BPS + jj], ones, xs);
+                        if constexpr (F32A) xs = mfma_bf16_16x16x32(al[s * BPS + jj], ones, xs);
+                    }
+                    const int g = group_of_c<BPS, GBIG>(kt, s, p.gmul);
+#pragma unroll
+                    for (int t = 0; t < T; ++t) {
+                        f32x4_t tt = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                        for (int jj = 0; jj < BPS; ++jj) {
+                            const int j = s * BPS + jj;
+                            const u32x4_t b = w4_operand(P.w[i][t][j]);
+                            tt = mfma_bf16_16x16x32(ah[j], b, tt);
+                            if constexpr (F32A) tt = mfma_bf16_16x16x32(al[j], b, tt);
+                        }
+                        float sc, zc;
+                        if constexpr (ASYM) {
+                            sc = f16_to_f32(static_cast<uint16_t>(P.sw[i][t][s] >> s_half));
+                            const uint32_t word = P.zw[(BPS < 4) ? (i * SEGS + s) / 8 : (GBIG ? i : 0)][t];
+                            zc = kW4Bias + static_cast<float>((word >> (4 * (g & 7))) & 15u);
+                        } else {
+                            sc = __uint_as_float(P.sw[i][t][s]);
+                            zc = kW4Bias + 8.0f;  // implied zero point 8
+                        }
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            acc[t][r] = __builtin_fmaf(sc, __builtin_fmaf(-zc, xs[r], tt[r]), acc[t][r]);
+                    }
+                }
+            }
+        }
+    };
+    // passes of this wave: kb0 + q*span for q < np.  Pairs of passes run
+    // with the loads of the next pass issued before the current one is
+    // consumed; every issue is unconditional within its block, so each wait
+    // the compiler places covers exactly the pass being consumed.
+    const int np = (p.Kt - kb0 + span - 1) / span;
+    int q = 0;
+    for (; q + 2 < np; q += 2) {
+        issue(pb, kb0 + (q + 1) * span);
+        consume(pa, kb0 + q * span);
+        issue(pa, kb0 + (q + 2) * span);
+        consume(pb, kb0 + (q + 1) * span);
+    }
+    if (q + 1 < np) {
+        issue(pb, kb0 + (q + 1) * span);
+        consume(pa, kb0 + q * span);
+        consume(pb, kb0 + (q + 1) * span);
+    } else {
+        consume(pa, kb0 + q * span);
+    }
+
+    auto store = [&](int t, int r_in, int ln, float v) {
+        const int r = 4 * (ln >> 4) + r_in;
+        const int ntt = static_cast<int>(blockIdx.x) * T + t;
+        const int c = ntt * kW4TileN + (ln & 15);
+        if (r >= p.M || c >= p.N || ntt >= p.Nt) return;
+        w4_store<F32C>(p, z * p.c_bs + static_cast<int64_t>(r) * p.N + c, v);
+    };
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) red[wave][t][r][lane] = acc[t][r];
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < T * 4 * 64; idx += 64 * S) {
+        const int t = idx >> 8, r = (idx >> 6) & 3, ln = idx & 63;
+        float sum = 0.0f;
+        for (int w2 = 0; w2 < S; ++w2) sum += red[w2][t][r][ln];
+        store(t, r, ln, sum);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Launch selection
+// ---------------------------------------------------------------------------
+
+constexpr int kDecodeMaxLds = 64 * 1024;  // activation bytes a decode workgroup may stage
+
+// Tuning knobs (read once; unset = heuristic):
+//   LHQ_W4_DECODE=-1 disables the decode kernel;
+//   LHQ_W4_DEC_T (1|2), LHQ_W4_DEC_NPW (4|8 tiles per wave per pass) and
+//   LHQ_W4_DEC_S (waves per workgroup, 1..16) shape it;
+//   LHQ_W4_TILES (1|2), LHQ_W4_WAVES (1|2|4|8) shape the generic kernel.
 int env_int(const char* name) {
     const char* v = std::getenv(name);
     return v ? std::atoi(v) : 0;
 }
 
+template <bool F32A, bool ASYM, bool F32C, int T, int NPW>
+void launch_decode_bps(const W4Args& a, dim3 grid, int S, int bps, size_t lds, hipStream_t s) {
+    switch (bps) {
+        case 1: w4_decode_kernel<F32A, ASYM, F32C, T, NPW, 1, false><<<grid, 64 * S, lds, s>>>(a); break;
+        case 2: w4_decode_kernel<F32A, ASYM, F32C, T, NPW, 2, false><<<grid, 64 * S, lds, s>>>(a); break;
+        default:
+            if (a.gmul) w4_decode_kernel<F32A, ASYM, F32C, T, NPW, 4, true><<<grid, 64 * S, lds, s>>>(a);
+            else w4_decode_kernel<F32A, ASYM, F32C, T, NPW, 4, false><<<grid, 64 * S, lds, s>>>(a);
+            break;
+    }
+}
+
 template <bool F32A, bool ASYM, bool F32C, int T, int WAVES, bool GR>
-void launch_bps(const W4Args& a, dim3 grid, int bps, hipStream_t s) {
+void launch_gemv_bps(const W4Args& a, dim3 grid, int bps, hipStream_t s) {
     switch (bps) {
         case 1: w4_gemv_kernel<F32A, ASYM, F32C, T, WAVES, 1, GR><<<grid, 64 * WAVES, 0, s>>>(a); break;
         case 2: w4_gemv_kernel<F32A, ASYM, F32C, T, WAVES, 2, GR><<<grid, 64 * WAVES, 0, s>>>(a); break;
@@ -232,13 +541,56 @@ void launch_bps(const W4Args& a, dim3 grid, int bps, hipStream_t s) {
     }
 }
 
+template <bool F32A, bool ASYM, bool F32C, int T, bool GR>
+void launch_gemv_waves(const W4Args& a, dim3 grid, int W, int bps, hipStream_t s) {
+    switch (W) {
+        case 1: launch_gemv_bps<F32A, ASYM, F32C, T, 1, GR>(a, grid, bps, s); break;
+        case 2: launch_gemv_bps<F32A, ASYM, F32C, T, 2, GR>(a, grid, bps, s); break;
+        case 4: launch_gemv_bps<F32A, ASYM, F32C, T, 4, GR>(a, grid, bps, s); break;
+        default: launch_gemv_bps<F32A, ASYM, F32C, T, 8, GR>(a, grid, bps, s); break;
+    }
+}
+
 // mblocks: 16-row blocks along grid.y (for a grouped launch, an upper bound
 // on the sum over groups of ceil(rows_e / 16)).
 template <bool F32A, bool ASYM, bool F32C, bool GR = false>
-int launch_w4_gemv(W4Args a, int batch, hipStream_t s, int mblocks = -1) {
+int launch_w4(W4Args a, int batch, hipStream_t s, int mblocks = -1) {
+    static const int env_dec = env_int("LHQ_W4_DECODE");
+    static const int env_dt = env_int("LHQ_W4_DEC_T");
+    static const int env_ds = env_int("LHQ_W4_DEC_S");
+    static const int env_np = env_int("LHQ_W4_DEC_NPW");
     static const int env_t = env_int("LHQ_W4_TILES");
     static const int env_w = env_int("LHQ_W4_WAVES");
     if (mblocks < 0) mblocks = ceil_div(a.M, 16);
+    const int bps = a.G >= 128 ? 4 : a.G / 32;
+
+    const size_t dec_lds = static_cast<size_t>(min(a.M, 16)) * a.Kt * kW4TileK * (F32A ? 4 : 2);
+    if (!GR && mblocks == 1 && env_dec >= 0 && dec_lds <= static_cast<size_t>(kDecodeMaxLds)) {
+        // Measured on MI355X at K=8192, N=28672: two column tiles per wave
+        // when there are many, four K tiles per wave per pass, four waves per
+        // workgroup; small launches split K over more waves so the grid still
+        // holds ~8 waves per CU.
+        int T = (a.Nt >= 1024) ? 2 : 1;
+        if (env_dt == 1 || env_dt == 2) T = env_dt;
+        int npw = 4;
+        if (env_np == 4 || env_np == 8) npw = env_np;
+        const int smax = (T == 1) ? 16 : 8;  // the kernel's launch bounds
+        const int64_t cols = static_cast<int64_t>(ceil_div(a.Nt, T)) * batch;
+        int S = 4;
+        while (S < smax && cols * S < 2048) S *= 2;
+        S = max(1, min(S, ceil_div(a.Kt, npw)));
+        if (env_ds >= 1 && env_ds <= smax) S = env_ds;
+        dim3 grid(ceil_div(a.Nt, T), 1, batch);
+        if (T == 1) {
+            if (npw == 4) launch_decode_bps<F32A, ASYM, F32C, 1, 4>(a, grid, S, bps, dec_lds, s);
+            else launch_decode_bps<F32A, ASYM, F32C, 1, 8>(a, grid, S, bps, dec_lds, s);
+        } else {
+            if (npw == 4) launch_decode_bps<F32A, ASYM, F32C, 2, 4>(a, grid, S, bps, dec_lds, s);
+            else launch_decode_bps<F32A, ASYM, F32C, 2, 8>(a, grid, S, bps, dec_lds, s);
+        }
+        return check_launch("w4a16 decode");
+    }
+
     int T = (a.Nt >= 1024) ? 2 : 1;
     if (env_t == 1 || env_t == 2) T = env_t;
     // Enough waves to cover 256 CUs several times over, but at least four
@@ -246,18 +598,10 @@ int launch_w4_gemv(W4Args a, int batch, hipStream_t s, int mblocks = -1) {
     const int64_t wgs = static_cast<int64_t>(ceil_div(a.Nt, T)) * mblocks * batch;
     int W = 2;
     while (W < 8 && wgs * W < 4096 && a.Kt / (2 * W) >= 4) W *= 2;
-    if (env_w == 2 || env_w == 4 || env_w == 8) W = env_w;
-    const int bps = a.G >= 128 ? 4 : a.G / 32;
+    if (env_w == 1 || env_w == 2 || env_w == 4 || env_w == 8) W = env_w;
     dim3 grid(ceil_div(a.Nt, T), mblocks, batch);
-    if (T == 1) {
-        if (W == 2) launch_bps<F32A, ASYM, F32C, 1, 2, GR>(a, grid, bps, s);
-        else if (W == 4) launch_bps<F32A, ASYM, F32C, 1, 4, GR>(a, grid, bps, s);
-        else launch_bps<F32A, ASYM, F32C, 1, 8, GR>(a, grid, bps, s);
-    } else {
-        if (W == 2) launch_bps<F32A, ASYM, F32C, 2, 2, GR>(a, grid, bps, s);
-        else if (W == 4) launch_bps<F32A, ASYM, F32C, 2, 4, GR>(a, grid, bps, s);
-        else launch_bps<F32A, ASYM, F32C, 2, 8, GR>(a, grid, bps, s);
-    }
+    if (T == 1) launch_gemv_waves<F32A, ASYM, F32C, 1, GR>(a, grid, W, bps, s);
+    else launch_gemv_waves<F32A, ASYM, F32C, 2, GR>(a, grid, W, bps, s);
     return check_launch("w4a16 gemv");
 }
 
@@ -278,6 +622,9 @@ W4Args make_args(const void* A, const uint8_t* qw, const void* sc, const uint32_
     a.M = M; a.N = N; a.K = K; a.G = G;
     a.Nt = ceil_div(N, kW4TileN); a.Kt = ceil_div(K, kW4TileK);
     a.NG = K / G; a.NG8 = ceil_div(a.NG, 8);
+    // G > 128 is a multiple of 128 (check_w4_shape): tile kt is in group
+    // kt / (G/128), computed as __umulhi(kt, ceil(2^32 / (G/128)))
+    a.gmul = (G > kW4TileK) ? static_cast<uint32_t>(((1ull << 32) + G / kW4TileK - 1) / (G / kW4TileK)) : 0u;
     a.alpha = alpha; a.beta = beta;
     return a;
 }
@@ -295,7 +642,7 @@ int lhq_gemm_w4a16(const float* A, const uint8_t* qweight, const float* scales, 
     LHQ_REQUIRE(qweight && scales && C && (A || M == 0), "gemm_w4a16: null pointer");
     if (M == 0) return LHQ_OK;
     W4Args a = make_args(A, qweight, scales, nullptr, C, M, N, K, G, alpha, beta);
-    return launch_w4_gemv<true, false, true>(a, 1, as_stream(stream));
+    return launch_w4<true, false, true>(a, 1, as_stream(stream));
 }
 
 int lhq_gemm_w4a16_bf16(const uint16_t* A, const uint8_t* qweight, const uint16_t* scales,
@@ -305,7 +652,7 @@ int lhq_gemm_w4a16_bf16(const uint16_t* A, const uint8_t* qweight, const uint16_
     LHQ_REQUIRE(qweight && scales && zeros && C && (A || M == 0), "gemm_w4a16_bf16: null pointer");
     if (M == 0) return LHQ_OK;
     W4Args a = make_args(A, qweight, scales, zeros, C, M, N, K, G, 1.0f, 0.0f);
-    return launch_w4_gemv<false, true, false>(a, 1, as_stream(stream));
+    return launch_w4<false, true, false>(a, 1, as_stream(stream));
 }
 
 int lhq_gemm_w4a16_bf16_batched(const uint16_t* A, const uint8_t* qweight, const uint16_t* scales,
@@ -321,7 +668,7 @@ int lhq_gemm_w4a16_bf16_batched(const uint16_t* A, const uint8_t* qweight, const
     a.qw_bs = lhq_w4_qweight_bytes(K, N);
     a.s_bs = static_cast<int64_t>(a.Nt) * a.NG * 16;
     a.z_bs = static_cast<int64_t>(a.Nt) * a.NG8 * 16;
-    return launch_w4_gemv<false, true, false>(a, batch, as_stream(stream));
+    return launch_w4<false, true, false>(a, batch, as_stream(stream));
 }
 
 int lhq_gemm_w4a16_bf16_grouped(const uint16_t* A, const int32_t* offsets, const uint8_t* const* qweights,
@@ -343,7 +690,7 @@ int lhq_gemm_w4a16_bf16_grouped(const uint16_t* A, const int32_t* offsets, const
     const int64_t mblocks = ceil_div64(row_capacity, 16) + num_groups;
     LHQ_SUPPORTED(mblocks <= 65535, "gemm_w4a16_bf16_grouped: %lld row blocks exceed the grid limit",
                   static_cast<long long>(mblocks));
-    return launch_w4_gemv<false, true, false, true>(a, 1, as_stream(stream), static_cast<int>(mblocks));
+    return launch_w4<false, true, false, true>(a, 1, as_stream(stream), static_cast<int>(mblocks));
 }
 
 }  // extern "C"

@@ -45,6 +45,9 @@ def _sym_case(oracle, ops, M, K, N, G, seed, alpha=1.0, beta=0.0):
     (17, 512, 100, 32),
     (40, 1024, 272, 256),
     (1, 8192, 28672, 128),   # decode target shape, fp32 API
+    (2, 96, 40, 32),         # K not a multiple of the 128-wide tile
+    (7, 4160, 72, 64),
+    (16, 28672, 64, 128),    # activations too large to stage: generic kernel
 ])
 def test_w4a16_f32_matches_oracle(oracle, ops, M, K, N, G):
     got, want = _sym_case(oracle, ops, M, K, N, G, seed=100 + M + K // 64)
@@ -104,6 +107,13 @@ def test_w4a16_bf16_matches_oracle(oracle, ops, M, K, N):
 @pytest.mark.parametrize("G", [32, 64, 256])
 def test_w4a16_bf16_group_sizes(oracle, ops, G):
     got, want = _asym_case(oracle, ops, 3, 1024, 96, G, seed=G)
+    assert rel_frobenius(got, want) <= TOL_BF16
+
+
+@pytest.mark.parametrize("M,K,N,G", [(1, 96, 48, 32), (16, 320, 64, 64), (9, 4160, 136, 64)])
+def test_w4a16_bf16_ragged_k(oracle, ops, M, K, N, G):
+    """K not a multiple of 128: the padded tail of the last tile must add nothing."""
+    got, want = _asym_case(oracle, ops, M, K, N, G, seed=K + M)
     assert rel_frobenius(got, want) <= TOL_BF16
 
 
