@@ -72,3 +72,38 @@ def test_empty_problems_are_noops(L):
     assert L.status("lhq_gemm_w4a16_bf16", None, FAKE, FAKE, FAKE, FAKE, 0, 64, 128, 128, None) == 0
     assert L.status("lhq_gemm_w8a8_i32", None, FAKE, FAKE, 0, 16, 16, None) == 0
     assert L.status("lhq_q8_quantize_per_row", FAKE, FAKE, FAKE, 0, 16, None) == 0
+
+
+def test_dropin_exports_reference_interface():
+    """liblonghorn_kernels.so defines every lh:: function of the reference's
+    kernel headers (quant.hpp:31-94, gemm_quant.hpp:42-70, gemm.hpp:14-29),
+    with the reference's parameter types."""
+    import subprocess
+    from longhornai_amd import KERNELS_LIB
+    out = subprocess.run(["nm", "-D", "-C", "--defined-only", KERNELS_LIB], capture_output=True, text=True,
+                         check=True).stdout
+    want = [
+        "lh::q8_quantize_per_tensor(float const*, signed char*, float*, long)",
+        "lh::q8_dequantize_per_tensor(signed char const*, float, float*, long)",
+        "lh::q8_quantize_per_row(float const*, signed char*, float*, int, int)",
+        "lh::q8_dequantize_per_row(signed char const*, float const*, float*, int, int)",
+        "lh::q8_quantize_per_col(float const*, signed char*, float*, int, int)",
+        "lh::q8_dequantize_per_col(signed char const*, float const*, float*, int, int)",
+        "lh::q4_quantize_groupwise(float const*, unsigned char*, float*, int, int, int)",
+        "lh::q4_dequantize_groupwise(unsigned char const*, float const*, float*, int, int, int)",
+        "lh::fp8_quantize_per_tensor(float const*, lh::fp8_e4m3*, float*, long)",
+        "lh::fp8_dequantize_per_tensor(lh::fp8_e4m3 const*, float, float*, long)",
+        "lh::fp8_quantize_per_row(float const*, lh::fp8_e4m3*, float*, int, int)",
+        "lh::fp8_dequantize_per_row(lh::fp8_e4m3 const*, float const*, float*, int, int)",
+        "lh::fp8_quantize_per_col(float const*, lh::fp8_e4m3*, float*, int, int)",
+        "lh::fp8_dequantize_per_col(lh::fp8_e4m3 const*, float const*, float*, int, int)",
+        "lh::gemm_w8a8(signed char const*, signed char const*, float const*, float const*, float*, int, int, int, float, float)",
+        "lh::gemm_w4a16_groupwise(float const*, unsigned char const*, float const*, float*, int, int, int, int, float, float)",
+        "lh::gemm_fp8_e4m3(lh::fp8_e4m3 const*, lh::fp8_e4m3 const*, float, float, float*, int, int, int, float, float)",
+        "lh::gemm_ref(float const*, float const*, float*, int, int, int, float, float)",
+        "lh::gemm(float const*, float const*, float*, int, int, int, float, float)",
+        "lh::gemm_batched(float const*, float const*, float*, int, int, int, int, float, float)",
+        "lh::gemm_grouped(float const* const*, float const* const*, float* const*, int const*, int const*, int const*, int, float, float)",
+    ]
+    missing = [w for w in want if w not in out]
+    assert not missing, missing
