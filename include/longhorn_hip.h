@@ -178,6 +178,13 @@ int lhq_gemm_f32_ref(const float* A, const float* B, float* C, int M, int N, int
 int lhq_gemm_f32_batched(const float* A, const float* B, float* C, int batch, int M,
                          int N, int K, float alpha, float beta, void* stream);
 
+/* ---- diagnostics (no counterpart in the reference) ----------------------- */
+/* Converts all 2^32 fp32 bit patterns to bf16 with the instruction the
+ * kernels use (v_cvt_pk_bf16_f32) and counts results that differ from the
+ * reference's rule (dtypes.hpp:87-98).  counts: 2 device uint64, set to
+ * {non-NaN mismatches, NaN mismatches}; both are 0 on a conforming device. */
+int lhq_selftest_bf16(unsigned long long* counts, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

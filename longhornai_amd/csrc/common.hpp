@@ -56,18 +56,24 @@ __device__ __forceinline__ f32x4_t mfma_fp8_16x16x32(u32x2_t a, u32x2_t b, f32x4
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
     return __uint_as_float(static_cast<uint32_t>(b) << 16);
 }
-// RNE on the dropped 16 bits; NaN keeps its payload with the quiet bit set
-// (dtypes.hpp:87-98).
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-    uint32_t x = __float_as_uint(f);
-    if ((x & 0x7f800000u) == 0x7f800000u && (x & 0x7fffffu))
-        return static_cast<uint16_t>((x >> 16) | 0x40u);
-    x += 0x7fffu + ((x >> 16) & 1u);
-    return static_cast<uint16_t>(x >> 16);
+// The reference's fp32 -> bf16 rule (dtypes.hpp:87-98): round to nearest
+// even on the dropped 16 bits; NaN keeps its payload with the quiet bit set.
+__device__ __forceinline__ uint32_t bf16_rule(uint32_t x) {
+    const uint32_t rounded = (x + 0x7fffu + ((x >> 16) & 1u)) >> 16;
+    const uint32_t quiet = (x >> 16) | 0x40u;
+    return ((x & 0x7fffffffu) > 0x7f800000u) ? quiet : rounded;
 }
-// Two fp32 -> packed bf16 pair with the same rounding (low half = a).
+// The same conversion on gfx950's v_cvt_pk_bf16_f32, which gives the rule's
+// result for every one of the 2^32 fp32 inputs (lhq_selftest_bf16 checks
+// this exhaustively on the device): one instruction per pair instead of
+// seven per element.
+typedef float lhq_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 lhq_bf16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-    return static_cast<uint32_t>(f32_to_bf16(a)) | (static_cast<uint32_t>(f32_to_bf16(b)) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(lhq_f32x2{a, b}, lhq_bf16x2));
+}
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 // binary16 -> fp32 (exact for every encoding; dtypes.hpp:57-85).
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {

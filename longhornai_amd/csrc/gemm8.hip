@@ -43,6 +43,7 @@ struct Gemm8Args {
     void* C;
     int M, N, K, Kp;
     int tiles_m, tiles_n, group_m;
+    int c_vec;  // C is 16-byte aligned (vector stores allowed where rows are)
     float alpha, beta;
 };
 
@@ -67,6 +68,300 @@ __device__ __forceinline__ void tile_of(int b, const Gemm8Args& p, int& tm, int&
     tn = in / rows;
 }
 
+// Epilogue shared by the 8-bit kernels: scale, apply beta and store the
+// 256x256 tile.  Element 4q+r of block (i, j) in lane l is C[row][col] with
+// row = m0 + 128*wm + 32*i + (l & 31) and
+// col = n0 + 128*wn + 32*j + 4*(l >> 5) + 8*q + r: four adjacent columns
+// per (i, j, q), stored as one vector.  INTERIOR: the whole tile is in range
+// and rows are 16-byte aligned (N % 4 == 0), so nothing is tested per
+// element; edge tiles test rows and columns.  Offsets are 32-bit from the
+// tile's first element (the launcher bounds 256*N).  LS: the int8 scales
+// of this tile are staged in LDS at ls (ls[r] = A_s[m0 + r],
+// ls[256 + c] = B_s[n0 + c], clamped to the last row / column).
+template <int OP, int EPI, bool INTERIOR, bool LS, typename Acc>
+__device__ __forceinline__ void gemm8_store(const Gemm8Args& p, const Acc (&acc)[4][4], int m0, int n0, int wm,
+                                            int wn, int lane, const float* ls) {
+    const int lr = lane & 31, lh = lane >> 5;
+    const bool vec_ok = INTERIOR || (p.c_vec && (p.N & 3) == 0);
+    float row_scale[4];     // int8: alpha * A_s[row] (gemm_quant.cpp:44-45)
+    float combined = 0.0f;  // fp8: (alpha * sA) * sB (gemm_quant.cpp:98)
+    if constexpr (EPI != EPI_I32) {
+        if constexpr (OP == OP_I8) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int rt = wm * 128 + i * 32 + lr;
+                const int row = m0 + rt;
+                row_scale[i] = p.alpha * (LS ? ls[rt] : p.As[INTERIOR ? row : min(row, p.M - 1)]);
+            }
+        } else {
+            combined = p.alpha * p.As[0];
+            combined = combined * p.Bs[0];
+        }
+    }
+    const size_t tile_off = static_cast<size_t>(m0) * p.N + n0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int cb = wn * 128 + j * 32 + 4 * lh;  // column within the tile
+        float bs[4][4];
+        if constexpr (OP == OP_I8 && EPI != EPI_I32) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                if constexpr (LS) {
+                    // cb + 8q is a multiple of 4: one 16-byte LDS read
+                    const f32x4_t v = *reinterpret_cast<const f32x4_t*>(ls + BM + cb + 8 * q);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) bs[q][r] = v[r];
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int col = n0 + cb + 8 * q + r;
+                        bs[q][r] = p.Bs[INTERIOR ? col : min(col, p.N - 1)];
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int rt = wm * 128 + i * 32 + lr;  // row within the tile
+            if (!INTERIOR && m0 + rt >= p.M) continue;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int ct = cb + 8 * q;
+                const int col = n0 + ct;
+                if (!INTERIOR && col >= p.N) continue;
+                const uint32_t o = static_cast<uint32_t>(rt) * static_cast<uint32_t>(p.N) + static_cast<uint32_t>(ct);
+                const bool full = INTERIOR || (vec_ok && col + 3 < p.N);
+                if constexpr (EPI == EPI_I32) {
+                    const i32x4_t v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                    int32_t* Cp = static_cast<int32_t*>(p.C) + tile_off + o;
+                    if (full) {
+                        *reinterpret_cast<i32x4_t*>(Cp) = v;
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            if (col + r < p.N) Cp[r] = v[r];
+                    }
+                } else {
+                    float f[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        if constexpr (OP == OP_I8) {
+                            f[r] = row_scale[i] * bs[q][r];  // left to right, as the reference
+                            f[r] = f[r] * static_cast<float>(acc[i][j][4 * q + r]);
+                        } else {
+                            f[r] = combined * acc[i][j][4 * q + r];
+                        }
+                    }
+                    if constexpr (EPI == EPI_F32) {
+                        // apply_beta (gemm_quant.cpp:12-21), then C += rescaled
+                        float* Cp = static_cast<float*>(p.C) + tile_off + o;
+                        if (full) {
+                            f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+                            if (p.beta != 0.0f) c = *reinterpret_cast<const f32x4_t*>(Cp);
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                const float base = (p.beta == 0.0f) ? 0.0f : (p.beta == 1.0f) ? c[r] : c[r] * p.beta;
+                                c[r] = base + f[r];
+                            }
+                            *reinterpret_cast<f32x4_t*>(Cp) = c;
+                        } else {
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                if (col + r >= p.N) continue;
+                                const float base = (p.beta == 0.0f) ? 0.0f : (p.beta == 1.0f) ? Cp[r] : Cp[r] * p.beta;
+                                Cp[r] = base + f[r];
+                            }
+                        }
+                    } else {
+                        // bf16 output of C = 0 + rescaled (beta = 0)
+                        uint16_t* Cp = static_cast<uint16_t*>(p.C) + tile_off + o;
+                        const uint32_t lo = pack_bf16x2(0.0f + f[0], 0.0f + f[1]);
+                        const uint32_t hi = pack_bf16x2(0.0f + f[2], 0.0f + f[3]);
+                        if (full) {
+                            *reinterpret_cast<u32x2_t*>(Cp) = u32x2_t{lo, hi};
+                        } else {
+                            const uint16_t h[4] = {static_cast<uint16_t>(lo), static_cast<uint16_t>(lo >> 16),
+                                                   static_cast<uint16_t>(hi), static_cast<uint16_t>(hi >> 16)};
+#pragma unroll
+                            for (int r = 0; r < 4; ++r)
+                                if (col + r < p.N) Cp[r] = h[r];
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+// Interior-tile epilogue of the int8 DMA kernel, through LDS.  Per 32-row
+// block i of the wave's 128x128 quadrant:
+//   1. the raw int32 accumulators go to the wave's LDS area, row-major
+//      (straight from the accumulator registers, no VALU work);
+//   2. the wave reads them back along rows, CPL consecutive columns per lane
+//      (8 for bf16 output, 4 otherwise), scales them and stores 16 bytes per
+//      lane: bf16 4 rows x 256 B, fp32 / int32 2 rows x 512 B per store.
+// In that layout a lane owns the same columns for every row, so it keeps
+// just CPL column scales in registers and reads one (broadcast) row scale
+// per row.  Scaling is the reference's ((alpha*A_s[r]) * B_s[c]) * acc
+// (gemm_quant.cpp:44-46); with beta = 0 the "0 + x" of apply_beta is folded
+// into the last multiply as fma(s, acc, +0), which is exact: for a nonzero
+// product no rounding to zero can occur (|acc| >= 1 and a nonzero fp32 s is
+// >= 2^-149), and an exactly zero product gives +0 either way (-0 + +0 =
+// +0).  area: this wave's 32 rows of 128 int32 plus a 4-word pad per row
+// (row starts 4 banks apart).  ls: the tile's scales in LDS (A_s, then B_s;
+// clamped to the last row / column).  EDGE: the tile crosses M or N (or
+// rows are not 16-byte aligned); rows and columns are tested and partial
+// column groups stored element by element.
+constexpr int STAGED_PITCH = 4 * (128 + 4);
+
+template <int EPI, bool EDGE>
+__device__ __forceinline__ void gemm8_store_staged(const Gemm8Args& p, const i32x16_t (&acc)[4][4], int m0, int n0,
+                                                   int wm, int wn, int lane, const float* ls, uint8_t* area) {
+    constexpr int CPL = EPI == EPI_BF16 ? 8 : 4;  // columns per lane (16 output bytes)
+    constexpr int LPR = 128 / CPL;                // lanes per row: 16 or 32
+    constexpr int RPP = 64 / LPR;                 // rows per pass: 4 or 2
+    const int lr = lane & 31, lh = lane >> 5;
+    const int rsub = lane / LPR, cl = lane % LPR;
+    float bsc[CPL];  // B_s of the lane's columns
+    if constexpr (EPI != EPI_I32) {
+#pragma unroll
+        for (int c = 0; c < CPL; c += 4) {
+            const f32x4_t v = *reinterpret_cast<const f32x4_t*>(ls + BM + wn * 128 + cl * CPL + c);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) bsc[c + r] = v[r];
+        }
+    }
+    // this wave's quadrant of C, 32-bit element offsets from its first element
+    const size_t quad_off = static_cast<size_t>(m0 + wm * 128) * p.N + n0 + wn * 128;
+    const bool beta0 = p.beta == 0.0f;
+    const int cols_left = p.N - (n0 + wn * 128 + cl * CPL);  // in-range columns from the lane's first
+    const bool vec_ok = !EDGE || (p.c_vec && cols_left >= CPL && p.N % CPL == 0);
+    // 1. raw accumulators of block i, row lr, columns 32j + 4lh + 8q ..+3
+    auto stage_block = [&](int i) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                *reinterpret_cast<i32x4_t*>(area + lr * STAGED_PITCH + (j * 32 + 4 * lh + 8 * q) * 4) =
+                    i32x4_t{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+    };
+    auto wave_sync = [&]() {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    stage_block(0);
+    wave_sync();  // the wave reads back what its other lanes wrote
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        // 2. along rows: every LDS read of the block first (data and row
+        // scales, 64 + 8..16 registers), then the passes that scale and store
+        constexpr int PASSES = 32 / RPP;
+        int32_t ab[PASSES][CPL];
+        float rsb[PASSES];
+#pragma unroll
+        for (int t = 0; t < PASSES; ++t) {
+            const int R = t * RPP + rsub;
+            const uint8_t* src = area + R * STAGED_PITCH + cl * CPL * 4;
+#pragma unroll
+            for (int c = 0; c < CPL; c += 4) {
+                const i32x4_t v = *reinterpret_cast<const i32x4_t*>(src + c * 4);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) ab[t][c + r] = v[r];
+            }
+            if constexpr (EPI != EPI_I32) rsb[t] = ls[wm * 128 + i * 32 + R];
+        }
+        // block i + 1 goes to LDS while block i is scaled and stored: a
+        // wave's LDS operations execute in order, so these writes land after
+        // the reads above
+        __builtin_amdgcn_sched_barrier(0);
+        if (i + 1 < 4) stage_block(i + 1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < PASSES; ++t) {
+            const int R = t * RPP + rsub;                  // row within the block
+            const int rq = i * 32 + R;                     // row within the quadrant
+            if (EDGE && (m0 + wm * 128 + rq >= p.M || cols_left <= 0)) continue;
+            const int32_t (&a)[CPL] = ab[t];
+            const uint32_t o = static_cast<uint32_t>(rq) * static_cast<uint32_t>(p.N) + static_cast<uint32_t>(cl * CPL);
+            if constexpr (EPI == EPI_I32) {
+                int32_t* Cp = static_cast<int32_t*>(p.C) + quad_off + o;
+                if (vec_ok) {
+                    *reinterpret_cast<i32x4_t*>(Cp) = i32x4_t{a[0], a[1], a[2], a[3]};
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c)
+                        if (c < cols_left) Cp[c] = a[c];
+                }
+            } else {
+                const float rs = p.alpha * rsb[t];  // gemm_quant.cpp:44-45
+                float f[CPL];
+                if constexpr (EPI == EPI_BF16) {
+                    // C = 0 + rescaled, rounded to bf16
+#pragma unroll
+                    for (int c = 0; c < CPL; ++c) f[c] = __builtin_fmaf(rs * bsc[c], static_cast<float>(a[c]), 0.0f);
+                    const u32x4_t v = {pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
+                                       pack_bf16x2(f[6], f[7])};
+                    uint16_t* Cp = static_cast<uint16_t*>(p.C) + quad_off + o;
+                    if (vec_ok) {
+                        *reinterpret_cast<u32x4_t*>(Cp) = v;
+                    } else {
+#pragma unroll
+                        for (int c = 0; c < CPL; ++c)
+                            if (c < cols_left) Cp[c] = static_cast<uint16_t>(v[c >> 1] >> (16 * (c & 1)));
+                    }
+                } else {
+                    float* Cp = static_cast<float*>(p.C) + quad_off + o;
+                    f32x4_t c4 = {0.f, 0.f, 0.f, 0.f};
+                    if (!vec_ok) {
+                        // partial group: element by element, same operations
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            if (c >= cols_left) continue;
+                            float x;
+                            if (beta0) {
+                                x = __builtin_fmaf(rs * bsc[c], static_cast<float>(a[c]), 0.0f);
+                            } else {
+                                f[c] = rs * bsc[c];
+                                f[c] = f[c] * static_cast<float>(a[c]);
+                                const float base = (p.beta == 1.0f) ? Cp[c] : Cp[c] * p.beta;
+                                x = base + f[c];
+                            }
+                            Cp[c] = x;
+                        }
+                        continue;
+                    }
+                    if (beta0) {
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) c4[c] = __builtin_fmaf(rs * bsc[c], static_cast<float>(a[c]), 0.0f);
+                    } else {
+                        // apply_beta (gemm_quant.cpp:12-21), then C += rescaled
+                        c4 = *reinterpret_cast<const f32x4_t*>(Cp);
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            f[c] = rs * bsc[c];
+                            f[c] = f[c] * static_cast<float>(a[c]);
+                            const float base = (p.beta == 1.0f) ? c4[c] : c4[c] * p.beta;
+                            c4[c] = base + f[c];
+                        }
+                    }
+                    *reinterpret_cast<f32x4_t*>(Cp) = c4;
+                }
+            }
+        }
+        wave_sync();  // block i + 1 is in LDS for every lane
+    }
+}
+
+template <int OP, int EPI, bool LS = false, typename Acc>
+__device__ __forceinline__ void gemm8_epilogue(const Gemm8Args& p, const Acc (&acc)[4][4], int m0, int n0, int wm,
+                                               int wn, int lane, const float* ls = nullptr) {
+    if (m0 + BM <= p.M && n0 + BN <= p.N && (p.N & 3) == 0 && p.c_vec)
+        gemm8_store<OP, EPI, true, LS>(p, acc, m0, n0, wm, wn, lane, ls);
+    else
+        gemm8_store<OP, EPI, false, LS>(p, acc, m0, n0, wm, wn, lane, ls);
+}
+
 template <int OP, int EPI>
 __global__ __launch_bounds__(NTHREADS) void gemm8_kernel(Gemm8Args p) {
     __shared__ __attribute__((aligned(16))) uint8_t lds[2][2][TILE_BYTES];
@@ -74,31 +369,50 @@ __global__ __launch_bounds__(NTHREADS) void gemm8_kernel(Gemm8Args p) {
     int tm, tn;
     tile_of(blockIdx.x, p, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
 
-    // global -> register staging
-    u32x4_t ra[CHUNKS], rb[CHUNKS];
-    auto load_stage = [&](int k0) {
+    // Global -> register staging.  Every load is unconditional: rows past M
+    // read row M-1 and k past K reads the row's last 16 bytes; both are
+    // replaced by zero codes before they reach LDS (a zero code times the
+    // zero-padded B contributes nothing, and for e4m3 a stray NaN code
+    // could not hide behind a zero weight).  Loads issued on only some
+    // control paths would make every later wait in the loop a full drain.
+    struct Stage {
+        u32x4_t a[CHUNKS], b[CHUNKS];
+        uint32_t a_ok;  // bit i: chunk i of A is in range
+    };
+    const int r_base = tid >> 3, kc = (tid & 7) * 16;
+    // Byte offsets fit in 32 bits (the launcher checks M*K and Np*Kp); the
+    // row parts are loop-invariant, only k advances.
+    uint32_t a_row[CHUNKS], b_row[CHUNKS];
+#pragma unroll
+    for (int i = 0; i < CHUNKS; ++i) {
+        const int r = r_base + (NTHREADS / 8) * i;
+        a_row[i] = static_cast<uint32_t>(min(m0 + r, p.M - 1)) * static_cast<uint32_t>(p.K);
+        b_row[i] = static_cast<uint32_t>(n0 + r) * static_cast<uint32_t>(p.Kp);
+    }
+    const uint32_t m_rows_ok = static_cast<uint32_t>(max(0, min(p.M - m0, BM)));  // rows of this tile in range
+    auto load_stage = [&](Stage& st, int kt) {
+        const int gk = kt * BK + kc;
+        const uint32_t ka = static_cast<uint32_t>(min(gk, p.K - 16));
+        st.a_ok = 0;
 #pragma unroll
         for (int i = 0; i < CHUNKS; ++i) {
-            const int c = tid + NTHREADS * i;
-            const int r = c >> 3, kc = (c & 7) * 16;
-            const int gm = m0 + r, gk = k0 + kc;
-            if (gm < p.M && gk < p.K)
-                ra[i] = *reinterpret_cast<const u32x4_t*>(p.A + static_cast<int64_t>(gm) * p.K + gk);
-            else
-                ra[i] = u32x4_t{0, 0, 0, 0};
-            rb[i] = *reinterpret_cast<const u32x4_t*>(p.Bt + static_cast<int64_t>(n0 + r) * p.Kp + gk);
+            const uint32_t r = static_cast<uint32_t>(r_base + (NTHREADS / 8) * i);
+            st.a_ok |= static_cast<uint32_t>(r < m_rows_ok && gk < p.K) << i;
+            st.a[i] = *reinterpret_cast<const u32x4_t*>(p.A + (a_row[i] + ka));
+            st.b[i] = *reinterpret_cast<const u32x4_t*>(p.Bt + (b_row[i] + static_cast<uint32_t>(gk)));
         }
     };
-    auto store_stage = [&](int buf) {
+    auto store_stage = [&](const Stage& st, int buf) {
+        const u32x4_t zero = {0, 0, 0, 0};
 #pragma unroll
         for (int i = 0; i < CHUNKS; ++i) {
-            const int c = tid + NTHREADS * i;
-            const int r = c >> 3, kc = (c & 7) * 16;
-            *reinterpret_cast<u32x4_t*>(&lds[buf][0][r * LROW + kc]) = ra[i];
-            *reinterpret_cast<u32x4_t*>(&lds[buf][1][r * LROW + kc]) = rb[i];
+            const int r = r_base + (NTHREADS / 8) * i;
+            *reinterpret_cast<u32x4_t*>(&lds[buf][0][r * LROW + kc]) = ((st.a_ok >> i) & 1u) ? st.a[i] : zero;
+            *reinterpret_cast<u32x4_t*>(&lds[buf][1][r * LROW + kc]) = st.b[i];
         }
     };
 
@@ -109,97 +423,267 @@ __global__ __launch_bounds__(NTHREADS) void gemm8_kernel(Gemm8Args p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = Acc{};
 
-    const int nk = p.Kp / BK;
-    load_stage(0);
-    store_stage(0);
-    __syncthreads();
-
     const int a_off = (wm * 128 + (lane & 31)) * LROW + 16 * (lane >> 5);
     const int b_off = (wn * 128 + (lane & 31)) * LROW + 16 * (lane >> 5);
-    for (int kt = 0; kt < nk; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < nk) load_stage((kt + 1) * BK);
+
+    // One 128-deep k tile from LDS buffer `buf`: four 32-deep k steps, the
+    // operand fragments of step kk+1 read while the 16 MFMAs of step kk run.
+    auto compute = [&](int buf) {
         const uint8_t* la = &lds[buf][0][a_off];
         const uint8_t* lb = &lds[buf][1][b_off];
+        u32x4_t fa[2][4], fb[2][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            fa[0][i] = *reinterpret_cast<const u32x4_t*>(la + i * 32 * LROW);
+            fb[0][i] = *reinterpret_cast<const u32x4_t*>(lb + i * 32 * LROW);
+        }
 #pragma unroll
         for (int kk = 0; kk < BK / 32; ++kk) {
-            u32x4_t fa[4], fb[4];
+            const int cur = kk & 1;
+            if (kk + 1 < BK / 32) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                fa[i] = *reinterpret_cast<const u32x4_t*>(la + i * 32 * LROW + kk * 32);
-                fb[i] = *reinterpret_cast<const u32x4_t*>(lb + i * 32 * LROW + kk * 32);
+                for (int i = 0; i < 4; ++i) {
+                    fa[cur ^ 1][i] = *reinterpret_cast<const u32x4_t*>(la + i * 32 * LROW + (kk + 1) * 32);
+                    fb[cur ^ 1][i] = *reinterpret_cast<const u32x4_t*>(lb + i * 32 * LROW + (kk + 1) * 32);
+                }
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
+                    // B^T fragment as the MFMA's row operand, A as its
+                    // column operand: the accumulator is the tile transposed,
+                    // so each lane ends up with four adjacent C columns
                     if constexpr (OP == OP_I8) {
-                        acc[i][j] = mfma_i8_32x32x32(fa[i], fb[j], acc[i][j]);
+                        acc[i][j] = mfma_i8_32x32x32(fb[cur][j], fa[cur][i], acc[i][j]);
                     } else {
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(
-                            __builtin_bit_cast(long, u32x2_t{fa[i][0], fa[i][1]}),
-                            __builtin_bit_cast(long, u32x2_t{fb[j][0], fb[j][1]}), acc[i][j], 0, 0, 0);
+                            __builtin_bit_cast(long, u32x2_t{fb[cur][j][0], fb[cur][j][1]}),
+                            __builtin_bit_cast(long, u32x2_t{fa[cur][i][0], fa[cur][i][1]}), acc[i][j], 0, 0, 0);
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_fp8_fp8(
-                            __builtin_bit_cast(long, u32x2_t{fa[i][2], fa[i][3]}),
-                            __builtin_bit_cast(long, u32x2_t{fb[j][2], fb[j][3]}), acc[i][j], 0, 0, 0);
+                            __builtin_bit_cast(long, u32x2_t{fb[cur][j][2], fb[cur][j][3]}),
+                            __builtin_bit_cast(long, u32x2_t{fa[cur][i][2], fa[cur][i][3]}), acc[i][j], 0, 0, 0);
                     }
                 }
         }
-        if (kt + 1 < nk) store_stage(buf ^ 1);
+    };
+
+    // One k tile in flight in registers while the previous one is consumed
+    // from LDS (a second register stage would not fit beside the 256
+    // accumulator registers).
+    const int nk = p.Kp / BK;
+    Stage st;
+    load_stage(st, 0);
+    store_stage(st, 0);
+    __syncthreads();
+    for (int kt = 0; kt + 1 < nk; ++kt) {
+        const int buf = kt & 1;
+        load_stage(st, kt + 1);
+        compute(buf);
+        store_stage(st, buf ^ 1);
         __syncthreads();
     }
+    compute((nk - 1) & 1);
 
-    // Epilogue.  Lane l of block (i, j) holds rows 8*(e>>2) + 4*(l>>5) + (e&3)
-    // and column l & 31 of that 32x32 block.
-    float combined = 0.0f;
-    if constexpr (OP == OP_FP8) {
-        if constexpr (EPI != EPI_I32) {
-            combined = p.alpha * p.As[0];
-            combined = combined * p.Bs[0];
+    gemm8_epilogue<OP, EPI>(p, acc, m0, n0, wm, wn, lane);
+}
+
+// ---------------------------------------------------------------------------
+// int8 kernel with an LDS-DMA pipeline (W8A8; the default int8 path).
+//
+// Same 256x256 tile, waves and MFMA as gemm8_kernel, but operands move
+// global -> LDS with global_load_lds_dwordx4 (no register staging) through
+// DS_STAGES buffers of 64-byte k steps held in dynamic LDS (32 KiB each).
+// A stage's buffer is refilled, DS_STAGES stages ahead, as soon as every
+// wave has read its fragments into registers, so DS_STAGES - 1 stages are
+// in flight while one is multiplied.  The per-stage rendezvous is an
+// explicit `s_waitcnt vmcnt` on this wave's older DMAs plus `s_barrier` (the
+// fence of __syncthreads would drain every DMA in flight).  Fragments of the
+// next 32-deep k step are read from LDS while the MFMAs of the current one
+// run.  Stages past the last k tile still issue their DMA, re-reading the
+// last tile into a buffer nothing reads again, so every wave always has the
+// same number of DMAs outstanding and the wait counts are constants.  The
+// tile's 256 row and 256 column scales are DMA'd into LDS ahead of the first
+// stage, so the epilogue reads them without a global round trip.
+//
+// LDS layout per buffer and operand: 256 rows x 64 bytes, 16-byte chunk c of
+// row r stored in slot c ^ ((r >> 2) & 3); the 32 rows one MFMA operand
+// read touches then cover every bank once per 16 lanes.
+// Rows past M read row M-1 and k past K reads the row's last 16 bytes: int8
+// codes times the zero-padded B contribute nothing, and those rows are
+// never stored.
+// ---------------------------------------------------------------------------
+constexpr int DS_BK = 64;                     // k bytes per stage
+constexpr int DS_STAGES = 4;                  // LDS buffers (default)
+constexpr int DS_OP_BYTES = BM * DS_BK;       // one operand of one stage (16 KiB)
+constexpr int DS_DMA_PER_STAGE = 2 * DS_OP_BYTES / 1024 / 4;  // per wave (8)
+constexpr int DS_SCALE_BYTES = (BM + BN) * 4;                 // int8 scales of one tile
+
+#define LHQ_LDS_AS __attribute__((address_space(3)))
+
+template <int EPI, int STAGES>
+__global__ __launch_bounds__(NTHREADS) void gemm8_dma_kernel(Gemm8Args p) {
+    static_assert(STAGES >= 3 && DS_DMA_PER_STAGE * (STAGES - 2) <= 63, "vmcnt range");
+    static_assert(STAGES * 2 * DS_OP_BYTES + DS_SCALE_BYTES <= 160 * 1024, "LDS");
+    static_assert(4 * 32 * STAGED_PITCH <= STAGES * 2 * DS_OP_BYTES, "epilogue staging fits the stages");
+    // Dynamic LDS: the compiler does not see the DMA as a store into it, so
+    // it may neither assume its contents nor insert its own waits for it;
+    // the rendezvous below orders every access.
+    extern __shared__ __attribute__((aligned(1024))) uint8_t ds_lds[];
+    auto stage_buf = [&](int u) { return ds_lds + u * 2 * DS_OP_BYTES; };
+    float* const lds_scales = reinterpret_cast<float*>(ds_lds + STAGES * 2 * DS_OP_BYTES);
+
+    int tm, tn;
+    tile_of(blockIdx.x, p, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+
+    // DMA: wave w moves operand chunks c = (4w + i)*64 + lane, i = 0..3, of
+    // each operand: row r = c >> 2, LDS slot c & 3, global chunk
+    // (c & 3) ^ ((r >> 2) & 3).
+    uint32_t a_row[4], b_src[4];
+    int kc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = (4 * wave + i) * 64 + lane;
+        const int r = c >> 2;
+        kc[i] = ((c & 3) ^ ((r >> 2) & 3)) * 16;
+        a_row[i] = static_cast<uint32_t>(min(m0 + r, p.M - 1)) * static_cast<uint32_t>(p.K);
+        b_src[i] = static_cast<uint32_t>(n0 + r) * static_cast<uint32_t>(p.Kp) + static_cast<uint32_t>(kc[i]);
+    }
+    const int nk = p.Kp / DS_BK;
+    // DMA d (0..7) of stage s into buf: chunk set d >> 1 of A (d even) or B
+    auto dma = [&](uint8_t* buf, int s, int d) {
+        const int i = d >> 1;
+        const int k0 = min(s, nk - 1) * DS_BK;
+        if ((d & 1) == 0) {
+            // k past K: the row's last in-range 16 bytes (their product with
+            // the zero-padded B is zero)
+            const uint32_t ka = static_cast<uint32_t>(min(k0 + kc[i], p.K - 16));
+            __builtin_amdgcn_global_load_lds(p.A + (a_row[i] + ka), (LHQ_LDS_AS void*)(buf + (4 * wave + i) * 1024),
+                                             16, 0, 0);
+        } else {
+            __builtin_amdgcn_global_load_lds(p.Bt + (b_src[i] + static_cast<uint32_t>(k0)),
+                                             (LHQ_LDS_AS void*)(buf + DS_OP_BYTES + (4 * wave + i) * 1024), 16, 0, 0);
         }
+    };
+    auto issue = [&](uint8_t* buf, int s) {
+#pragma unroll
+        for (int d = 0; d < DS_DMA_PER_STAGE; ++d) dma(buf, s, d);
+    };
+
+    using Acc = i32x16_t;
+    Acc acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = Acc{};
+
+    // operand fragments: row (lane & 31) of each 32-row block, k chunk
+    // 2*kk + (lane >> 5), swizzled by the row's (r >> 2) & 3
+    const int swz = ((lane & 31) >> 2) & 3;
+    const int a_base = (wm * 128 + (lane & 31)) * DS_BK;
+    const int b_base = DS_OP_BYTES + (wn * 128 + (lane & 31)) * DS_BK;
+    using Frag = u32x4_t[8];  // [0..3]: A blocks i, [4..7]: B blocks j
+    // fragment x (A block x for x < 4, B block x - 4 otherwise) of k step kk
+    auto read = [&](const uint8_t* buf, int kk, Frag& f, int x) {
+        const int off = (((2 * kk + (lane >> 5)) ^ swz) * 16);
+        const int base = x < 4 ? a_base + x * 32 * DS_BK : b_base + (x - 4) * 32 * DS_BK;
+        f[x] = *reinterpret_cast<const u32x4_t*>(buf + base + off);
+    };
+    // MFMA t (0..15) of one k step: block (t >> 2, t & 3)
+    auto mfma = [&](const Frag& f, int t) {
+        const int i = t >> 2, j = t & 3;
+        acc[i][j] = mfma_i8_32x32x32(f[4 + j], f[i], acc[i][j]);
+    };
+    // Rendezvous: this wave's DMA for the next stage has landed (the
+    // STAGES - 2 younger stages may still be in flight), its own LDS reads
+    // are done, and every wave got this far, so all reads of the current
+    // stage's buffer are complete and the buffer can take the DMA STAGES
+    // stages ahead.
+    auto rendezvous = [&]() {
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(DS_DMA_PER_STAGE * (STAGES - 2))
+                     : "memory");
+    };
+
+    // One stage: fragments of its first k step are in f0 on entry.  The 32
+    // MFMAs are issued with one LDS read or one DMA between consecutive
+    // ones, so the matrix pipe always has work queued while those issue:
+    //   first k step:  MFMA t, then read fragment t of the second k step
+    //                  (t < 8);
+    //   rendezvous;
+    //   second k step: MFMA t, then read fragment t of the next stage's
+    //                  first k step (t < 8) or DMA t - 8 into this stage's
+    //                  buffer (t >= 8).
+    // Each k step starts with an MFMA on fragments read long before, so the
+    // compiler's wait for them (which drains every LDS read in flight) comes
+    // before the next reads are issued.  sched_barrier pins the order.
+    Frag f0, f1;
+    auto step = [&](uint8_t* cur, const uint8_t* next, int s) {
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            mfma(f0, t);
+            if (t < 8) read(cur, 1, f1, t);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        rendezvous();
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            mfma(f1, t);
+            if (t < 8)
+                read(next, 0, f0, t);
+            else
+                dma(cur, s + STAGES, t - 8);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+
+    // The tile's scales go to LDS first (wave w: rows / columns 64w..64w+63,
+    // clamped); the wait for stage 0 below also covers them.
+    if constexpr (EPI != EPI_I32) {
+        const int r = min(m0 + 64 * wave + lane, p.M - 1), c = min(n0 + 64 * wave + lane, p.N - 1);
+        __builtin_amdgcn_global_load_lds(p.As + r, (LHQ_LDS_AS void*)(lds_scales + 64 * wave), 4, 0, 0);
+        __builtin_amdgcn_global_load_lds(p.Bs + c, (LHQ_LDS_AS void*)(lds_scales + BM + 64 * wave), 4, 0, 0);
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int col = n0 + wn * 128 + j * 32 + (lane & 31);
-        if (col >= p.N) continue;
-        float bs = 0.0f;
-        if constexpr (OP == OP_I8 && EPI != EPI_I32) bs = p.Bs[col];
+    for (int u = 0; u < STAGES; ++u) issue(stage_buf(u), u);
+    // stage 0 landed everywhere
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(DS_DMA_PER_STAGE * (STAGES - 1)) : "memory");
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+    for (int x = 0; x < 8; ++x) read(stage_buf(0), 0, f0, x);
+    for (int s = 0; s < nk; s += STAGES) {
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int row = m0 + wm * 128 + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-                if (row >= p.M) continue;
-                const int64_t o = static_cast<int64_t>(row) * p.N + col;
-                if constexpr (EPI == EPI_I32) {
-                    static_cast<int32_t*>(p.C)[o] = acc[i][j][e];
-                } else {
-                    float f;
-                    if constexpr (OP == OP_I8) {
-                        f = p.alpha * p.As[row];            // gemm_quant.cpp:44-45, left to right
-                        f = f * bs;
-                        f = f * static_cast<float>(acc[i][j][e]);
-                    } else {
-                        f = combined * acc[i][j][e];        // gemm_quant.cpp:101
-                    }
-                    if constexpr (EPI == EPI_F32) {
-                        float* Cp = static_cast<float*>(p.C);
-                        // apply_beta (gemm_quant.cpp:12-21), then C += rescaled
-                        const float base = (p.beta == 0.0f) ? 0.0f
-                                           : (p.beta == 1.0f) ? Cp[o] : Cp[o] * p.beta;
-                        Cp[o] = base + f;
-                    } else {
-                        static_cast<uint16_t*>(p.C)[o] = f32_to_bf16(0.0f + f);
-                    }
-                }
-            }
-        }
+        for (int u = 0; u < STAGES; ++u)
+            if (u == 0 || s + u < nk) step(stage_buf(u), stage_buf((u + 1) % STAGES), s + u);
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // every wave's DMAs have landed and every wave is done with the stage
+    // buffers: the epilogue may reuse them
+    __syncthreads();
+    uint8_t* const area = ds_lds + wave * 32 * STAGED_PITCH;
+    if (m0 + BM <= p.M && n0 + BN <= p.N && p.N % 8 == 0 && p.c_vec)
+        gemm8_store_staged<EPI, false>(p, acc, m0, n0, wm, wn, lane, lds_scales, area);
+    else
+        gemm8_store_staged<EPI, true>(p, acc, m0, n0, wm, wn, lane, lds_scales, area);
 }
 
 int env_int(const char* name, int dflt) {
     const char* v = std::getenv(name);
     return v ? std::atoi(v) : dflt;
+}
+
+template <int EPI, int STAGES>
+int launch_dma(const Gemm8Args& p, int tiles, void* stream, const char* who) {
+    constexpr size_t lds = static_cast<size_t>(STAGES) * 2 * DS_OP_BYTES + DS_SCALE_BYTES;
+    static const hipError_t attr =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm8_dma_kernel<EPI, STAGES>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (attr != hipSuccess)
+        return set_error(LHQ_ERR_HIP, "%s: dynamic LDS attribute: %s", who, hipGetErrorString(attr));
+    gemm8_dma_kernel<EPI, STAGES><<<tiles, NTHREADS, lds, as_stream(stream)>>>(p);
+    return check_launch(who);
 }
 
 template <int OP, int EPI>
@@ -210,6 +694,10 @@ int launch_gemm8(const uint8_t* A, const uint8_t* Bt, const float* As, const flo
     LHQ_REQUIRE(Bt && C && (A || M == 0), "%s: null pointer", who);
     if (EPI != EPI_I32) LHQ_REQUIRE(As && Bs, "%s: null scale pointer", who);
     if (M == 0) return LHQ_OK;
+    LHQ_SUPPORTED(N < (1 << 23), "%s: N=%d above 2^23 is not supported", who, N);
+    LHQ_SUPPORTED(static_cast<int64_t>(M) * K < (int64_t{1} << 32) &&
+                      static_cast<int64_t>(ceil_div(N, BN)) * BN * (ceil_div(K, BK) * BK) < (int64_t{1} << 32),
+                  "%s: operands above 4 GiB are not supported (M=%d N=%d K=%d)", who, M, N, K);
     static const int group_m = env_int("LHQ_GEMM8_GROUP_M", 4);
     Gemm8Args p{};
     p.A = A; p.Bt = Bt; p.As = As; p.Bs = Bs; p.C = C;
@@ -218,7 +706,21 @@ int launch_gemm8(const uint8_t* A, const uint8_t* Bt, const float* As, const flo
     p.tiles_n = ceil_div(N, BN);
     p.group_m = group_m > 0 ? group_m : 4;
     p.alpha = alpha; p.beta = beta;
+    p.c_vec = (reinterpret_cast<uintptr_t>(C) % 16) == 0;
     const int tiles = p.tiles_m * p.tiles_n;
+    // int8: the LDS-DMA pipeline (LHQ_GEMM8_DMA=0 selects the register-
+    // staged kernel); fp8 always uses the register-staged kernel, which zeroes
+    // the K padding of A before it reaches the MFMA
+    static const int use_dma = env_int("LHQ_GEMM8_DMA", 1);
+    if constexpr (OP == OP_I8) {
+        if (use_dma) {
+            static const int stages = env_int("LHQ_GEMM8_STAGES", DS_STAGES);
+            switch (stages) {
+                case 3: return launch_dma<EPI, 3>(p, tiles, stream, who);
+                default: return launch_dma<EPI, 4>(p, tiles, stream, who);
+            }
+        }
+    }
     gemm8_kernel<OP, EPI><<<tiles, NTHREADS, 0, as_stream(stream)>>>(p);
     return check_launch(who);
 }

@@ -1,0 +1,21 @@
+"""On-device check of the bf16 conversion instruction the kernels use.
+
+The GEMM and quantizer kernels round fp32 to bf16 with gfx950's
+v_cvt_pk_bf16_f32.  The reference's rule (dtypes.hpp:87-98) is round to
+nearest even, NaN -> payload kept with the quiet bit set; this test runs the
+instruction over all 2^32 fp32 bit patterns and requires it to agree with the
+rule on every one (NaNs, infinities, denormals and ties included).
+"""
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def test_bf16_convert_matches_reference_rule_exhaustively(lib):
+    import torch
+    from longhornai_amd import ops
+    counts = torch.zeros(2, dtype=torch.int64, device="cuda")
+    lib.call("lhq_selftest_bf16", counts.data_ptr(), ops.stream())
+    torch.cuda.synchronize()
+    non_nan, nan = counts.cpu().tolist()
+    assert non_nan == 0 and nan == 0, f"mismatches: {non_nan} non-NaN, {nan} NaN"
