@@ -184,6 +184,51 @@ def bench_w4a16(ops, M, K, N, G, steps, warmup, seed=0, min_rotate_bytes=2 * INF
     return res
 
 
+def bench_moe(ops, steps, warmup, seed=0, T=512, E=8, topk=2, K=4096, N=14336, G=128):
+    """Config 4: ragged grouped W4A16 over E experts in one launch.  T tokens
+    each pick `topk` distinct experts (top-k of seeded uniform scores); the
+    dispatched rows are expert-major and the group table is the exclusive
+    prefix sum of the per-expert counts (moe.cpp:111-123)."""
+    import numpy as np
+    import torch
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    scores = torch.rand((T, E), generator=gen, device="cuda")
+    ids = torch.topk(scores, topk, dim=1).indices.flatten()
+    counts = torch.bincount(ids, minlength=E).cpu().numpy()
+    off = np.zeros(E + 1, np.int32)
+    off[1:] = np.cumsum(counts)
+    rows = int(off[-1])
+    sets = make_w4_sets(ops, K, N, G, E, seed)
+    A = torch.randn((rows, K), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    C = ops.empty((rows, N), np.int16)
+    offd = torch.tensor(off, device="cuda")
+    qptr = torch.tensor([w.qweight.data_ptr() for w in sets], dtype=torch.int64, device="cuda")
+    sptr = torch.tensor([w.scales.data_ptr() for w in sets], dtype=torch.int64, device="cuda")
+    zptr = torch.tensor([w.zeros.data_ptr() for w in sets], dtype=torch.int64, device="cuda")
+    fn = ops.lib().cdll.lhq_gemm_w4a16_bf16_grouped
+
+    def launch(_i):
+        st = fn(A.data_ptr(), offd.data_ptr(), qptr.data_ptr(), sptr.data_ptr(), zptr.data_ptr(), C.data_ptr(),
+                E, rows, N, K, G, ops.stream())
+        if st:
+            raise RuntimeError(f"lhq_gemm_w4a16_bf16_grouped: {ops.lib().last_error()}")
+
+    ms, _ = GraphTimer(launch, 1, chunk=16).time(steps, warmup)
+    us = ms * 1e3 / steps
+    flops = 2 * rows * K * N
+    byts = E * (K * N // 2 + (K // G) * N * 2 + (K // G) * N // 2) + rows * K * 2 + rows * N * 2
+    res = {"tokens": T, "experts": E, "top_k": topk, "rows": rows, "rows_per_expert": counts.tolist(),
+           "K": K, "N": N, "G": G, "us_per_call": us, "tflops": flops / (us * 1e-6) / 1e12,
+           "gbs": byts / (us * 1e-6) / 1e9, "flops": flops, "bytes": byts}
+    res["mfma_frac"] = res["tflops"] / BF16_PEAK_TFLOPS
+    res["hbm_frac"] = res["gbs"] / HBM_PEAK_GBS
+    del sets, A, C
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_w8a8(ops, M, K, N, steps, warmup, seed=0):
     import numpy as np
     import torch
@@ -302,6 +347,28 @@ def committed_traffic(kernel_key: str):
     return int(m.group(1)) if m else None
 
 
+def prefill_legs(ops):
+    """Configs 5 (W4A16 at M = 64 and 4096 on the K=8192, N=28672 target
+    shape) and 4 (grouped MoE), timed like the decode leg."""
+    out = []
+    for m, steps in ((64, 500), (4096, 40)):
+        log(f"w4a16 prefill M={m} K=8192 N=28672: {steps} steps")
+        r = bench_w4a16(ops, m, 8192, 28672, 128, steps, max(5, steps // 10))
+        tf = 2 * m * 8192 * 28672 / (r["us_per_call"] * 1e-6) / 1e12
+        log(f"  {r['us_per_call']:.1f} us/call  {tf:.0f} TFLOPS ({100 * tf / BF16_PEAK_TFLOPS:.1f}% of bf16 peak), "
+            f"{r['gbs']:.0f} GB/s ({100 * r['hbm_frac']:.1f}% of HBM peak)")
+        out.append({"leg": "w4a16_prefill", "M": m, "K": 8192, "N": 28672, "G": 128,
+                    "us_per_call": round(r["us_per_call"], 2), "tflops": round(tf, 1),
+                    "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4), "gbs": round(r["gbs"], 1),
+                    "hbm_frac": round(r["hbm_frac"], 4)})
+    log("moe grouped W4A16 (config 4): 200 steps")
+    r = bench_moe(ops, 200, 20)
+    log(f"  {r['us_per_call']:.1f} us/call  {r['tflops']:.0f} TFLOPS ({100 * r['mfma_frac']:.1f}% of bf16 peak), "
+        f"{r['gbs']:.0f} GB/s")
+    out.append({"leg": "moe_grouped_w4a16", **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}})
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -313,7 +380,8 @@ def main() -> int:
     ap.add_argument("--w8a8-steps", type=int, default=200)
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a 1 GiB device copy (PMC calibration kernel)")
-    ap.add_argument("--only", choices=["w4a16", "w8a8"], default=None,
+    ap.add_argument("--no-prefill", action="store_true", help="skip the W4A16 prefill and MoE legs")
+    ap.add_argument("--only", choices=["w4a16", "w8a8", "prefill"], default=None,
                     help="run one leg only (profiling); prints that leg's summary, not the bench line")
     args = ap.parse_args()
 
@@ -341,6 +409,10 @@ def main() -> int:
             r = bench_w8a8(ops, m, 4096, 14336, args.w8a8_steps, max(10, args.w8a8_steps // 10))
             print(json.dumps({"leg": "w8a8_prefill", **r}), flush=True)
         return 0
+    if args.only == "prefill":
+        for r in prefill_legs(ops):
+            print(json.dumps(r), flush=True)
+        return 0
     log(f"w4a16 decode M={M} K={K} N={N} G={G}: {args.warmup} warmup + {args.steps} timed steps")
     w4 = bench_w4a16(ops, M, K, N, G, args.steps, args.warmup)
     log(f"  {w4['us_per_call']:.2f} us/call  {w4['gbs']:.1f} GB/s  ({100 * w4['hbm_frac']:.1f}% of HBM peak), "
@@ -358,6 +430,8 @@ def main() -> int:
             log(f"  {r['us_per_call']:.1f} us/call  {r['tops']:.0f} TOPS ({100 * r['mfma_frac']:.1f}% of int8 peak); "
                 f"act quant {r['act_quant_us']:.1f} us ({r['act_quant_gbs']:.0f} GB/s)")
             w8.append(r)
+
+    pre = [] if args.no_prefill else prefill_legs(ops)
 
     cpu = None
     if not args.no_cpu:
@@ -393,6 +467,7 @@ def main() -> int:
              "value": round(r["tops"], 1), "unit": "TOPS", "peak": INT8_PEAK_TOPS,
              "frac": round(r["mfma_frac"], 4), "act_quant_us": round(r["act_quant_us"], 2)}
             for r in w8],
+        "w4a16_prefill": pre,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -21,6 +21,7 @@
 //     grouped launches (device-side group table).
 // Both split K over the waves of a workgroup and reduce through LDS in wave
 // order, so results are deterministic.
+#include <algorithm>
 #include <cstdlib>
 #include <type_traits>
 
@@ -70,15 +71,16 @@ __device__ __forceinline__ int group_of_c(int kt, int s, uint32_t gmul) {
 }
 
 // Map blockIdx.y of a grouped launch to (group, first row, row end): groups
-// take ceil(rows/16) row blocks each, in order.  Offsets are clamped to
+// take ceil(rows/RB) row blocks each, in order.  Offsets are clamped to
 // [0, row_capacity] so a malformed table can never index outside A or C.
+template <int RB = 16>
 __device__ __forceinline__ bool resolve_group(const W4Args& p, int y, int& e, int& m0, int& m_end) {
     for (e = 0; e < p.num_groups; ++e) {
         const int r0 = min(max(p.offsets[e], 0), p.row_capacity);
         const int r1 = min(max(p.offsets[e + 1], r0), p.row_capacity);
-        const int nb = (r1 - r0 + 15) >> 4;
+        const int nb = (r1 - r0 + RB - 1) / RB;
         if (y < nb) {
-            m0 = r0 + 16 * y;
+            m0 = r0 + RB * y;
             m_end = r1;
             return true;
         }
@@ -267,17 +269,26 @@ __global__ __launch_bounds__(64 * WAVES) void w4_gemv_kernel(W4Args p) {
 // clamped to valid ones, the values discarded): the compiler counts
 // outstanding loads per path, and a load that only some paths issue would
 // turn each later wait into a wait for everything.
-template <bool F32A, bool ASYM, bool F32C, int T, int NPW, int BPS, bool GBIG>
-__global__ __launch_bounds__(T == 1 ? 1024 : 512) void w4_decode_kernel(W4Args p) {
+// MR: accumulator rows per lane that can hold an output row.  Lane l holds
+// rows 4*(l >> 4) + r, r < 4; with M == 1 only row 0 (r = 0 of lanes 0..15)
+// is real, so MR = 1 skips the per-group correction of the other three.
+// Launch bounds: one-column-tile bf16-activation variants are held to four
+// waves per SIMD (<= 128 VGPRs; they need ~90).  Two-column-tile variants
+// need ~136 and would spill inside the loop under that bound.
+template <bool F32A, bool ASYM, bool F32C, int T, int NPW, int BPS, bool GBIG, int MR>
+__global__ __launch_bounds__(T == 1 ? 1024 : 512, (F32A || T == 2) ? 1 : 4) void w4_decode_kernel(W4Args p) {
     static_assert(NPW == 4 || NPW == 8, "passes start at multiples of NPW tiles");
+    static_assert(MR == 1 || MR == 4, "one row or all four");
     constexpr int SEGS = 4 / BPS;
     // zero words (8 groups each) per pass: G < 128 -> the pass's words
     // (passes start at multiples of 8 tiles); G == 128 -> one shared word;
     // G > 128 -> one per tile
     constexpr int NZW = (BPS < 4) ? (NPW * SEGS + 7) / 8 : (GBIG ? NPW : 1);
-    // [F32A ? 2 : 1 planes][Ml rows][Kp], bf16 (fp32 activations: hi, lo)
+    // [F32A ? 2 : 1 planes][Ml rows][Kp], bf16 (fp32 activations: hi, lo);
+    // after the main loop the same memory holds the cross-wave reduction
+    // (the launcher sizes it for both), so a workgroup takes no more LDS
+    // than its activations and more workgroups fit on a CU
     extern __shared__ __attribute__((aligned(16))) uint16_t a_lds[];
-    __shared__ float red[T == 1 ? 16 : 8][T][4][64];
 
     const int S = blockDim.x >> 6;
     const int lane = threadIdx.x & 63;
@@ -457,7 +468,7 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512) void w4_decode_kernel(W4Args p
                             zc = kW4Bias + 8.0f;  // implied zero point 8
                         }
 #pragma unroll
-                        for (int r = 0; r < 4; ++r)
+                        for (int r = 0; r < MR; ++r)
                             acc[t][r] = __builtin_fmaf(sc, __builtin_fmaf(-zc, xs[r], tt[r]), acc[t][r]);
                     }
                 }
@@ -491,16 +502,215 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512) void w4_decode_kernel(W4Args p
         if (r >= p.M || c >= p.N || ntt >= p.Nt) return;
         w4_store<F32C>(p, z * p.c_bs + static_cast<int64_t>(r) * p.N + c, v);
     };
+    // red[wave][t][r][lane], r < MR, in the activation area once every
+    // wave is done reading it
+    float* const red = reinterpret_cast<float*>(a_lds);
+    __syncthreads();
 #pragma unroll
     for (int t = 0; t < T; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) red[wave][t][r][lane] = acc[t][r];
+        for (int r = 0; r < MR; ++r) red[((wave * T + t) * MR + r) * 64 + lane] = acc[t][r];
     __syncthreads();
-    for (int idx = threadIdx.x; idx < T * 4 * 64; idx += 64 * S) {
-        const int t = idx >> 8, r = (idx >> 6) & 3, ln = idx & 63;
+    for (int idx = threadIdx.x; idx < T * MR * 64; idx += 64 * S) {
+        const int t = idx / (MR * 64), r = (idx / 64) % MR, ln = idx & 63;
         float sum = 0.0f;
-        for (int w2 = 0; w2 < S; ++w2) sum += red[w2][t][r][ln];
+        for (int w2 = 0; w2 < S; ++w2) sum += red[((w2 * T + t) * MR + r) * 64 + ln];
         store(t, r, ln, sum);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Prefill tile kernel: bf16 activations and output, asymmetric int4 weights,
+// many rows (plain, uniform batches, ragged groups).  A 256-thread
+// workgroup owns a 128 x 128 output tile; wave (wm, wn) owns rows
+// 64*wm .. +63 and columns 64*wn .. +63 as 4 x 4 blocks of 16x16x32 MFMA
+// accumulators.  Per 128-deep K tile:
+//   - the workgroup's 128 activation rows x 128 k (32 KiB) go global -> LDS
+//     by DMA into one of two buffers; 16-byte chunk c of row r sits in slot
+//     c ^ (r & 15), so the 16 rows of a fragment read hit 16 different bank
+//     groups;
+//   - each wave loads its four 1 KiB weight tiles and their scales / zero
+//     words straight into registers, one K tile ahead of their use;
+//   - per scale group segment: t = sum_k x*(128 + u) (MFMA on the exact
+//     bf16 integers of w4_operand), xs = sum_k x (MFMA against ones), and
+//     acc += s * (t - (128 + z) * xs) -- the decode kernel's arithmetic, with
+//     each weight tile decoded once per 64 rows instead of once per 16.
+// The K loop alternates two register sets (A buffer and weights of the tile
+// in flight vs the tile in use) and meets at one `s_waitcnt vmcnt(0)` +
+// `s_barrier` per tile: before it, only the tile about to be used is in
+// flight.  Every load is unconditional (rows past the end read the last
+// row; column tiles past Nt re-read the last one).  Requires K % 128 == 0
+// (the activations are not zero-padded in LDS).
+// ---------------------------------------------------------------------------
+constexpr int MM_BM = 128;                          // rows per workgroup tile
+constexpr int MM_CT = 4;                            // column tiles per wave
+constexpr int MM_BN = 2 * MM_CT * kW4TileN;         // columns per workgroup tile (128)
+constexpr int MM_A_BYTES = MM_BM * kW4TileK * 2;    // one activation buffer (32 KiB)
+constexpr int MM_DMA = MM_A_BYTES / 1024 / 4;       // activation DMAs per wave per tile (8)
+
+#define LHQ_LDS_AS __attribute__((address_space(3)))
+
+template <int BPS, bool GBIG, bool GR>
+__global__ __launch_bounds__(256, 2) void w4_mma_kernel(W4Args p) {
+    constexpr int SEGS = 4 / BPS;
+    extern __shared__ __attribute__((aligned(1024))) uint8_t mm_lds[];  // 2 x MM_A_BYTES
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int z = blockIdx.z;
+    int m0, m_end;
+    const uint8_t* qw;
+    const uint16_t* sc;
+    const uint32_t* zs;
+    if constexpr (GR) {
+        int e;
+        if (!resolve_group<MM_BM>(p, blockIdx.y, e, m0, m_end)) return;  // uniform per workgroup
+        qw = p.qws[e];
+        sc = static_cast<const uint16_t*>(p.scs[e]);
+        zs = p.zss[e];
+    } else {
+        m0 = blockIdx.y * MM_BM;
+        m_end = p.M;
+        qw = p.qw + z * p.qw_bs;
+        sc = static_cast<const uint16_t*>(p.scales) + z * p.s_bs;
+        zs = p.zeros + z * p.z_bs;
+    }
+    const uint16_t* A = static_cast<const uint16_t*>(p.A) + (GR ? 0 : z * p.a_bs);
+    const int col = lane & 15;
+
+    // activation DMA q of this wave: chunk idx = (8*wave + q)*64 + lane is
+    // row idx >> 4, LDS slot idx & 15, global chunk slot ^ (row & 15);
+    // element offsets are 32-bit (the launcher bounds rows * K)
+    uint32_t a_off[MM_DMA];
+#pragma unroll
+    for (int q = 0; q < MM_DMA; ++q) {
+        const int idx = (MM_DMA * wave + q) * 64 + lane;
+        const int r = idx >> 4, slot = idx & 15;
+        const int row = min(m0 + r, m_end - 1);
+        a_off[q] = static_cast<uint32_t>(row) * static_cast<uint32_t>(p.K) + static_cast<uint32_t>((slot ^ (r & 15)) * 8);
+    }
+    // this wave's column tiles (clamped to the last one) and their bases
+    uint32_t w_base[MM_CT], s_base[MM_CT], z_base[MM_CT];
+#pragma unroll
+    for (int c = 0; c < MM_CT; ++c) {
+        const int nt = min(static_cast<int>(blockIdx.x) * 2 * MM_CT + wn * MM_CT + c, p.Nt - 1);
+        w_base[c] = static_cast<uint32_t>(nt * p.Kt) * kW4TileBytes + static_cast<uint32_t>(lane * 16);
+        s_base[c] = static_cast<uint32_t>(nt * p.NG * 16 + (col & ~1));  // fp16 pair holding this column
+        z_base[c] = static_cast<uint32_t>(nt * p.NG8 * 16 + col);
+    }
+    const uint32_t s_half = 16u * (col & 1);
+
+    struct Regs {
+        u32x4_t w[MM_CT];
+        uint32_t sw[MM_CT][SEGS];
+        uint32_t zw[MM_CT];
+    };
+    // all loads of K tile kt (clamped) into LDS buffer buf and registers R
+    auto issue = [&](uint8_t* buf, Regs& R, int kt_in) {
+        const int kt = min(kt_in, p.Kt - 1);
+        const uint32_t k0 = static_cast<uint32_t>(kt * kW4TileK);
+#pragma unroll
+        for (int q = 0; q < MM_DMA; ++q)
+            __builtin_amdgcn_global_load_lds(A + (a_off[q] + k0), (LHQ_LDS_AS void*)(buf + (MM_DMA * wave + q) * 1024),
+                                             16, 0, 0);
+#pragma unroll
+        for (int c = 0; c < MM_CT; ++c) {
+            R.zw[c] = zs[z_base[c] + static_cast<uint32_t>((group_of_c<BPS, GBIG>(kt, 0, p.gmul) >> 3) * 16)];
+#pragma unroll
+            for (int s = 0; s < SEGS; ++s)
+                R.sw[c][s] = *reinterpret_cast<const uint32_t*>(
+                    sc + s_base[c] + static_cast<uint32_t>(group_of_c<BPS, GBIG>(kt, s, p.gmul) * 16));
+            R.w[c] = *reinterpret_cast<const u32x4_t*>(qw + (w_base[c] + static_cast<uint32_t>(kt * kW4TileBytes)));
+        }
+    };
+
+    f32x4_t acc[4][MM_CT];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int c = 0; c < MM_CT; ++c) acc[i][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const u32x4_t ones = {kOnesBf16x2, kOnesBf16x2, kOnesBf16x2, kOnesBf16x2};
+    // fragment (row block i, k block j): row 64*wm + 16*i + (lane & 15), k
+    // chunk 4j + (lane >> 4), stored in slot chunk ^ (lane & 15)
+    const uint32_t a_frag = static_cast<uint32_t>((wm * 64 + col) * 256);
+
+    auto compute = [&](const uint8_t* buf, const Regs& R, int kt) {
+        u32x4_t a[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                a[i][j] = *reinterpret_cast<const u32x4_t*>(buf + a_frag + i * 16 * 256 +
+                                                            (((4 * j + (lane >> 4)) ^ col) * 16));
+        f32x4_t xs[4][SEGS];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int s = 0; s < SEGS; ++s) {
+                xs[i][s] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int jj = 0; jj < BPS; ++jj) xs[i][s] = mfma_bf16_16x16x32(a[i][s * BPS + jj], ones, xs[i][s]);
+            }
+#pragma unroll
+        for (int c = 0; c < MM_CT; ++c) {
+            u32x4_t b[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) b[j] = w4_operand(R.w[c][j]);
+#pragma unroll
+            for (int s = 0; s < SEGS; ++s) {
+                const int g = group_of_c<BPS, GBIG>(kt, s, p.gmul);
+                const float scl = f16_to_f32(static_cast<uint16_t>(R.sw[c][s] >> s_half));
+                const float zc = kW4Bias + static_cast<float>((R.zw[c] >> (4 * (g & 7))) & 15u);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    f32x4_t tt = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int jj = 0; jj < BPS; ++jj) tt = mfma_bf16_16x16x32(a[i][s * BPS + jj], b[s * BPS + jj], tt);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        acc[i][c][r] = __builtin_fmaf(scl, __builtin_fmaf(-zc, xs[i][s][r], tt[r]), acc[i][c][r]);
+                }
+            }
+        }
+    };
+    // all of this wave's loads have landed and every wave is done with the
+    // buffer the next DMA overwrites
+    auto rendezvous = [&]() { asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory"); };
+
+    uint8_t* const buf0 = mm_lds;
+    uint8_t* const buf1 = mm_lds + MM_A_BYTES;
+    Regs ra, rb;
+    issue(buf0, ra, 0);
+    int kt = 0;
+    for (; kt + 2 <= p.Kt; kt += 2) {
+        rendezvous();
+        issue(buf1, rb, kt + 1);
+        compute(buf0, ra, kt);
+        rendezvous();
+        issue(buf0, ra, kt + 2);  // clamped past the end: never used
+        compute(buf1, rb, kt + 1);
+    }
+    if (kt < p.Kt) {
+        rendezvous();
+        compute(buf0, ra, kt);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    // D element r of block (i, c): row 64*wm + 16*i + 4*(lane >> 4) + r,
+    // column of tile (blockIdx.x*8 + 4*wn + c), lane & 15
+    uint16_t* C = static_cast<uint16_t*>(p.C) + (GR ? 0 : z * p.c_bs);
+#pragma unroll
+    for (int c = 0; c < MM_CT; ++c) {
+        const int nt = static_cast<int>(blockIdx.x) * 2 * MM_CT + wn * MM_CT + c;
+        const int cn = nt * kW4TileN + col;
+        if (nt >= p.Nt || cn >= p.N) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = m0 + wm * 64 + i * 16 + 4 * (lane >> 4) + r;
+                if (row < m_end) C[static_cast<int64_t>(row) * p.N + cn] = f32_to_bf16(acc[i][c][r]);
+            }
     }
 }
 
@@ -520,16 +730,23 @@ int env_int(const char* name) {
     return v ? std::atoi(v) : 0;
 }
 
-template <bool F32A, bool ASYM, bool F32C, int T, int NPW>
-void launch_decode_bps(const W4Args& a, dim3 grid, int S, int bps, size_t lds, hipStream_t s) {
+template <bool F32A, bool ASYM, bool F32C, int T, int NPW, int MR>
+void launch_decode_mr(const W4Args& a, dim3 grid, int S, int bps, size_t lds, hipStream_t s) {
+    lds = std::max(lds, static_cast<size_t>(S) * T * MR * 64 * sizeof(float));  // the reduction reuses it
     switch (bps) {
-        case 1: w4_decode_kernel<F32A, ASYM, F32C, T, NPW, 1, false><<<grid, 64 * S, lds, s>>>(a); break;
-        case 2: w4_decode_kernel<F32A, ASYM, F32C, T, NPW, 2, false><<<grid, 64 * S, lds, s>>>(a); break;
+        case 1: w4_decode_kernel<F32A, ASYM, F32C, T, NPW, 1, false, MR><<<grid, 64 * S, lds, s>>>(a); break;
+        case 2: w4_decode_kernel<F32A, ASYM, F32C, T, NPW, 2, false, MR><<<grid, 64 * S, lds, s>>>(a); break;
         default:
-            if (a.gmul) w4_decode_kernel<F32A, ASYM, F32C, T, NPW, 4, true><<<grid, 64 * S, lds, s>>>(a);
-            else w4_decode_kernel<F32A, ASYM, F32C, T, NPW, 4, false><<<grid, 64 * S, lds, s>>>(a);
+            if (a.gmul) w4_decode_kernel<F32A, ASYM, F32C, T, NPW, 4, true, MR><<<grid, 64 * S, lds, s>>>(a);
+            else w4_decode_kernel<F32A, ASYM, F32C, T, NPW, 4, false, MR><<<grid, 64 * S, lds, s>>>(a);
             break;
     }
+}
+
+template <bool F32A, bool ASYM, bool F32C, int T, int NPW>
+void launch_decode_bps(const W4Args& a, dim3 grid, int S, int bps, size_t lds, hipStream_t s) {
+    if (a.M == 1) launch_decode_mr<F32A, ASYM, F32C, T, NPW, 1>(a, grid, S, bps, lds, s);
+    else launch_decode_mr<F32A, ASYM, F32C, T, NPW, 4>(a, grid, S, bps, lds, s);
 }
 
 template <bool F32A, bool ASYM, bool F32C, int T, int WAVES, bool GR>
@@ -549,6 +766,31 @@ void launch_gemv_waves(const W4Args& a, dim3 grid, int W, int bps, hipStream_t s
         case 4: launch_gemv_bps<F32A, ASYM, F32C, T, 4, GR>(a, grid, bps, s); break;
         default: launch_gemv_bps<F32A, ASYM, F32C, T, 8, GR>(a, grid, bps, s); break;
     }
+}
+
+// G >= 128 only (one scale group per K tile segment); smaller groups would
+// need four times the activation-sum registers and spill.
+template <bool GR>
+void launch_mma(const W4Args& a, dim3 grid, hipStream_t s) {
+    constexpr size_t lds = 2 * MM_A_BYTES;
+    if (a.gmul) w4_mma_kernel<4, true, GR><<<grid, 256, lds, s>>>(a);
+    else w4_mma_kernel<4, false, GR><<<grid, 256, lds, s>>>(a);
+}
+
+// The prefill tile kernel serves the bf16 entry points when there are rows
+// enough to reuse each decoded weight tile (LHQ_W4_MMA=0 / 1 forces it off /
+// on where it applies): G >= 128, K % 128 == 0 (no activation padding in
+// LDS) and 32-bit element offsets for the activations.
+bool mma_applies(const W4Args& a, int64_t rows, double rows_per_block) {
+    static const int env = [] {
+        const char* v = std::getenv("LHQ_W4_MMA");
+        return v ? std::atoi(v) : -1;
+    }();
+    if (env == 0) return false;
+    if (a.G < kW4TileK || a.K % kW4TileK != 0 || rows * a.K >= (int64_t{1} << 31)) return false;
+    // measured at K=8192, N=28672: M=32 is faster on the 16-row GEMV (72 vs
+    // 123 us), M=64 on the tile kernel (123 vs 143 us)
+    return env == 1 || rows_per_block >= 48.0;
 }
 
 // mblocks: 16-row blocks along grid.y (for a grouped launch, an upper bound
@@ -652,6 +894,11 @@ int lhq_gemm_w4a16_bf16(const uint16_t* A, const uint8_t* qweight, const uint16_
     LHQ_REQUIRE(qweight && scales && zeros && C && (A || M == 0), "gemm_w4a16_bf16: null pointer");
     if (M == 0) return LHQ_OK;
     W4Args a = make_args(A, qweight, scales, zeros, C, M, N, K, G, 1.0f, 0.0f);
+    if (mma_applies(a, M, M)) {
+        LHQ_SUPPORTED(ceil_div(M, MM_BM) <= 65535, "gemm_w4a16_bf16: M=%d exceeds the grid limit", M);
+        launch_mma<false>(a, dim3(ceil_div(a.Nt, 2 * MM_CT), ceil_div(M, MM_BM), 1), as_stream(stream));
+        return check_launch("w4a16 prefill");
+    }
     return launch_w4<false, true, false>(a, 1, as_stream(stream));
 }
 
@@ -668,6 +915,11 @@ int lhq_gemm_w4a16_bf16_batched(const uint16_t* A, const uint8_t* qweight, const
     a.qw_bs = lhq_w4_qweight_bytes(K, N);
     a.s_bs = static_cast<int64_t>(a.Nt) * a.NG * 16;
     a.z_bs = static_cast<int64_t>(a.Nt) * a.NG8 * 16;
+    if (mma_applies(a, M, M)) {
+        LHQ_SUPPORTED(ceil_div(M, MM_BM) <= 65535, "gemm_w4a16_bf16_batched: M=%d exceeds the grid limit", M);
+        launch_mma<false>(a, dim3(ceil_div(a.Nt, 2 * MM_CT), ceil_div(M, MM_BM), batch), as_stream(stream));
+        return check_launch("w4a16 prefill batched");
+    }
     return launch_w4<false, true, false>(a, batch, as_stream(stream));
 }
 
@@ -686,6 +938,14 @@ int lhq_gemm_w4a16_bf16_grouped(const uint16_t* A, const int32_t* offsets, const
     a.zss = zeros;
     a.num_groups = num_groups;
     a.row_capacity = row_capacity;
+    if (mma_applies(a, row_capacity, static_cast<double>(row_capacity) / num_groups)) {
+        // sum_e ceil(rows_e / 128) <= ceil(row_capacity / 128) + num_groups
+        const int64_t tiles = ceil_div64(row_capacity, MM_BM) + num_groups;
+        LHQ_SUPPORTED(tiles <= 65535, "gemm_w4a16_bf16_grouped: %lld row tiles exceed the grid limit",
+                      static_cast<long long>(tiles));
+        launch_mma<true>(a, dim3(ceil_div(a.Nt, 2 * MM_CT), static_cast<unsigned>(tiles), 1), as_stream(stream));
+        return check_launch("w4a16 prefill grouped");
+    }
     // sum_e ceil(rows_e / 16) <= ceil(row_capacity / 16) + num_groups
     const int64_t mblocks = ceil_div64(row_capacity, 16) + num_groups;
     LHQ_SUPPORTED(mblocks <= 65535, "gemm_w4a16_bf16_grouped: %lld row blocks exceed the grid limit",

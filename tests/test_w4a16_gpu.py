@@ -172,3 +172,67 @@ def test_w4a16_grouped_empty_expert(oracle, ops):
     got, want, off = _grouped(oracle, ops, T=20, E=4, topk=1, K=128, N=48, G=64, seed=3, empty_expert=2)
     assert off[3] == off[2]
     assert rel_frobenius(got, want) <= TOL_BF16
+
+
+# ---------------------------------------------------------------------------
+# Prefill tile kernel (rows > 16, G >= 128, K % 128 == 0): 128 x 128 tiles,
+# activations staged in LDS, each weight tile decoded once per 64 rows.
+# ---------------------------------------------------------------------------
+def _ulp_close(got, want_f32, oracle, frac=0.999):
+    want_b = D.bf16_bits_to_f32(D.to_bf16_bits(oracle, want_f32))
+    ulp = np.abs(want_b) * 2.0 ** -7 + 1e-30
+    return (np.abs(got - want_b) <= ulp).mean() > frac
+
+
+@pytest.mark.parametrize("M,K,N,G", [
+    (48, 256, 48, 128),      # just above the GEMV range
+    (64, 1024, 136, 128),    # config 5 M, ragged N (not a multiple of 128)
+    (128, 512, 256, 128),    # one full row tile
+    (200, 512, 300, 256),    # partial row tile, G spanning two K tiles
+    (300, 1024, 512, 128),   # three row tiles
+    (129, 768, 130, 384),    # G = 3 K tiles (the __umulhi group index)
+    (257, 256, 16, 128),     # a single 16-column tile
+    (64, 8192, 256, 128),    # config 5 K
+])
+def test_w4a16_bf16_prefill_matches_oracle(oracle, ops, M, K, N, G):
+    got, want = _asym_case(oracle, ops, M, K, N, G, seed=500 + M + N)
+    err = rel_frobenius(got, want)
+    assert err <= TOL_BF16, f"rel Frobenius {err:.3e}"
+    assert _ulp_close(got, want, oracle)
+
+
+def test_w4a16_bf16_prefill_batched(oracle, ops):
+    import torch
+    B, M, K, N, G = 2, 150, 512, 96, 128
+    As, Ws, wants = [], [], []
+    for b in range(B):
+        A = D.to_bf16_bits(oracle, D.normal((M, K), 1.0, 40 + b))
+        p, s, z = oracle.q4a_quantize_groupwise(D.normal((K, N), 0.02, 50 + b), G)
+        As.append(A)
+        Ws.append(ops.prepack_w4_asym(ops.dev(p), ops.dev(s), ops.dev(z), K, N, G))
+        wants.append(oracle.gemm_w4a16_asym(A, p, s, z, N, G))
+    A_all = ops.dev(np.stack(As))
+    q = torch.cat([w.qweight for w in Ws])
+    s = torch.cat([w.scales for w in Ws])
+    z = torch.cat([w.zeros for w in Ws])
+    C = ops.empty((B, M, N), np.int16)
+    ops.run("lhq_gemm_w4a16_bf16_batched", A_all, q, s, z, C, B, M, N, K, G)
+    got = D.bf16_bits_to_f32(ops.host(C, np.uint16))
+    for b in range(B):
+        assert rel_frobenius(got[b], wants[b]) <= TOL_BF16
+        assert _ulp_close(got[b], wants[b], oracle)
+
+
+def test_w4a16_grouped_prefill_config4_routing(oracle, ops):
+    """Config 4's routing (512 tokens, top-2 of 8 experts, sum M_g = 1024) at full K, reduced N."""
+    got, want, off = _grouped(oracle, ops, T=512, E=8, topk=2, K=4096, N=256, G=128, seed=11)
+    assert off[-1] == 1024
+    assert rel_frobenius(got, want) <= TOL_BF16
+    assert _ulp_close(got, want, oracle)
+
+
+def test_w4a16_grouped_prefill_empty_expert(oracle, ops):
+    got, want, off = _grouped(oracle, ops, T=200, E=4, topk=1, K=384, N=80, G=128, seed=5, empty_expert=1)
+    assert off[2] == off[1]
+    assert rel_frobenius(got, want) <= TOL_BF16
+    assert _ulp_close(got, want, oracle)
