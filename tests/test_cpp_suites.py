@@ -31,3 +31,38 @@ def test_cpp_dtypes_suite():
 def test_cpp_kernel_suites():
     out = _run("lh_kernel_tests", 110)
     assert "FAILED" not in out
+
+
+def _bench(args, timeout):
+    exe = os.path.join(ROOT, "longhornai_amd", "bin", "lh_bench")
+    assert os.path.exists(exe), f"{exe} is not built (run __graft_entry__.build())"
+    print("running lh_bench " + " ".join(args), flush=True)
+    r = subprocess.run([exe] + args, capture_output=True, text=True, timeout=timeout)
+    out = r.stdout + r.stderr
+    print(out[-3000:], flush=True)
+    assert r.returncode == 0, f"lh_bench failed:\n{out[-3000:]}"
+    return out
+
+
+@pytest.mark.gpu
+def test_lh_bench_hip_timing(tmp_path):
+    """The benchmark driver's HIP timing mode: event-timed launches of the
+    decode GEMV with rotating weight sets, table + roofline + CSV."""
+    csv = tmp_path / "bench.csv"
+    roof = tmp_path / "roofline.csv"
+    out = _bench(["--timing", "hip", "--filter", "w4a16/decode", "--iters", "20", "--warmup", "3",
+                  "--csv", str(csv), "--roofline", str(roof)], 100)
+    assert "w4a16/decode[1x8192x28672]" in out
+    rows = csv.read_text().strip().splitlines()
+    assert rows[0].startswith("name,timing,mean_us")
+    name, timing, mean_us = rows[1].split(",")[:3]
+    assert timing == "hip" and float(mean_us) > 0
+    r = roof.read_text().strip().splitlines()[1].split(",")
+    assert r[5] == "memory"  # AI of a decode GEMV is far below the bf16 ridge
+
+
+@pytest.mark.gpu
+def test_lh_bench_host_timing():
+    """Host timing over the synchronous lh:: drop-in, as the reference's driver."""
+    out = _bench(["--timing", "host", "--filter", "lh/c1_w8_gemv", "--iters", "3", "--warmup", "1"], 100)
+    assert "lh/c1_w8_gemv[1x4096x4096]" in out
