@@ -669,6 +669,86 @@ __global__ __launch_bounds__(NTHREADS) void gemm8_dma_kernel(Gemm8Args p) {
         gemm8_store_staged<EPI, true>(p, acc, m0, n0, wm, wn, lane, lds_scales, area);
 }
 
+// ---------------------------------------------------------------------------
+// Skinny int8 kernel (W8A8 with M <= 16, e.g. the M = 1 GEMV of config 1).
+// The 256x256 tile kernel would spend 255/256 of its MFMA work and all but
+// N/256 of its workgroups on nothing there.  Here a 256-thread workgroup
+// owns one 16-column tile and its eight waves split K; per 64-deep k step a
+// lane loads 16 contiguous k bytes of its column from the prepacked B^T (one
+// 1 KiB coalesced load per wave) and 16 of its row of A, and one
+// v_mfma_i32_16x16x64_i8 accumulates the 16 x 16 block (rows past M read
+// row M-1, their outputs are not stored).  The eight int32 partial blocks
+// are summed through LDS -- integer addition, so the result is the
+// reference's accumulator exactly -- and the epilogue is the tile kernel's.
+// ---------------------------------------------------------------------------
+constexpr int SK_WAVES = 8;
+constexpr int SK_BATCH = 8;  // k steps loaded before they are consumed
+
+template <int EPI>
+__global__ __launch_bounds__(64 * SK_WAVES) void gemm8_skinny_kernel(Gemm8Args p) {
+    __shared__ i32x4_t red[SK_WAVES][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n0 = blockIdx.x * 16;
+    const int col = n0 + (lane & 15);          // < Np: B^T rows are zero-padded to a multiple of 256
+    const int row = min(lane & 15, p.M - 1);   // the A row this lane feeds
+    const int kl = 16 * (lane >> 4);           // this lane's 16 k within a 64-deep step
+    const int steps = p.Kp / 64;
+    const int per = (steps + SK_WAVES - 1) / SK_WAVES;
+    const int s0 = min(wave * per, steps), s1 = min(s0 + per, steps);
+    const uint8_t* a_row = p.A + static_cast<size_t>(row) * p.K;
+    const uint8_t* b_col = p.Bt + static_cast<size_t>(col) * p.Kp;
+
+    i32x4_t acc = {0, 0, 0, 0};
+    for (int sb = s0; sb < s1; sb += SK_BATCH) {
+        u32x4_t a[SK_BATCH], b[SK_BATCH];
+#pragma unroll
+        for (int u = 0; u < SK_BATCH; ++u) {
+            // steps past this wave's range re-read its last one (discarded);
+            // k past K reads the row's last 16 bytes (B^T is zero there)
+            const int k = min(sb + u, s1 - 1) * 64 + kl;
+            a[u] = *reinterpret_cast<const u32x4_t*>(a_row + min(k, p.K - 16));
+            b[u] = *reinterpret_cast<const u32x4_t*>(b_col + k);
+        }
+#pragma unroll
+        for (int u = 0; u < SK_BATCH; ++u)
+            if (sb + u < s1) acc = mfma_i8_16x16x64(a[u], b[u], acc);
+    }
+    red[wave][lane] = acc;
+    __syncthreads();
+    if (wave != 0) return;
+    i32x4_t sum = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < SK_WAVES; ++w) sum += red[w][lane];
+
+    // D element j of lane l: row 4*(l >> 4) + j, column n0 + (l & 15)
+    const int c = n0 + (lane & 15);
+    if (c >= p.N) return;
+    float bs = 0.0f;
+    if constexpr (EPI != EPI_I32) bs = p.Bs[c];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int r = 4 * (lane >> 4) + j;
+        if (r >= p.M) continue;
+        const size_t o = static_cast<size_t>(r) * p.N + c;
+        if constexpr (EPI == EPI_I32) {
+            static_cast<int32_t*>(p.C)[o] = sum[j];
+        } else {
+            float f = p.alpha * p.As[r];  // gemm_quant.cpp:44-46, left to right
+            f = f * bs;
+            f = f * static_cast<float>(sum[j]);
+            if constexpr (EPI == EPI_F32) {
+                // apply_beta (gemm_quant.cpp:12-21), then C += rescaled
+                float* Cp = static_cast<float*>(p.C);
+                const float base = (p.beta == 0.0f) ? 0.0f : (p.beta == 1.0f) ? Cp[o] : Cp[o] * p.beta;
+                Cp[o] = base + f;
+            } else {
+                static_cast<uint16_t*>(p.C)[o] = f32_to_bf16(0.0f + f);
+            }
+        }
+    }
+}
+
 int env_int(const char* name, int dflt) {
     const char* v = std::getenv(name);
     return v ? std::atoi(v) : dflt;
@@ -712,7 +792,12 @@ int launch_gemm8(const uint8_t* A, const uint8_t* Bt, const float* As, const flo
     // staged kernel); fp8 always uses the register-staged kernel, which zeroes
     // the K padding of A before it reaches the MFMA
     static const int use_dma = env_int("LHQ_GEMM8_DMA", 1);
+    static const int use_skinny = env_int("LHQ_GEMM8_SKINNY", 1);
     if constexpr (OP == OP_I8) {
+        if (use_skinny && M <= 16) {
+            gemm8_skinny_kernel<EPI><<<ceil_div(N, 16), 64 * SK_WAVES, 0, as_stream(stream)>>>(p);
+            return check_launch(who);
+        }
         if (use_dma) {
             static const int stages = env_int("LHQ_GEMM8_STAGES", DS_STAGES);
             switch (stages) {

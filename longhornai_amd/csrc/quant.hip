@@ -79,6 +79,59 @@ __global__ __launch_bounds__(kBlock) void quant_per_row_kernel(const T* __restri
     if (threadIdx.x == 0) scales[blockIdx.x] = scale;
 }
 
+// fp32 rows whose length is a multiple of 4: 16-byte loads and 4-byte
+// stores; rows of up to 4 * 4 * kBlock elements stay in registers between
+// the max-abs pass and the quantizing pass (one read of the row), longer
+// rows are read again (from L2).  Same rule as quant_per_row_kernel.
+template <bool FP8>
+__global__ __launch_bounds__(kBlock) void quant_per_row_f32_vec_kernel(const float* __restrict__ src,
+                                                                       uint8_t* __restrict__ dst,
+                                                                       float* __restrict__ scales, int dim) {
+    constexpr int R = 4;  // float4 chunks a thread keeps
+    const int64_t base = static_cast<int64_t>(blockIdx.x) * dim;
+    const f32x4_t* s4 = reinterpret_cast<const f32x4_t*>(src + base);
+    const int n4 = dim >> 2;
+    const bool cached = n4 <= R * kBlock;
+    f32x4_t keep[R];
+    float m = 0.0f;
+    if (cached) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int i = threadIdx.x + r * kBlock;
+            keep[r] = i < n4 ? s4[i] : f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) m = amax(m, fabsf(keep[r][j]));
+        }
+    } else {
+        for (int i = threadIdx.x; i < n4; i += kBlock) {
+            const f32x4_t v = s4[i];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) m = amax(m, fabsf(v[j]));
+        }
+    }
+    m = block_max(m);
+    const float qmax = FP8 ? 448.0f : 127.0f;
+    const float scale = (m > 0.0f) ? m / qmax : 1.0f;
+    const float inv = 1.0f / scale;
+    uint32_t* d4 = reinterpret_cast<uint32_t*>(dst + base);
+    auto put = [&](int i, const f32x4_t& v) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) w |= static_cast<uint32_t>(quant_mul<FP8>(v[j], inv)) << (8 * j);
+        d4[i] = w;
+    };
+    if (cached) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int i = threadIdx.x + r * kBlock;
+            if (i < n4) put(i, keep[r]);
+        }
+    } else {
+        for (int i = threadIdx.x; i < n4; i += kBlock) put(i, s4[i]);
+    }
+    if (threadIdx.x == 0) scales[blockIdx.x] = scale;
+}
+
 // bf16 rows whose length is a multiple of 8: 16-byte loads, the row is read
 // twice (the second pass hits in L2), 8-byte stores.
 template <bool FP8>
@@ -336,6 +389,12 @@ int quantize_per_row(const T* src, uint8_t* dst, float* scales, int rows, int di
     if constexpr (sizeof(T) == 2) {
         if (vec) {
             quant_per_row_bf16_vec_kernel<FP8><<<rows, kBlock, 0, s>>>(src, dst, scales, dim);
+            return check_launch(who);
+        }
+    } else {
+        if (dim % 4 == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0 &&
+            (reinterpret_cast<uintptr_t>(dst) & 3) == 0) {
+            quant_per_row_f32_vec_kernel<FP8><<<rows, kBlock, 0, s>>>(src, dst, scales, dim);
             return check_launch(who);
         }
     }
