@@ -460,7 +460,7 @@ def main() -> int:
                    "bytes_per_step": w4["bytes_per_call"]},
         "roofline": {"bound": "hbm", "achieved": round(w4["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(w4["hbm_frac"], 4), "traffic": traffic,
-                     "kernel": "w4_decode_kernel", "algorithmic_bytes": w4["bytes_per_call"],
+                     "kernel": "w4_decode_i8_kernel", "algorithmic_bytes": w4["bytes_per_call"],
                      "us_per_launch": round(w4["us_per_call"], 3)},
         "w8a8_prefill": [
             {"M": r["M"], "K": r["K"], "N": r["N"], "us_per_call": round(r["us_per_call"], 2),

@@ -70,6 +70,17 @@ __device__ __forceinline__ int group_of_c(int kt, int s, uint32_t gmul) {
     else return kt;
 }
 
+// The group of a segment as read from the scale / zero arrays: with G < 128
+// and K % 128 != 0 the last K tile has segments past K (their activations
+// are zero), and their scale and zero point are read from the last group so
+// every load stays inside the arrays.
+template <int BPS, bool GBIG>
+__device__ __forceinline__ int seg_group(int kt, int s, const W4Args& p) {
+    const int g = group_of_c<BPS, GBIG>(kt, s, p.gmul);
+    if constexpr (BPS < 4) return min(g, p.NG - 1);
+    else return g;
+}
+
 // Map blockIdx.y of a grouped launch to (group, first row, row end): groups
 // take ceil(rows/RB) row blocks each, in order.  Offsets are clamped to
 // [0, row_capacity] so a malformed table can never index outside A or C.
@@ -192,7 +203,7 @@ __global__ __launch_bounds__(64 * WAVES) void w4_gemv_kernel(W4Args p) {
                 xs = mfma_bf16_16x16x32(ah[j], ones, xs);
                 if constexpr (F32A) xs = mfma_bf16_16x16x32(al[j], ones, xs);
             }
-            const int g = group_of<BPS>(kt, s, p.gmul);
+            const int g = (BPS < 4) ? min(group_of<BPS>(kt, s, p.gmul), p.NG - 1) : group_of<BPS>(kt, s, p.gmul);
 #pragma unroll
             for (int t = 0; t < T; ++t) {
                 f32x4_t acc_t = {0.f, 0.f, 0.f, 0.f};
@@ -344,7 +355,7 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512, (F32A || T == 2) ? 1 : 4) void
             for (int t = 0; t < T; ++t) {
 #pragma unroll
                 for (int s = 0; s < SEGS; ++s) {
-                    const uint32_t off = static_cast<uint32_t>(group_of_c<BPS, GBIG>(kt, s, p.gmul) * 16 * (ASYM ? 2 : 4)) + s_col;
+                    const uint32_t off = static_cast<uint32_t>(seg_group<BPS, GBIG>(kt, s, p) * 16 * (ASYM ? 2 : 4)) + s_col;
                     P.sw[i][t][s] = *reinterpret_cast<const uint32_t*>(scb[t] + off);
                 }
                 P.w[i][t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(
@@ -447,7 +458,7 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512, (F32A || T == 2) ? 1 : 4) void
                         xs = mfma_bf16_16x16x32(ah[s * BPS + jj], ones, xs);
                         if constexpr (F32A) xs = mfma_bf16_16x16x32(al[s * BPS + jj], ones, xs);
                     }
-                    const int g = group_of_c<BPS, GBIG>(kt, s, p.gmul);
+                    const int g = seg_group<BPS, GBIG>(kt, s, p);
 #pragma unroll
                     for (int t = 0; t < T; ++t) {
                         f32x4_t tt = {0.f, 0.f, 0.f, 0.f};
@@ -516,6 +527,351 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512, (F32A || T == 2) ? 1 : 4) void
         float sum = 0.0f;
         for (int w2 = 0; w2 < S; ++w2) sum += red[((w2 * T + t) * MR + r) * 64 + ln];
         store(t, r, ln, sum);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Integer decode kernel (M <= 4 rows; G = 64 or a multiple of 128).
+//
+// The workgroup converts its activation rows once, into LDS, to fixed point
+// per 128-wide K block: q = round(x * 2^-E), with E taken from the block's
+// largest magnitude so that |q| < 2^21, written as three signed base-256
+// digits q = d0 + 256 d1 + 65536 d2 (d0, d1 in [-128, 127], |d2| <= 32).
+// The 4-bit codes u (0..15) are int8 operands after one mask (and a shift),
+// so the dot products run on v_mfma_i32_16x16x64_i8: A row 4p + r is digit
+// plane p of activation row r, and accumulator rows 4p + r come out as the
+// exact sums S_p = sum_k d_p[k] u[k].  Per block and scale segment,
+//     sum_k x[k] (u[k] - z) = 2^E (S_0 + 256 S_1 + 65536 S_2 - z XS),
+// XS = sum_k q[k] being an exact integer sum taken during the conversion.
+// Lane group p of the accumulator layout holds plane p, so each lane adds
+// s 2^E (w_p S_p - [p == 0] z XS) to its own fp32 accumulator (w = 1, 256,
+// 65536; lane group 3 weighs 0) and the planes meet once, in the final
+// cross-wave reduction.  Per 1 KiB weight tile and column tile that is 12
+// decode instructions and two MFMAs, against 28 and four (plus the
+// activation-sum MFMAs) for the bf16 form.
+// Precision: a bf16 activation within 2^-13 of its block's largest is
+// represented exactly, anything smaller (and any fp32 activation) to within
+// 2^-21 of that largest; a block holding Inf or NaN makes its row's
+// outputs NaN.
+//
+// LDS: digit planes [3][Ml][Kp] bytes, each row in MFMA operand order (the
+// 16 bytes lane l reads for MFMA m of tile kt are k = 128 kt + 64 m + 32 h
+// + 8 (l >> 4) + e, h = 0, 1, e = 0..7: the codes of the prepacked weight
+// dwords 2m and 2m + 1 of that lane), then one float4 per (row, K tile):
+// {2^E, 2^E XS(first 64-wide segment or whole tile), 2^E XS(second), 0}.
+// Passes, loads and the wave-ordered reduction follow the bf16 decode kernel.
+// ---------------------------------------------------------------------------
+constexpr float kQMagic = 12615808.0f;         // 1.5 * 2^23 + 0x8080
+constexpr uint32_t kQMagicBits = 0x4B408080u;  // bits of (kQMagic + q) for |q| < 2^22
+constexpr uint32_t kNib = 0x0F0F0F0Fu;
+
+__device__ __forceinline__ uint32_t umax32(uint32_t a, uint32_t b) { return a > b ? a : b; }
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp(uint32_t x) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), CTRL, 0xf, 0xf, false));
+}
+// All-reduce over the 16 lanes of a DPP row (row_ror 8, 4, 2, 1) and over
+// each half row (quad_perm xor 1, xor 2, then row_half_mirror).
+__device__ __forceinline__ uint32_t row16_max(uint32_t x) {
+    x = umax32(x, dpp<0x128>(x));
+    x = umax32(x, dpp<0x124>(x));
+    x = umax32(x, dpp<0x122>(x));
+    return umax32(x, dpp<0x121>(x));
+}
+__device__ __forceinline__ uint32_t row16_sum(uint32_t x) {
+    x += dpp<0x128>(x);
+    x += dpp<0x124>(x);
+    x += dpp<0x122>(x);
+    return x + dpp<0x121>(x);
+}
+__device__ __forceinline__ uint32_t row8_sum(uint32_t x) {
+    x += dpp<0xB1>(x);
+    x += dpp<0x4E>(x);
+    return x + dpp<0x141>(x);
+}
+
+template <bool F32A, bool ASYM, bool F32C, int T, int NPW, int BPS, bool GBIG, int MR>
+__global__ __launch_bounds__(T == 1 ? 1024 : 512) void w4_decode_i8_kernel(W4Args p) {
+    static_assert(BPS == 2 || BPS == 4, "scale segments of 64 or 128 k");
+    static_assert(NPW == 4 || NPW == 8, "passes start at multiples of NPW tiles");
+    static_assert(MR == 1 || MR == 4, "one row or all four");
+    constexpr int SEGS = 4 / BPS;
+    constexpr int NZW = (BPS < 4) ? (NPW * SEGS + 7) / 8 : (GBIG ? NPW : 1);
+    extern __shared__ __attribute__((aligned(16))) uint8_t q_lds[];
+
+    const int S = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int z = blockIdx.z;
+    const int Ml = min(p.M, 4);
+    const int col = lane & 15;
+    const int Kp = p.Kt * kW4TileK;
+    uint8_t* const dig = q_lds;
+    float4* const tab = reinterpret_cast<float4*>(q_lds + 3 * Ml * Kp);
+
+    const uint8_t* qwb[T];
+    const char* scb[T];
+    const char* zwb[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        const int64_t nt = min(static_cast<int>(blockIdx.x) * T + t, p.Nt - 1);
+        qwb[t] = p.qw + z * p.qw_bs + nt * p.Kt * kW4TileBytes;
+        scb[t] = static_cast<const char*>(p.scales) + (z * p.s_bs + nt * p.NG * 16) * (ASYM ? 2 : 4);
+        zwb[t] = ASYM ? reinterpret_cast<const char*>(p.zeros + z * p.z_bs + nt * p.NG8 * 16) : nullptr;
+    }
+    const uint32_t s_col = static_cast<uint32_t>(col * (ASYM ? 2 : 4));
+
+    struct Pass {
+        u32x4_t w[NPW][T];
+        uint32_t sw[NPW][T][SEGS];
+        uint32_t zw[NZW][T];
+    };
+    auto issue = [&](Pass& P, int kt0) {
+        if constexpr (ASYM) {
+#pragma unroll
+            for (int q = 0; q < NZW; ++q) {
+                const int g = (BPS < 4) ? group_of_c<BPS, GBIG>(min(kt0, p.Kt - 1), 0, 0) + 8 * q
+                                        : group_of_c<BPS, GBIG>(min(kt0 + q, p.Kt - 1), 0, p.gmul);
+                const uint32_t off = static_cast<uint32_t>((min(g >> 3, p.NG8 - 1) * 16 + col) * 4);
+#pragma unroll
+                for (int t = 0; t < T; ++t) P.zw[q][t] = *reinterpret_cast<const uint32_t*>(zwb[t] + off);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NPW; ++i) {
+            const int kt = min(kt0 + i, p.Kt - 1);
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+#pragma unroll
+                for (int s = 0; s < SEGS; ++s) {
+                    const uint32_t off = static_cast<uint32_t>(seg_group<BPS, GBIG>(kt, s, p) * 16 * (ASYM ? 2 : 4)) + s_col;
+                    if constexpr (ASYM) P.sw[i][t][s] = *reinterpret_cast<const uint16_t*>(scb[t] + off);
+                    else P.sw[i][t][s] = *reinterpret_cast<const uint32_t*>(scb[t] + off);
+                }
+                P.w[i][t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(
+                    qwb[t] + static_cast<uint32_t>(kt * kW4TileBytes + lane * 16)));
+            }
+        }
+    };
+
+    // 1. activations: loads first, then the first pass's weights, then the
+    //    conversion (the weights are in flight meanwhile)
+    const int span = S * NPW;
+    const int rc = Kp >> 3;  // 8-element chunks per padded row; 16 per K tile
+    const int chunks = Ml * rc;
+    const char* A = static_cast<const char*>(p.A) + z * p.a_bs * (F32A ? 4 : 2);
+    constexpr int B = 4;  // chunks per thread per batch
+    u32x4_t av[B], av2[B];
+    auto stage_load = [&](int c0) {
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const int c = c0 + b * 64 * S;
+            const int r = c / rc, k = (c - r * rc) * 8;
+            const bool ok = c < chunks && k < p.K;
+            const int64_t e = ok ? static_cast<int64_t>(r) * p.K + k : 0;
+            if constexpr (F32A) {
+                av[b] = *reinterpret_cast<const u32x4_t*>(A + e * 4);
+                av2[b] = *reinterpret_cast<const u32x4_t*>(A + e * 4 + 16);
+            } else {
+                av[b] = *reinterpret_cast<const u32x4_t*>(A + e * 2);
+            }
+        }
+    };
+    // Chunk c (row r, k = kk .. kk+7) -> digits.  Chunks are dealt to
+    // consecutive threads and a K tile is 16 chunks, so each DPP row of 16
+    // lanes holds exactly one (row, K tile) block, valid or past the end as a
+    // whole: the block reductions are row reductions.
+    auto stage_store = [&](int c0) {
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const int c = c0 + b * 64 * S;
+            const int r = c / rc, kk = (c - r * rc) * 8;
+            // a chunk past K (the zero padding of the last tile) or past the
+            // last row holds whatever the clamped load read: it takes no part
+            // in the block maximum and is scaled by 0 (q = 0); only non-finite
+            // values there could leak, and those sit in row 0, whose outputs
+            // are then NaN anyway
+            const bool ok = c < chunks && kk < p.K;
+            float f[8];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                if constexpr (F32A) {
+                    f[i] = __uint_as_float(av[b][i]);
+                    f[i + 4] = __uint_as_float(av2[b][i]);
+                } else {
+                    f[2 * i] = __uint_as_float(av[b][i] << 16);
+                    f[2 * i + 1] = __uint_as_float(av[b][i] & 0xffff0000u);
+                }
+            }
+            uint32_t mx = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) mx = umax32(mx, __float_as_uint(f[i]) & 0x7fffffffu);
+            mx = row16_max(ok ? mx : 0u);
+            const int be = static_cast<int>(mx >> 23);  // 255: Inf or NaN in the block
+            const int E = min(max(be - 147, -126), 107);
+            const float inv = ok ? __uint_as_float(static_cast<uint32_t>(127 - E) << 23) : 0.0f;
+            // q = round(f * 2^-E): bits(kQMagic + f*2^-E) = kQMagicBits + q, so
+            // d = bits - 0x4B400000 = q + 0x8080, whose byte 2 is the top digit
+            // and whose bytes 0, 1 are the low digits + 128 (re-biased below,
+            // four at a time, once they are packed into planes)
+            uint32_t d[8], vs = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                d[i] = __float_as_uint(__builtin_fmaf(f[i], inv, kQMagic)) - 0x4B400000u;
+                vs += d[i];
+            }
+            uint32_t pl[3][2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t* e = d + 4 * h;
+                const uint32_t x01 = __builtin_amdgcn_perm(e[1], e[0], 0x05010400u);
+                const uint32_t x23 = __builtin_amdgcn_perm(e[3], e[2], 0x05010400u);
+                const uint32_t y01 = __builtin_amdgcn_perm(e[1], e[0], 0x06020602u);
+                const uint32_t y23 = __builtin_amdgcn_perm(e[3], e[2], 0x06020602u);
+                pl[0][h] = __builtin_amdgcn_perm(x23, x01, 0x05040100u) ^ 0x80808080u;
+                pl[1][h] = __builtin_amdgcn_perm(x23, x01, 0x07060302u) ^ 0x80808080u;
+                pl[2][h] = __builtin_amdgcn_perm(y23, y01, 0x05040100u);
+            }
+            const int pos = (kk & ~63) + 16 * ((kk >> 3) & 3) + 8 * ((kk >> 5) & 1);
+            if (c < chunks) {
+#pragma unroll
+                for (int pp = 0; pp < 3; ++pp)
+                    *reinterpret_cast<u32x2_t*>(dig + (pp * Ml + r) * Kp + pos) = u32x2_t{pl[pp][0], pl[pp][1]};
+            }
+            const uint32_t xs = vs - 8u * 0x8080u;  // this chunk's sum of q
+            const float sc = (be == 255) ? __uint_as_float(0x7fc00000u)
+                                         : __uint_as_float(static_cast<uint32_t>(127 + E) << 23);
+            float4 tv;
+            if constexpr (BPS == 4) {
+                const uint32_t x16 = row16_sum(xs);
+                tv = float4{sc, static_cast<float>(static_cast<int>(x16)) * sc, 0.0f, 0.0f};
+            } else {
+                const uint32_t x8 = row8_sum(xs);
+                const uint32_t x8b = dpp<0x128>(x8);  // the second half row's sum
+                tv = float4{sc, static_cast<float>(static_cast<int>(x8)) * sc,
+                            static_cast<float>(static_cast<int>(x8b)) * sc, 0.0f};
+            }
+            if ((lane & 15) == 0 && c < chunks) tab[r * p.Kt + (kk >> 7)] = tv;
+        }
+    };
+    const int kb0 = wave * NPW;
+    stage_load(threadIdx.x);
+    Pass pa, pb;
+    issue(pa, kb0);
+    stage_store(threadIdx.x);
+    for (int c0 = threadIdx.x + B * 64 * S; c0 < chunks; c0 += B * 64 * S) {
+        stage_load(c0);
+        stage_store(c0);
+    }
+    __syncthreads();
+
+    // 2. main loop.  A row (lane & 15) = 4p + r reads digit plane p of row r
+    //    (plane 3 does not exist: those rows read plane 2 and weigh 0; rows
+    //    r >= M read row M-1, their outputs are never stored)
+    const int g4 = lane >> 4;
+    const float wl = g4 == 0 ? 1.0f : (g4 == 1 ? 256.0f : (g4 == 2 ? 65536.0f : 0.0f));
+    const float zl = g4 == 0 ? 1.0f : 0.0f;
+    const uint8_t* const abase =
+        dig + (min((lane & 15) >> 2, 2) * Ml + min(lane & 3, Ml - 1)) * Kp + 16 * g4;
+    float acc[T][MR];
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int j = 0; j < MR; ++j) acc[t][j] = 0.0f;
+
+    auto tile = [&](const Pass& P, int i, int kt) {
+        const u32x4_t a0 = *reinterpret_cast<const u32x4_t*>(abase + kt * kW4TileK);
+        const u32x4_t a1 = *reinterpret_cast<const u32x4_t*>(abase + kt * kW4TileK + 64);
+        float W[MR], Z0[MR], Z1[MR];
+#pragma unroll
+        for (int j = 0; j < MR; ++j) {
+            const float4 tb = tab[min(j, Ml - 1) * p.Kt + kt];
+            W[j] = wl * tb.x;
+            Z0[j] = zl * tb.y;
+            Z1[j] = zl * tb.z;
+        }
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const u32x4_t w = P.w[i][t];
+            const u32x4_t b0 = {w[0] & kNib, (w[0] >> 4) & kNib, w[1] & kNib, (w[1] >> 4) & kNib};
+            const u32x4_t b1 = {w[2] & kNib, (w[2] >> 4) & kNib, w[3] & kNib, (w[3] >> 4) & kNib};
+            const i32x4_t zero4 = {0, 0, 0, 0};
+            i32x4_t sv[SEGS];
+            if constexpr (BPS == 4) {
+                sv[0] = mfma_i8_16x16x64(a1, b1, mfma_i8_16x16x64(a0, b0, zero4));
+            } else {
+                sv[0] = mfma_i8_16x16x64(a0, b0, zero4);
+                sv[1] = mfma_i8_16x16x64(a1, b1, zero4);
+            }
+#pragma unroll
+            for (int s = 0; s < SEGS; ++s) {
+                const int g = seg_group<BPS, GBIG>(kt, s, p);
+                float sc, zc;
+                if constexpr (ASYM) {
+                    sc = f16_to_f32(static_cast<uint16_t>(P.sw[i][t][s]));
+                    const uint32_t word = P.zw[(BPS < 4) ? (i * SEGS + s) / 8 : (GBIG ? i : 0)][t];
+                    zc = static_cast<float>((word >> (4 * (g & 7))) & 15u);
+                } else {
+                    sc = __uint_as_float(P.sw[i][t][s]);
+                    zc = 8.0f;  // implied zero point
+                }
+#pragma unroll
+                for (int j = 0; j < MR; ++j) {
+                    const float part = static_cast<float>(sv[s][j]) * W[j];
+                    acc[t][j] = __builtin_fmaf(sc, __builtin_fmaf(-zc, s == 0 ? Z0[j] : Z1[j], part), acc[t][j]);
+                }
+            }
+        }
+    };
+    // a full pass runs its tiles without a branch between them, so the
+    // compiler can overlap one tile's MFMA latency with the next tile's decode
+    auto consume = [&](const Pass& P, int kb) {
+        const int n = min(NPW, p.Kt - kb);
+        if (n == NPW) {
+#pragma unroll
+            for (int i = 0; i < NPW; ++i) tile(P, i, kb + i);
+        } else {
+#pragma unroll
+            for (int i = 0; i < NPW; ++i)
+                if (i < n) tile(P, i, kb + i);
+        }
+    };
+    const int np = (p.Kt - kb0 + span - 1) / span;
+    int q = 0;
+    for (; q + 2 < np; q += 2) {
+        issue(pb, kb0 + (q + 1) * span);
+        consume(pa, kb0 + q * span);
+        issue(pa, kb0 + (q + 2) * span);
+        consume(pb, kb0 + (q + 1) * span);
+    }
+    if (q + 1 < np) {
+        issue(pb, kb0 + (q + 1) * span);
+        consume(pa, kb0 + q * span);
+        consume(pb, kb0 + (q + 1) * span);
+    } else {
+        consume(pa, kb0 + q * span);
+    }
+
+    // 3. red[wave][t][j][lane]; output (row j, column c) sums the waves in
+    //    order, then the three digit-plane lane groups
+    float* const red = reinterpret_cast<float*>(q_lds);
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int j = 0; j < MR; ++j) red[((wave * T + t) * MR + j) * 64 + lane] = acc[t][j];
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < T * MR * 16; idx += 64 * S) {
+        const int t = idx / (MR * 16), j = (idx / 16) % MR, c = idx & 15;
+        float sum = 0.0f;
+        for (int w2 = 0; w2 < S; ++w2) {
+            const float* rp = red + ((w2 * T + t) * MR + j) * 64 + c;
+            sum += rp[0] + rp[16] + rp[32];
+        }
+        const int ntt = static_cast<int>(blockIdx.x) * T + t;
+        const int cn = ntt * kW4TileN + c;
+        if (j < p.M && cn < p.N && ntt < p.Nt)
+            w4_store<F32C>(p, z * p.c_bs + static_cast<int64_t>(j) * p.N + cn, sum);
     }
 }
 
@@ -721,7 +1077,8 @@ __global__ __launch_bounds__(256, 2) void w4_mma_kernel(W4Args p) {
 constexpr int kDecodeMaxLds = 64 * 1024;  // activation bytes a decode workgroup may stage
 
 // Tuning knobs (read once; unset = heuristic):
-//   LHQ_W4_DECODE=-1 disables the decode kernel;
+//   LHQ_W4_I8=-1 disables the integer decode kernel (M <= 4);
+//   LHQ_W4_DECODE=-1 disables the bf16 decode kernel;
 //   LHQ_W4_DEC_T (1|2), LHQ_W4_DEC_NPW (4|8 tiles per wave per pass) and
 //   LHQ_W4_DEC_S (waves per workgroup, 1..16) shape it;
 //   LHQ_W4_TILES (1|2), LHQ_W4_WAVES (1|2|4|8) shape the generic kernel.
@@ -756,6 +1113,14 @@ void launch_gemv_bps(const W4Args& a, dim3 grid, int bps, hipStream_t s) {
         case 2: w4_gemv_kernel<F32A, ASYM, F32C, T, WAVES, 2, GR><<<grid, 64 * WAVES, 0, s>>>(a); break;
         default: w4_gemv_kernel<F32A, ASYM, F32C, T, WAVES, 4, GR><<<grid, 64 * WAVES, 0, s>>>(a); break;
     }
+}
+
+template <bool F32A, bool ASYM, bool F32C, int T, int NPW, int MR>
+void launch_i8_mr(const W4Args& a, dim3 grid, int S, size_t lds, hipStream_t s) {
+    lds = std::max(lds, static_cast<size_t>(S) * T * MR * 64 * sizeof(float));  // the reduction reuses it
+    if (a.G == 64) w4_decode_i8_kernel<F32A, ASYM, F32C, T, NPW, 2, false, MR><<<grid, 64 * S, lds, s>>>(a);
+    else if (a.gmul) w4_decode_i8_kernel<F32A, ASYM, F32C, T, NPW, 4, true, MR><<<grid, 64 * S, lds, s>>>(a);
+    else w4_decode_i8_kernel<F32A, ASYM, F32C, T, NPW, 4, false, MR><<<grid, 64 * S, lds, s>>>(a);
 }
 
 template <bool F32A, bool ASYM, bool F32C, int T, bool GR>
@@ -803,8 +1168,33 @@ int launch_w4(W4Args a, int batch, hipStream_t s, int mblocks = -1) {
     static const int env_np = env_int("LHQ_W4_DEC_NPW");
     static const int env_t = env_int("LHQ_W4_TILES");
     static const int env_w = env_int("LHQ_W4_WAVES");
+    static const int env_i8 = env_int("LHQ_W4_I8");
     if (mblocks < 0) mblocks = ceil_div(a.M, 16);
     const int bps = a.G >= 128 ? 4 : a.G / 32;
+
+    // Integer-MFMA decode: one row (the kernel handles up to 4, but each
+    // workgroup converts its rows' activations, and measured at M = 4 that
+    // costs more than the bf16 kernel's decode: 11.9 vs 8.9 us at K=4096,
+    // N=11008), G = 64 or a multiple of 128, digit planes and block table
+    // within the LDS budget (LHQ_W4_I8=-1 disables).
+    const size_t i8_lds = static_cast<size_t>(a.Kt) * (3 * kW4TileK + 16);
+    if (!GR && mblocks == 1 && a.M == 1 && env_i8 >= 0 && (a.G == 64 || a.G % kW4TileK == 0) &&
+        i8_lds <= static_cast<size_t>(kDecodeMaxLds)) {
+        // one column tile per wave: measured at K=8192, N=28672 (1792 column
+        // tiles) 21.7 us against 22.4 us with two
+        int T = 1;
+        if (env_dt == 1 || env_dt == 2) T = env_dt;
+        const int smax = (T == 1) ? 16 : 8;  // the kernel's launch bounds
+        const int64_t cols = static_cast<int64_t>(ceil_div(a.Nt, T)) * batch;
+        int S = 4;
+        while (S < smax && cols * S < 2048) S *= 2;
+        S = max(1, min(S, ceil_div(a.Kt, 4)));
+        if (env_ds >= 1 && env_ds <= smax) S = env_ds;
+        dim3 grid(ceil_div(a.Nt, T), 1, batch);
+        if (T == 1) launch_i8_mr<F32A, ASYM, F32C, 1, 4, 1>(a, grid, S, i8_lds, s);
+        else launch_i8_mr<F32A, ASYM, F32C, 2, 4, 1>(a, grid, S, i8_lds, s);
+        return check_launch("w4a16 decode (int8 MFMA)");
+    }
 
     const size_t dec_lds = static_cast<size_t>(min(a.M, 16)) * a.Kt * kW4TileK * (F32A ? 4 : 2);
     if (!GR && mblocks == 1 && env_dec >= 0 && dec_lds <= static_cast<size_t>(kDecodeMaxLds)) {

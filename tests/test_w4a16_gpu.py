@@ -117,6 +117,62 @@ def test_w4a16_bf16_ragged_k(oracle, ops, M, K, N, G):
     assert rel_frobenius(got, want) <= TOL_BF16
 
 
+# M = 1 with G = 64 or a multiple of 128 runs the integer-MFMA decode kernel,
+# which holds activations as 21-bit fixed point per 128-wide K block.  These
+# inputs spread magnitudes over 2^-12 .. 2^12 inside every block and zero a
+# whole block, with one and two column tiles per wave (Nt < 1024 and >= 1024,
+# odd Nt), G = 64 (also with a ragged last K tile), 128 and 256.
+INT8_DECODE_CASES = [
+    (1, 4096, 16400, 128),
+    (1, 1024, 272, 64),
+    (1, 4160, 72, 64),
+    (1, 2048, 16400, 256),
+    (1, 640, 48, 64),
+]
+
+
+def _wide_range(M, K, seed):
+    x = D.normal((M, K), 1.0, seed) * np.exp2(D.uniform((M, K), -12, 12, seed + 7)).astype(np.float32)
+    x[:, 128:256] = 0.0  # one all-zero block per row
+    return x.astype(np.float32)
+
+
+@pytest.mark.parametrize("M,K,N,G", INT8_DECODE_CASES)
+def test_w4a16_int8_decode_bf16_wide_range(oracle, ops, M, K, N, G):
+    A = D.to_bf16_bits(oracle, _wide_range(M, K, 40 + M))
+    p, s, z = oracle.q4a_quantize_groupwise(D.normal((K, N), 0.02, 41 + M), G)
+    want = oracle.gemm_w4a16_asym(A, p, s, z, N, G)
+    w = ops.prepack_w4_asym(ops.dev(p), ops.dev(s), ops.dev(z), K, N, G)
+    got = D.bf16_bits_to_f32(ops.host(ops.gemm_w4a16_bf16(ops.dev(A), w), np.uint16))
+    assert rel_frobenius(got, want) <= TOL_BF16
+
+
+@pytest.mark.parametrize("M,K,N,G", INT8_DECODE_CASES)
+def test_w4a16_int8_decode_f32_wide_range(oracle, ops, M, K, N, G):
+    A = _wide_range(M, K, 50 + M)
+    Bp, Bs = oracle.q4_quantize_groupwise(D.uniform((K, N), -1, 1, 51 + M), G)
+    want = oracle.gemm_w4a16_groupwise(A, Bp, Bs, N, G)
+    w = ops.prepack_w4_sym(ops.dev(Bp), ops.dev(Bs), K, N, G)
+    C = ops.dev(np.zeros((M, N), np.float32))
+    ops.gemm_w4a16(ops.dev(A), w, C, 1.0, 0.0)
+    assert rel_frobenius(ops.host(C), want) <= TOL_F32
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 8192, 2048), (1, 4096, 1040)])
+def test_w4a16_int8_decode_correctly_rounded(oracle, ops, M, K, N):
+    """N(0,1) activations are exact in the fixed-point form: the bf16 output
+    is the correctly rounded value up to one ulp."""
+    G = 128
+    A = D.to_bf16_bits(oracle, D.normal((M, K), 1.0, 61))
+    p, s, z = oracle.q4a_quantize_groupwise(D.normal((K, N), 0.02, 62), G)
+    want = oracle.gemm_w4a16_asym(A, p, s, z, N, G)
+    w = ops.prepack_w4_asym(ops.dev(p), ops.dev(s), ops.dev(z), K, N, G)
+    got = D.bf16_bits_to_f32(ops.host(ops.gemm_w4a16_bf16(ops.dev(A), w), np.uint16))
+    want_b = D.bf16_bits_to_f32(D.to_bf16_bits(oracle, want))
+    ulp = np.abs(want_b) * 2.0 ** -7 + 1e-30
+    assert (np.abs(got - want_b) <= ulp).mean() > 0.999
+
+
 def test_w4a16_bf16_batched(oracle, ops):
     import torch
     B, M, K, N, G = 3, 5, 512, 80, 128
