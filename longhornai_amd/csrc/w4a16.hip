@@ -13,14 +13,17 @@
 // fp32 activations are split into bf16 hi + lo (two MFMAs), which keeps the
 // product error near 2^-17 relative.
 //
-// Two kernels share that arithmetic:
+// Three kernels share that arithmetic:
 //   w4_decode_kernel -- M <= 16 with the activations small enough to stage in
 //     LDS: a streaming GEMV whose only global loads in the main loop are the
-//     weight tiles and their scales / zero points (a D-deep ring per wave).
+//     weight tiles and their scales / zero points.
 //   w4_gemv_kernel   -- any M in 16-row blocks, uniform batches and ragged
 //     grouped launches (device-side group table).
-// Both split K over the waves of a workgroup and reduce through LDS in wave
-// order, so results are deterministic.
+//   w4_mma_kernel    -- bf16 prefill tiles (many rows per weight tile).
+// w4_decode_i8_kernel (M = 1) computes the same sums on the int8 MFMA, with
+// the activations as exact fixed-point digit planes (see its comment).
+// The GEMV kernels split K over the waves of a workgroup and reduce through
+// LDS in wave order, so results are deterministic.
 #include <algorithm>
 #include <cstdlib>
 #include <type_traits>
