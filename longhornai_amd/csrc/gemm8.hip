@@ -51,13 +51,7 @@ struct Gemm8Args {
 // range of tile ids, and walk tile ids in groups of `group_m` tile rows
 // (column-major inside a group) so concurrently running tiles share A rows
 // and B columns.
-__device__ __forceinline__ void tile_of(int b, const Gemm8Args& p, int& tm, int& tn) {
-    // XCD x receives blocks x, x+8, ...: q + (x < r) of them; hand it the
-    // contiguous id range starting at x*q + min(x, r) (a bijection).
-    const int total = p.tiles_m * p.tiles_n;
-    const int q = total / 8, r = total % 8;
-    const int xcd = b % 8, slot = b / 8;
-    const int id = xcd * q + min(xcd, r) + slot;
+__device__ __forceinline__ void tile_of_id(int id, const Gemm8Args& p, int& tm, int& tn) {
     const int gm = p.group_m;
     const int per_group = gm * p.tiles_n;
     const int group = id / per_group;
@@ -66,6 +60,14 @@ __device__ __forceinline__ void tile_of(int b, const Gemm8Args& p, int& tm, int&
     const int in = id - group * per_group;
     tm = first + in % rows;
     tn = in / rows;
+}
+__device__ __forceinline__ void tile_of(int b, const Gemm8Args& p, int& tm, int& tn) {
+    // XCD x receives blocks x, x+8, ...: q + (x < r) of them; hand it the
+    // contiguous id range starting at x*q + min(x, r) (a bijection).
+    const int total = p.tiles_m * p.tiles_n;
+    const int q = total / 8, r = total % 8;
+    const int xcd = b % 8, slot = b / 8;
+    tile_of_id(xcd * q + min(xcd, r) + slot, p, tm, tn);
 }
 
 // Epilogue shared by the 8-bit kernels: scale, apply beta and store the
@@ -212,34 +214,37 @@ __device__ __forceinline__ void gemm8_store(const Gemm8Args& p, const Acc (&acc)
 // clamped to the last row / column).  EDGE: the tile crosses M or N (or
 // rows are not 16-byte aligned); rows and columns are tested and partial
 // column groups stored element by element.
+// JB: 32-column accumulator blocks per wave (4: a 128x128 quadrant of a
+// 256x256 tile; 2: a 128x64 quadrant of a 256x128 half tile).
 constexpr int STAGED_PITCH = 4 * (128 + 4);
 
-template <int EPI, bool EDGE>
+template <int EPI, bool EDGE, int JB = 4>
 __device__ __forceinline__ void gemm8_store_staged(const Gemm8Args& p, const i32x16_t (&acc)[4][4], int m0, int n0,
                                                    int wm, int wn, int lane, const float* ls, uint8_t* area) {
+    constexpr int WQ = 32 * JB;                   // quadrant width
     constexpr int CPL = EPI == EPI_BF16 ? 8 : 4;  // columns per lane (16 output bytes)
-    constexpr int LPR = 128 / CPL;                // lanes per row: 16 or 32
-    constexpr int RPP = 64 / LPR;                 // rows per pass: 4 or 2
+    constexpr int LPR = WQ / CPL;                 // lanes per row
+    constexpr int RPP = 64 / LPR;                 // rows per pass
     const int lr = lane & 31, lh = lane >> 5;
     const int rsub = lane / LPR, cl = lane % LPR;
     float bsc[CPL];  // B_s of the lane's columns
     if constexpr (EPI != EPI_I32) {
 #pragma unroll
         for (int c = 0; c < CPL; c += 4) {
-            const f32x4_t v = *reinterpret_cast<const f32x4_t*>(ls + BM + wn * 128 + cl * CPL + c);
+            const f32x4_t v = *reinterpret_cast<const f32x4_t*>(ls + BM + wn * WQ + cl * CPL + c);
 #pragma unroll
             for (int r = 0; r < 4; ++r) bsc[c + r] = v[r];
         }
     }
     // this wave's quadrant of C, 32-bit element offsets from its first element
-    const size_t quad_off = static_cast<size_t>(m0 + wm * 128) * p.N + n0 + wn * 128;
+    const size_t quad_off = static_cast<size_t>(m0 + wm * 128) * p.N + n0 + wn * WQ;
     const bool beta0 = p.beta == 0.0f;
-    const int cols_left = p.N - (n0 + wn * 128 + cl * CPL);  // in-range columns from the lane's first
+    const int cols_left = p.N - (n0 + wn * WQ + cl * CPL);  // in-range columns from the lane's first
     const bool vec_ok = !EDGE || (p.c_vec && cols_left >= CPL && p.N % CPL == 0);
     // 1. raw accumulators of block i, row lr, columns 32j + 4lh + 8q ..+3
     auto stage_block = [&](int i) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < JB; ++j)
 #pragma unroll
             for (int q = 0; q < 4; ++q)
                 *reinterpret_cast<i32x4_t*>(area + lr * STAGED_PITCH + (j * 32 + 4 * lh + 8 * q) * 4) =
@@ -521,81 +526,89 @@ constexpr int DS_SCALE_BYTES = (BM + BN) * 4;                 // int8 scales of 
 
 #define LHQ_LDS_AS __attribute__((address_space(3)))
 
-template <int EPI, int STAGES>
-__global__ __launch_bounds__(NTHREADS) void gemm8_dma_kernel(Gemm8Args p) {
-    static_assert(STAGES >= 3 && DS_DMA_PER_STAGE * (STAGES - 2) <= 63, "vmcnt range");
+// One output tile of BM rows x 64*JB columns (JB = 4: the full 256x256
+// tile; JB = 2: a 256x128 half tile) starting at (m0, n0), with the LDS of
+// the calling workgroup.  acc is the caller's (one set of accumulator
+// registers for both tile widths; a half tile uses blocks j < 2).  Returns
+// with every LDS access of the tile complete in this wave (the caller
+// separates tiles with a barrier).
+template <int EPI, int STAGES, int JB>
+__device__ __forceinline__ void dma_tile(const Gemm8Args& p, uint8_t* ds_lds, int m0, int n0,
+                                         i32x16_t (&acc)[4][4]) {
+    constexpr int DPS = 4 + JB;  // DMAs per wave per stage: 4 of A, JB of B
+    constexpr int NT = 4 * JB;   // MFMAs per 32-deep k step
+    static_assert(STAGES >= 3 && DPS * (STAGES - 2) <= 63, "vmcnt range");
     static_assert(STAGES * 2 * DS_OP_BYTES + DS_SCALE_BYTES <= 160 * 1024, "LDS");
     static_assert(4 * 32 * STAGED_PITCH <= STAGES * 2 * DS_OP_BYTES, "epilogue staging fits the stages");
-    // Dynamic LDS: the compiler does not see the DMA as a store into it, so
-    // it may neither assume its contents nor insert its own waits for it;
-    // the rendezvous below orders every access.
-    extern __shared__ __attribute__((aligned(1024))) uint8_t ds_lds[];
     auto stage_buf = [&](int u) { return ds_lds + u * 2 * DS_OP_BYTES; };
     float* const lds_scales = reinterpret_cast<float*>(ds_lds + STAGES * 2 * DS_OP_BYTES);
 
-    int tm, tn;
-    tile_of(blockIdx.x, p, tm, tn);
-    const int m0 = tm * BM, n0 = tn * BN;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
 
-    // DMA: wave w moves operand chunks c = (4w + i)*64 + lane, i = 0..3, of
-    // each operand: row r = c >> 2, LDS slot c & 3, global chunk
-    // (c & 3) ^ ((r >> 2) & 3).
-    uint32_t a_row[4], b_src[4];
-    int kc[4];
+    // DMA: wave w moves A chunks c = (4w + i)*64 + lane (i < 4) and B chunks
+    // c = (JB*w + i)*64 + lane (i < JB): row r = c >> 2, LDS slot c & 3,
+    // global chunk (c & 3) ^ ((r >> 2) & 3).
+    uint32_t a_row[4], b_src[JB];
+    int kca[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int c = (4 * wave + i) * 64 + lane;
         const int r = c >> 2;
-        kc[i] = ((c & 3) ^ ((r >> 2) & 3)) * 16;
+        kca[i] = ((c & 3) ^ ((r >> 2) & 3)) * 16;
         a_row[i] = static_cast<uint32_t>(min(m0 + r, p.M - 1)) * static_cast<uint32_t>(p.K);
-        b_src[i] = static_cast<uint32_t>(n0 + r) * static_cast<uint32_t>(p.Kp) + static_cast<uint32_t>(kc[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < JB; ++i) {
+        const int c = (JB * wave + i) * 64 + lane;
+        const int r = c >> 2;
+        b_src[i] = static_cast<uint32_t>(n0 + r) * static_cast<uint32_t>(p.Kp) +
+                   static_cast<uint32_t>(((c & 3) ^ ((r >> 2) & 3)) * 16);
     }
     const int nk = p.Kp / DS_BK;
-    // DMA d (0..7) of stage s into buf: chunk set d >> 1 of A (d even) or B
+    // DMA d (0..DPS-1) of stage s into buf: A and B chunk sets alternate
+    // while both last (d < 2*JB), then the remaining A sets
     auto dma = [&](uint8_t* buf, int s, int d) {
-        const int i = d >> 1;
         const int k0 = min(s, nk - 1) * DS_BK;
-        if ((d & 1) == 0) {
+        const bool is_b = d < 2 * JB && (d & 1);
+        const int i = d < 2 * JB ? d >> 1 : d - JB;
+        if (!is_b) {
             // k past K: the row's last in-range 16 bytes (their product with
             // the zero-padded B is zero)
-            const uint32_t ka = static_cast<uint32_t>(min(k0 + kc[i], p.K - 16));
+            const uint32_t ka = static_cast<uint32_t>(min(k0 + kca[i], p.K - 16));
             __builtin_amdgcn_global_load_lds(p.A + (a_row[i] + ka), (LHQ_LDS_AS void*)(buf + (4 * wave + i) * 1024),
                                              16, 0, 0);
         } else {
             __builtin_amdgcn_global_load_lds(p.Bt + (b_src[i] + static_cast<uint32_t>(k0)),
-                                             (LHQ_LDS_AS void*)(buf + DS_OP_BYTES + (4 * wave + i) * 1024), 16, 0, 0);
+                                             (LHQ_LDS_AS void*)(buf + DS_OP_BYTES + (JB * wave + i) * 1024), 16, 0, 0);
         }
     };
     auto issue = [&](uint8_t* buf, int s) {
 #pragma unroll
-        for (int d = 0; d < DS_DMA_PER_STAGE; ++d) dma(buf, s, d);
+        for (int d = 0; d < DPS; ++d) dma(buf, s, d);
     };
 
-    using Acc = i32x16_t;
-    Acc acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = Acc{};
+        for (int j = 0; j < JB; ++j) acc[i][j] = i32x16_t{};
 
     // operand fragments: row (lane & 31) of each 32-row block, k chunk
     // 2*kk + (lane >> 5), swizzled by the row's (r >> 2) & 3
     const int swz = ((lane & 31) >> 2) & 3;
     const int a_base = (wm * 128 + (lane & 31)) * DS_BK;
-    const int b_base = DS_OP_BYTES + (wn * 128 + (lane & 31)) * DS_BK;
-    using Frag = u32x4_t[8];  // [0..3]: A blocks i, [4..7]: B blocks j
+    const int b_base = DS_OP_BYTES + (wn * 32 * JB + (lane & 31)) * DS_BK;
+    using Frag = u32x4_t[4 + JB];  // [0..3]: A blocks i, [4..]: B blocks j
     // fragment x (A block x for x < 4, B block x - 4 otherwise) of k step kk
     auto read = [&](const uint8_t* buf, int kk, Frag& f, int x) {
         const int off = (((2 * kk + (lane >> 5)) ^ swz) * 16);
         const int base = x < 4 ? a_base + x * 32 * DS_BK : b_base + (x - 4) * 32 * DS_BK;
         f[x] = *reinterpret_cast<const u32x4_t*>(buf + base + off);
     };
-    // MFMA t (0..15) of one k step: block (t >> 2, t & 3)
+    // MFMA t (0..NT-1) of one k step: block (t / JB, t % JB)
     auto mfma = [&](const Frag& f, int t) {
-        const int i = t >> 2, j = t & 3;
+        const int i = t / JB, j = t % JB;
         acc[i][j] = mfma_i8_32x32x32(f[4 + j], f[i], acc[i][j]);
     };
     // Rendezvous: this wave's DMA for the next stage has landed (the
@@ -604,38 +617,41 @@ __global__ __launch_bounds__(NTHREADS) void gemm8_dma_kernel(Gemm8Args p) {
     // stage's buffer are complete and the buffer can take the DMA STAGES
     // stages ahead.
     auto rendezvous = [&]() {
-        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(DS_DMA_PER_STAGE * (STAGES - 2))
-                     : "memory");
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(DPS * (STAGES - 2)) : "memory");
     };
 
-    // One stage: fragments of its first k step are in f0 on entry.  The 32
-    // MFMAs are issued with one LDS read or one DMA between consecutive
-    // ones, so the matrix pipe always has work queued while those issue:
+    // One stage: fragments of its first k step are in f0 on entry.  The
+    // MFMAs are issued with LDS reads and DMAs between them, so the matrix
+    // pipe always has work queued while those issue:
     //   first k step:  MFMA t, then read fragment t of the second k step
-    //                  (t < 8);
+    //                  (t < 4 + JB);
     //   rendezvous;
-    //   second k step: MFMA t, then read fragment t of the next stage's
-    //                  first k step (t < 8) or DMA t - 8 into this stage's
-    //                  buffer (t >= 8).
+    //   second k step: MFMA t, then the next of these 2*(4 + JB) operations:
+    //                  the next stage's first-k-step fragment reads, then
+    //                  this stage's DMAs (one per MFMA for the full tile).
     // Each k step starts with an MFMA on fragments read long before, so the
     // compiler's wait for them (which drains every LDS read in flight) comes
     // before the next reads are issued.  sched_barrier pins the order.
+    constexpr int NOPS = 2 * DPS;
     Frag f0, f1;
     auto step = [&](uint8_t* cur, const uint8_t* next, int s) {
 #pragma unroll
-        for (int t = 0; t < 16; ++t) {
+        for (int t = 0; t < NT; ++t) {
             mfma(f0, t);
-            if (t < 8) read(cur, 1, f1, t);
+            if (t < 4 + JB) read(cur, 1, f1, t);
             __builtin_amdgcn_sched_barrier(0);
         }
         rendezvous();
 #pragma unroll
-        for (int t = 0; t < 16; ++t) {
+        for (int t = 0; t < NT; ++t) {
             mfma(f1, t);
-            if (t < 8)
-                read(next, 0, f0, t);
-            else
-                dma(cur, s + STAGES, t - 8);
+#pragma unroll
+            for (int o = t * NOPS / NT; o < (t + 1) * NOPS / NT; ++o) {
+                if (o < 4 + JB)
+                    read(next, 0, f0, o);
+                else
+                    dma(cur, s + STAGES, o - (4 + JB));
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
     };
@@ -650,9 +666,9 @@ __global__ __launch_bounds__(NTHREADS) void gemm8_dma_kernel(Gemm8Args p) {
 #pragma unroll
     for (int u = 0; u < STAGES; ++u) issue(stage_buf(u), u);
     // stage 0 landed everywhere
-    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(DS_DMA_PER_STAGE * (STAGES - 1)) : "memory");
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(DPS * (STAGES - 1)) : "memory");
 #pragma unroll
-    for (int x = 0; x < 8; ++x) read(stage_buf(0), 0, f0, x);
+    for (int x = 0; x < 4 + JB; ++x) read(stage_buf(0), 0, f0, x);
     for (int s = 0; s < nk; s += STAGES) {
 #pragma unroll
         for (int u = 0; u < STAGES; ++u)
@@ -663,10 +679,55 @@ __global__ __launch_bounds__(NTHREADS) void gemm8_dma_kernel(Gemm8Args p) {
     // buffers: the epilogue may reuse them
     __syncthreads();
     uint8_t* const area = ds_lds + wave * 32 * STAGED_PITCH;
-    if (m0 + BM <= p.M && n0 + BN <= p.N && p.N % 8 == 0 && p.c_vec)
-        gemm8_store_staged<EPI, false>(p, acc, m0, n0, wm, wn, lane, lds_scales, area);
+    if (m0 + BM <= p.M && n0 + 64 * JB <= p.N && p.N % 8 == 0 && p.c_vec)
+        gemm8_store_staged<EPI, false, JB>(p, acc, m0, n0, wm, wn, lane, lds_scales, area);
     else
-        gemm8_store_staged<EPI, true>(p, acc, m0, n0, wm, wn, lane, lds_scales, area);
+        gemm8_store_staged<EPI, true, JB>(p, acc, m0, n0, wm, wn, lane, lds_scales, area);
+}
+
+// The kernel.  A plain launch has one workgroup per tile (gridDim.x ==
+// tiles), in tile_of's order.  A persistent launch has G = gridDim.x < tiles
+// workgroups, one per CU: R = tiles / G rounds of full tiles, then the
+// rem = tiles - R*G tiles left split into 256x128 halves, one per workgroup
+// (the launcher requires 2*rem <= G and G % 8 == 0).  At M=4096, N=14336
+// that is 896 tiles = 3 rounds + 128 tiles: 3.5 tiles of work per CU instead
+// of 4 rounds with the last one half empty.  Persistent full tiles keep
+// tile_of's locality: XCD x (workgroups x, x+8, ...) walks the contiguous id
+// range x*R*G/8 .. (x+1)*R*G/8, G/8 tiles per round.
+template <int EPI, int STAGES>
+__global__ __launch_bounds__(NTHREADS) void gemm8_dma_kernel(Gemm8Args p) {
+    // Dynamic LDS: the compiler does not see the DMA as a store into it, so
+    // it may neither assume its contents nor insert its own waits for it;
+    // the rendezvous inside the tile orders every access.
+    extern __shared__ __attribute__((aligned(1024))) uint8_t ds_lds[];
+    const int G = gridDim.x, b = blockIdx.x;
+    const int total = p.tiles_m * p.tiles_n;
+    const int R = total / G, rem = total - R * G;
+    const int per_xcd = G / 8, xcd = b % 8, slot = b / 8;
+    i32x16_t acc[4][4];
+    if constexpr (EPI != EPI_BF16) {
+        // fp32 / int32 outputs keep one tile per workgroup: their epilogues
+        // need more registers than a persistent loop leaves without spills
+        int tm, tn;
+        tile_of(b, p, tm, tn);
+        dma_tile<EPI, STAGES, 4>(p, ds_lds, tm * BM, tn * BN, acc);
+        return;
+    }
+    for (int r = 0; r < R; ++r) {
+        int tm, tn;
+        if (G == total)
+            tile_of(b, p, tm, tn);
+        else
+            tile_of_id(xcd * R * per_xcd + r * per_xcd + slot, p, tm, tn);
+        if (r > 0) __syncthreads();  // the previous epilogue's LDS reads are done
+        dma_tile<EPI, STAGES, 4>(p, ds_lds, tm * BM, tn * BN, acc);
+    }
+    if (b < 2 * rem) {
+        int tm, tn;
+        tile_of_id(R * G + (b >> 1), p, tm, tn);
+        __syncthreads();
+        dma_tile<EPI, STAGES, 2>(p, ds_lds, tm * BM, tn * BN + (b & 1) * (BN / 2), acc);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -754,6 +815,15 @@ int env_int(const char* name, int dflt) {
     return v ? std::atoi(v) : dflt;
 }
 
+// Compute units of the current device (one persistent workgroup each).
+int device_cus() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 0;
+    return cus;
+}
+
 template <int EPI, int STAGES>
 int launch_dma(const Gemm8Args& p, int tiles, void* stream, const char* who) {
     constexpr size_t lds = static_cast<size_t>(STAGES) * 2 * DS_OP_BYTES + DS_SCALE_BYTES;
@@ -762,6 +832,18 @@ int launch_dma(const Gemm8Args& p, int tiles, void* stream, const char* who) {
                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     if (attr != hipSuccess)
         return set_error(LHQ_ERR_HIP, "%s: dynamic LDS attribute: %s", who, hipGetErrorString(attr));
+    // Persistent launch (one workgroup per CU) when the tiles leave a
+    // partial last round that splits into at most one half tile per
+    // workgroup (LHQ_GEMM8_PERSIST=0 disables).  A tile takes a whole CU
+    // (256 accumulator registers per wave, ~130 KiB of LDS).
+    static const int persist = env_int("LHQ_GEMM8_PERSIST", 1);
+    static const int cus = device_cus();
+    const int G = cus;
+    const int rem = G > 0 ? tiles % G : 0;
+    if (EPI == EPI_BF16 && persist && G > 0 && G % 8 == 0 && tiles > G && rem != 0 && 2 * rem <= G) {
+        gemm8_dma_kernel<EPI, STAGES><<<G, NTHREADS, lds, as_stream(stream)>>>(p);
+        return check_launch(who);
+    }
     gemm8_dma_kernel<EPI, STAGES><<<tiles, NTHREADS, lds, as_stream(stream)>>>(p);
     return check_launch(who);
 }

@@ -103,6 +103,30 @@ def test_w8a8_full_config3_sampled(oracle, ops):
     assert np.array_equal(out[np.ix_(rows, cols)], sub)
 
 
+@pytest.mark.parametrize("M,K,N", [(4096, 4096, 14336), (4000, 1024, 14136)])
+def test_w8a8_bf16_persistent_tiles(oracle, ops, M, K, N):
+    """896 tiles on a 256-CU device run as a persistent launch: 3 rounds of
+    256x256 tiles, then the last 128 tiles as 256x128 halves (the second shape
+    has partial row and column tiles, and halves wholly past N).  Every bf16
+    output equals the fp32-output kernel's value (one tile per workgroup)
+    rounded by the oracle's bf16 rule; sampled entries equal the oracle."""
+    X = D.to_bf16_bits(oracle, D.with_outliers(D.normal((M, K), 1.0, 41), 0.001, 20.0, 42))
+    Aq, As = oracle.q8_quantize_per_row_bf16(X)
+    Bq, Bs = oracle.q8_quantize_per_col(D.normal((K, N), 0.02, 43))
+    Bt = ops.prepack_b8(ops.dev(Bq), K, N)
+    dA, dAs, dBs = ops.dev(Aq), ops.dev(As), ops.dev(Bs)
+    out = ops.host(ops.gemm_w8a8_bf16(dA, Bt, dAs, dBs, M, N, K), np.uint16)
+    C = ops.dev(np.zeros((M, N), np.float32))
+    ops.gemm_w8a8(dA, Bt, dAs, dBs, M, N, K, C, 1.0, 0.0)
+    assert np.array_equal(out, oracle.f32_to_bf16_n(ops.host(C)))
+    g = D.rng(44)
+    rows = np.sort(g.choice(M, 64, replace=False))
+    cols = np.sort(np.concatenate([g.choice(N, 60, replace=False), np.arange(N - 4, N)]))
+    sub = oracle.gemm_w8a8_bf16out(np.ascontiguousarray(Aq[rows]), np.ascontiguousarray(Bq[:, cols]),
+                                   As[rows], Bs[cols])
+    assert np.array_equal(out[np.ix_(rows, cols)], sub)
+
+
 @pytest.mark.parametrize("M,K,N", [(16, 64, 32), (100, 512, 300), (256, 1024, 256)])
 @pytest.mark.parametrize("alpha,beta", [(1.0, 0.0), (0.5, 2.0)])
 def test_fp8_matches_oracle(oracle, ops, M, K, N, alpha, beta):
