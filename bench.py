@@ -298,6 +298,43 @@ def copy_probe(nbytes: int = 1 << 30, reps: int = 5) -> None:
 # CPU baseline (test infrastructure: the reference's path or its restatement)
 # ---------------------------------------------------------------------------
 
+def cpu_baseline_w8a8(K: int, N: int, budget_s: float):
+    """The reference's gemm_w8a8 (gemm_quant.cpp:29-49, fp32 output) on an
+    M-slice of the W8A8 prefill workload.  Its rows are independent
+    (gemm_quant.cpp:33), so the time per row extrapolates linearly to the
+    M=4096 and M=2048 calls; the figure says so."""
+    import numpy as np
+    from oracle import Oracle, Ref, ref_available
+    kind = "reference" if ref_available() else "port"
+    impl = Ref() if kind == "reference" else Oracle()
+    rng = np.random.default_rng(1)
+    Bq = rng.integers(-127, 128, (K, N), dtype=np.int8)
+    Bs = (rng.random(N, dtype=np.float32) + np.float32(0.5)) * np.float32(1e-3)
+
+    def run(m):
+        Aq = rng.integers(-127, 128, (m, K), dtype=np.int8)
+        As = rng.random(m, dtype=np.float32) + np.float32(0.5)
+        t0 = time.perf_counter()
+        impl.gemm_w8a8(Aq, Bq, As, Bs)
+        return time.perf_counter() - t0
+
+    run(1)  # warm-up (touches B)
+    t1 = run(1)
+    m = max(1, min(64, int(budget_s / max(t1, 1e-6))))
+    per_row = run(m) / m
+    ops_row = 2 * K * N
+    return {
+        "value": ops_row / per_row / 1e12,
+        "unit": "TOPS",
+        "cores": 1,
+        "kind": kind,
+        "sample": (f"gemm_w8a8 (gemm_quant.cpp:29-49) on {m} rows of the K={K}, N={N} workload, "
+                   f"{per_row * 1e3:.0f} ms/row, 1 thread; extrapolated linearly in M (rows are independent): "
+                   f"M=4096 {4096 * per_row:.0f} s, M=2048 {2048 * per_row:.0f} s; host nproc={os.cpu_count()}"),
+        "s_per_call_m4096_extrapolated": 4096 * per_row,
+    }
+
+
 def cpu_baseline(M: int, K: int, N: int, G: int, budget_s: float):
     import numpy as np
     from oracle import Oracle, Ref, ref_available
@@ -433,12 +470,17 @@ def main() -> int:
 
     pre = [] if args.no_prefill else prefill_legs(ops)
 
-    cpu = None
+    cpu = cpu_w8 = None
     if not args.no_cpu:
         log(f"cpu baseline: ~{args.cpu_budget:.0f} s")
         cpu = cpu_baseline(M, K, N, G, args.cpu_budget)
         cpu["speedup_gpu_over_cpu"] = (cpu["ms_per_call"] * 1e3) / w4["us_per_call"]
         log(f"  {cpu['kind']}: {cpu['ms_per_call']:.1f} ms/call, {cpu['value']:.2f} GB/s")
+        if w8:
+            log(f"cpu baseline w8a8: ~{args.cpu_budget / 3:.0f} s")
+            cpu_w8 = cpu_baseline_w8a8(4096, 14336, args.cpu_budget / 3)
+            cpu_w8["speedup_gpu_over_cpu"] = cpu_w8["s_per_call_m4096_extrapolated"] * 1e6 / w8[0]["us_per_call"]
+            log(f"  {cpu_w8['kind']}: {cpu_w8['value'] * 1e3:.2f} GOPS; {cpu_w8['sample']}")
 
     traffic = committed_traffic("w4a16_decode")
     line = {
@@ -467,6 +509,7 @@ def main() -> int:
              "value": round(r["tops"], 1), "unit": "TOPS", "peak": INT8_PEAK_TOPS,
              "frac": round(r["mfma_frac"], 4), "act_quant_us": round(r["act_quant_us"], 2)}
             for r in w8],
+        "w8a8_cpu_baseline": cpu_w8,
         "w4a16_prefill": pre,
         "cpu_baseline": cpu,
     }
