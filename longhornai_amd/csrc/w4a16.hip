@@ -1033,8 +1033,15 @@ __global__ __launch_bounds__(256, 2) void w4_mma_kernel(W4Args p) {
         }
     };
     // all of this wave's loads have landed and every wave is done with the
-    // buffer the next DMA overwrites
-    auto rendezvous = [&]() { asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory"); };
+    // buffer the next DMA overwrites.  Builtins, not inline asm: the
+    // compiler's wait counting then knows every older load is complete and
+    // does not add a drain-everything wait behind the next tile's loads
+    // before this tile's registers are used.  0x0F70: vmcnt(0), expcnt and
+    // lgkmcnt at their maxima (not waited on).
+    auto rendezvous = [&]() {
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        __builtin_amdgcn_s_barrier();
+    };
 
     uint8_t* const buf0 = mm_lds;
     uint8_t* const buf1 = mm_lds + MM_A_BYTES;
