@@ -1085,6 +1085,17 @@ __global__ __launch_bounds__(256, 2) void w4_mma_kernel(W4Args p) {
 // ---------------------------------------------------------------------------
 
 constexpr int kDecodeMaxLds = 64 * 1024;  // activation bytes a decode workgroup may stage
+constexpr int kDecodeBigLds = 96 * 1024;   // ... when its workgroups fit one per CU
+constexpr int kCuLds = 160 * 1024;         // LDS of one CU (gfx950)
+
+// Lets a kernel take more than the default 64 KiB of dynamic LDS (set once
+// per kernel, to the CU's whole LDS).
+template <auto Kern>
+void allow_cu_lds() {
+    static const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(Kern),
+                                                    hipFuncAttributeMaxDynamicSharedMemorySize, kCuLds);
+    (void)e;
+}
 
 // Tuning knobs (read once; unset = heuristic):
 //   LHQ_W4_I8=-1 disables the integer decode kernel (M <= 4);
@@ -1101,11 +1112,22 @@ template <bool F32A, bool ASYM, bool F32C, int T, int NPW, int MR>
 void launch_decode_mr(const W4Args& a, dim3 grid, int S, int bps, size_t lds, hipStream_t s) {
     lds = std::max(lds, static_cast<size_t>(S) * T * MR * 64 * sizeof(float));  // the reduction reuses it
     switch (bps) {
-        case 1: w4_decode_kernel<F32A, ASYM, F32C, T, NPW, 1, false, MR><<<grid, 64 * S, lds, s>>>(a); break;
-        case 2: w4_decode_kernel<F32A, ASYM, F32C, T, NPW, 2, false, MR><<<grid, 64 * S, lds, s>>>(a); break;
+        case 1:
+            allow_cu_lds<&w4_decode_kernel<F32A, ASYM, F32C, T, NPW, 1, false, MR>>();
+            w4_decode_kernel<F32A, ASYM, F32C, T, NPW, 1, false, MR><<<grid, 64 * S, lds, s>>>(a);
+            break;
+        case 2:
+            allow_cu_lds<&w4_decode_kernel<F32A, ASYM, F32C, T, NPW, 2, false, MR>>();
+            w4_decode_kernel<F32A, ASYM, F32C, T, NPW, 2, false, MR><<<grid, 64 * S, lds, s>>>(a);
+            break;
         default:
-            if (a.gmul) w4_decode_kernel<F32A, ASYM, F32C, T, NPW, 4, true, MR><<<grid, 64 * S, lds, s>>>(a);
-            else w4_decode_kernel<F32A, ASYM, F32C, T, NPW, 4, false, MR><<<grid, 64 * S, lds, s>>>(a);
+            if (a.gmul) {
+                allow_cu_lds<&w4_decode_kernel<F32A, ASYM, F32C, T, NPW, 4, true, MR>>();
+                w4_decode_kernel<F32A, ASYM, F32C, T, NPW, 4, true, MR><<<grid, 64 * S, lds, s>>>(a);
+            } else {
+                allow_cu_lds<&w4_decode_kernel<F32A, ASYM, F32C, T, NPW, 4, false, MR>>();
+                w4_decode_kernel<F32A, ASYM, F32C, T, NPW, 4, false, MR><<<grid, 64 * S, lds, s>>>(a);
+            }
             break;
     }
 }
@@ -1207,7 +1229,21 @@ int launch_w4(W4Args a, int batch, hipStream_t s, int mblocks = -1) {
     }
 
     const size_t dec_lds = static_cast<size_t>(min(a.M, 16)) * a.Kt * kW4TileK * (F32A ? 4 : 2);
-    if (!GR && mblocks == 1 && env_dec >= 0 && dec_lds <= static_cast<size_t>(kDecodeMaxLds)) {
+    // Up to 64 KiB of staged activations always; up to 96 KiB when the
+    // workgroups fit one per CU (measured: M=4, K=11008, N=4096 12.1 -> 9.1 us
+    // against the generic kernel; at 128 KiB, or with more workgroups than
+    // CUs, the generic kernel stays faster).
+    static const int cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return 0;
+        return n;
+    }();
+    const int64_t dec_wgs = static_cast<int64_t>(ceil_div(a.Nt, a.Nt >= 1024 ? 2 : 1)) * batch;
+    const bool dec_fits = dec_lds <= static_cast<size_t>(kDecodeMaxLds) ||
+                          (dec_lds <= static_cast<size_t>(kDecodeBigLds) && dec_wgs <= cus);
+    if (!GR && mblocks == 1 && env_dec >= 0 && dec_fits) {
         // Measured on MI355X at K=8192, N=28672: two column tiles per wave
         // when there are many, four K tiles per wave per pass, four waves per
         // workgroup; small launches split K over more waves so the grid still

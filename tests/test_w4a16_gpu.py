@@ -89,6 +89,7 @@ def _asym_case(oracle, ops, M, K, N, G, seed):
 
 @pytest.mark.parametrize("M,K,N", [
     (1, 4096, 4096), (4, 4096, 11008), (16, 11008, 4096),      # config 2
+    (4, 11008, 4096),                                          # 86 KiB of staged activations
     (1, 8192, 10240), (8, 8192, 8192), (1, 28672, 8192),       # config 5 (decode M)
     (1, 8192, 28672),                                          # decode target
     (5, 384, 40),
