@@ -993,7 +993,13 @@ __global__ __launch_bounds__(256, 2) void w4_mma_kernel(W4Args p) {
     // chunk 4j + (lane >> 4), stored in slot chunk ^ (lane & 15)
     const uint32_t a_frag = static_cast<uint32_t>((wm * 64 + col) * 256);
 
+    // a wave whose 64 rows all lie past the block's last row (a ragged
+    // group's tail block, or M <= 64) has nothing to compute; it still
+    // takes part in the loads and rendezvous, and its SIMD time goes to
+    // the other waves resident there
+    const bool live = m0 + 64 * wm < m_end;
     auto compute = [&](const uint8_t* buf, const Regs& R, int kt) {
+        if (!live) return;
         u32x4_t a[4][4];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
