@@ -1016,27 +1016,38 @@ __global__ __launch_bounds__(256, 2) void w4_mma_kernel(W4Args p) {
 #pragma unroll
                 for (int jj = 0; jj < BPS; ++jj) xs[i][s] = mfma_bf16_16x16x32(a[i][s * BPS + jj], ones, xs[i][s]);
             }
+        // Software pipeline over (column tile, row block) units: the t chain
+        // of unit k is issued before the correction of unit k-1, which does
+        // not depend on it, so the correction VALU runs while the matrix core
+        // works instead of waiting on each chain.
+        static_assert(SEGS == 1, "one scale segment per K tile");
+        f32x4_t tp = {0.f, 0.f, 0.f, 0.f};
+        float sp = 0.f, zp = 0.f;
+        auto correct = [&](int c, int i, const f32x4_t& t, float sc, float zc) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                acc[i][c][r] = __builtin_fmaf(sc, __builtin_fmaf(-zc, xs[i][0][r], t[r]), acc[i][c][r]);
+        };
 #pragma unroll
         for (int c = 0; c < MM_CT; ++c) {
             u32x4_t b[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) b[j] = w4_operand(R.w[c][j]);
+            const int g = group_of_c<BPS, GBIG>(kt, 0, p.gmul);
+            const float sc = f16_to_f32(static_cast<uint16_t>(R.sw[c][0] >> s_half));
+            const float zc = kW4Bias + static_cast<float>((R.zw[c] >> (4 * (g & 7))) & 15u);
 #pragma unroll
-            for (int s = 0; s < SEGS; ++s) {
-                const int g = group_of_c<BPS, GBIG>(kt, s, p.gmul);
-                const float scl = f16_to_f32(static_cast<uint16_t>(R.sw[c][s] >> s_half));
-                const float zc = kW4Bias + static_cast<float>((R.zw[c] >> (4 * (g & 7))) & 15u);
+            for (int i = 0; i < 4; ++i) {
+                f32x4_t t = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    f32x4_t tt = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int jj = 0; jj < BPS; ++jj) tt = mfma_bf16_16x16x32(a[i][s * BPS + jj], b[s * BPS + jj], tt);
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        acc[i][c][r] = __builtin_fmaf(scl, __builtin_fmaf(-zc, xs[i][s][r], tt[r]), acc[i][c][r]);
-                }
+                for (int j = 0; j < 4; ++j) t = mfma_bf16_16x16x32(a[i][j], b[j], t);
+                if (c > 0 || i > 0) correct(i == 0 ? c - 1 : c, i == 0 ? 3 : i - 1, tp, sp, zp);
+                tp = t;
+                sp = sc;
+                zp = zc;
             }
         }
+        correct(MM_CT - 1, 3, tp, sp, zp);
     };
     // all of this wave's loads have landed and every wave is done with the
     // buffer the next DMA overwrites.  Builtins, not inline asm: the
