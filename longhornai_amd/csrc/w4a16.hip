@@ -440,53 +440,59 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512, (F32A || T == 2) ? 1 : 4) void
 #pragma unroll
     for (int t = 0; t < T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
+    auto tile = [&](const Pass& P, int i, int kt) {
+        u32x4_t ah[4], al[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            ah[j] = *reinterpret_cast<const u32x4_t*>(arow + kt * kW4TileK + 32 * j);
+            if constexpr (F32A)
+                al[j] = *reinterpret_cast<const u32x4_t*>(arow + Ml * Kp + kt * kW4TileK + 32 * j);
+        }
+#pragma unroll
+        for (int s = 0; s < SEGS; ++s) {
+            f32x4_t xs = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int jj = 0; jj < BPS; ++jj) {
+                xs = mfma_bf16_16x16x32(ah[s * BPS + jj], ones, xs);
+                if constexpr (F32A) xs = mfma_bf16_16x16x32(al[s * BPS + jj], ones, xs);
+            }
+            const int g = seg_group<BPS, GBIG>(kt, s, p);
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                f32x4_t tt = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int jj = 0; jj < BPS; ++jj) {
+                    const int j = s * BPS + jj;
+                    const u32x4_t b = w4_operand(P.w[i][t][j]);
+                    tt = mfma_bf16_16x16x32(ah[j], b, tt);
+                    if constexpr (F32A) tt = mfma_bf16_16x16x32(al[j], b, tt);
+                }
+                float sc, zc;
+                if constexpr (ASYM) {
+                    sc = f16_to_f32(static_cast<uint16_t>(P.sw[i][t][s] >> s_half));
+                    const uint32_t word = P.zw[(BPS < 4) ? (i * SEGS + s) / 8 : (GBIG ? i : 0)][t];
+                    zc = kW4Bias + static_cast<float>((word >> (4 * (g & 7))) & 15u);
+                } else {
+                    sc = __uint_as_float(P.sw[i][t][s]);
+                    zc = kW4Bias + 8.0f;  // implied zero point 8
+                }
+#pragma unroll
+                for (int r = 0; r < MR; ++r)
+                    acc[t][r] = __builtin_fmaf(sc, __builtin_fmaf(-zc, xs[r], tt[r]), acc[t][r]);
+            }
+        }
+    };
+    // a full pass runs its tiles without a branch between them, so the
+    // compiler can overlap one tile's MFMA latency with the next tile's decode
     auto consume = [&](const Pass& P, int kb) {
         const int n = min(NPW, p.Kt - kb);
+        if (n == NPW) {
 #pragma unroll
-        for (int i = 0; i < NPW; ++i) {
-            if (i < n) {
-                const int kt = kb + i;
-                u32x4_t ah[4], al[4];
+            for (int i = 0; i < NPW; ++i) tile(P, i, kb + i);
+        } else {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    ah[j] = *reinterpret_cast<const u32x4_t*>(arow + kt * kW4TileK + 32 * j);
-                    if constexpr (F32A)
-                        al[j] = *reinterpret_cast<const u32x4_t*>(arow + Ml * Kp + kt * kW4TileK + 32 * j);
-                }
-#pragma unroll
-                for (int s = 0; s < SEGS; ++s) {
-                    f32x4_t xs = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int jj = 0; jj < BPS; ++jj) {
-                        xs = mfma_bf16_16x16x32(ah[s * BPS + jj], ones, xs);
-                        if constexpr (F32A) xs = mfma_bf16_16x16x32(al[s * BPS + jj], ones, xs);
-                    }
-                    const int g = seg_group<BPS, GBIG>(kt, s, p);
-#pragma unroll
-                    for (int t = 0; t < T; ++t) {
-                        f32x4_t tt = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                        for (int jj = 0; jj < BPS; ++jj) {
-                            const int j = s * BPS + jj;
-                            const u32x4_t b = w4_operand(P.w[i][t][j]);
-                            tt = mfma_bf16_16x16x32(ah[j], b, tt);
-                            if constexpr (F32A) tt = mfma_bf16_16x16x32(al[j], b, tt);
-                        }
-                        float sc, zc;
-                        if constexpr (ASYM) {
-                            sc = f16_to_f32(static_cast<uint16_t>(P.sw[i][t][s] >> s_half));
-                            const uint32_t word = P.zw[(BPS < 4) ? (i * SEGS + s) / 8 : (GBIG ? i : 0)][t];
-                            zc = kW4Bias + static_cast<float>((word >> (4 * (g & 7))) & 15u);
-                        } else {
-                            sc = __uint_as_float(P.sw[i][t][s]);
-                            zc = kW4Bias + 8.0f;  // implied zero point 8
-                        }
-#pragma unroll
-                        for (int r = 0; r < MR; ++r)
-                            acc[t][r] = __builtin_fmaf(sc, __builtin_fmaf(-zc, xs[r], tt[r]), acc[t][r]);
-                    }
-                }
-            }
+            for (int i = 0; i < NPW; ++i)
+                if (i < n) tile(P, i, kb + i);
         }
     };
     // passes of this wave: kb0 + q*span for q < np.  Pairs of passes run
