@@ -103,11 +103,12 @@ def test_w8a8_full_config3_sampled(oracle, ops):
     assert np.array_equal(out[np.ix_(rows, cols)], sub)
 
 
-@pytest.mark.parametrize("M,K,N", [(4096, 4096, 14336), (4000, 1024, 14136)])
+@pytest.mark.parametrize("M,K,N", [(4096, 4096, 14336), (4000, 1024, 14136), (4000, 512, 14330)])
 def test_w8a8_bf16_persistent_tiles(oracle, ops, M, K, N):
     """896 tiles on a 256-CU device run as a persistent launch: 3 rounds of
     256x256 tiles, then the last 128 tiles as 256x128 halves (the second shape
-    has partial row and column tiles, and halves wholly past N).  Every bf16
+    has partial row and column tiles, and halves wholly past N; the third has
+    N % 8 != 0, so every tile takes the edge epilogue).  Every bf16
     output equals the fp32-output kernel's value (one tile per workgroup)
     rounded by the oracle's bf16 rule; sampled entries equal the oracle."""
     X = D.to_bf16_bits(oracle, D.with_outliers(D.normal((M, K), 1.0, 41), 0.001, 20.0, 42))
