@@ -54,7 +54,9 @@ def test_per_row(oracle, ops, rows, dim, kind):
     _eq(ops.host(d), d_w)
 
 
-@pytest.mark.parametrize("rows,dim", [(2048, 4096), (3, 24), (5, 13)])
+# the vectorised kernel (dim % 8 == 0, short and long rows) and the scalar
+# kernel (dim % 8 != 0)
+@pytest.mark.parametrize("rows,dim", [(2048, 4096), (2049, 4096), (3, 24), (5, 13), (6, 8192), (7, 4104)])
 def test_per_row_bf16(oracle, ops, rows, dim):
     x = D.with_outliers(D.normal((rows, dim), 1.0, 5), 0.001, 20.0, 6)
     x[0] = 0.0
