@@ -540,7 +540,8 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512, (F32A || T == 2) ? 1 : 4) void
 }
 
 // ---------------------------------------------------------------------------
-// Integer decode kernel (M <= 4 rows; G = 64 or a multiple of 128).
+// Integer decode kernel (G = 64 or a multiple of 128; written for M <= 4
+// rows, launched for M = 1, where converting the activations costs least).
 //
 // The workgroup converts its activation rows once, into LDS, to fixed point
 // per 128-wide K block: q = round(x * 2^-E), with E taken from the block's
@@ -726,7 +727,7 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512) void w4_decode_i8_kernel(W4Arg
             uint32_t d[8], vs = 0;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                d[i] = __float_as_uint(__builtin_fmaf(f[i], inv, kQMagic)) - 0x4B400000u;
+                d[i] = __float_as_uint(__builtin_fmaf(f[i], inv, kQMagic)) - (kQMagicBits - 0x8080u);
                 vs += d[i];
             }
             uint32_t pl[3][2];
