@@ -112,6 +112,16 @@ int lhq_w4_prepack_asym(const uint8_t* packed, const uint16_t* scales_f16,
                         const uint8_t* zeros, int K, int N, int group_size,
                         uint8_t* qweight, uint16_t* scales_out, uint32_t* zeros_out,
                         void* stream);
+/* Gate and up projections of a SwiGLU MLP in one W4 tensor (no reference
+ * counterpart; feeds lhq_gemm_w4a16_bf16_grouped_swiglu): both prepacked by
+ * lhq_w4_prepack_asym for [K, I]; column tile 2j of the output is gate tile
+ * j, tile 2j+1 is up tile j.  Each output array is twice the size given by
+ * lhq_w4_*_bytes(K, I, ...).  All pointers 16-byte aligned. */
+int lhq_w4_interleave_gate_up(const uint8_t* gate_qweight, const uint16_t* gate_scales,
+                              const uint32_t* gate_zeros, const uint8_t* up_qweight,
+                              const uint16_t* up_scales, const uint32_t* up_zeros, int K, int I,
+                              int group_size, uint8_t* qweight, uint16_t* scales_out,
+                              uint32_t* zeros_out, void* stream);
 /* 8-bit B operand (int8 or fp8 e4m3) [K, N] -> k-contiguous Bt [Np][Kp]
  * with Np = N rounded up to 256 and Kp = K rounded up to 128, zero padded. */
 int64_t lhq_b8_prepacked_bytes(int K, int N);
@@ -146,6 +156,62 @@ int lhq_gemm_w4a16_bf16_grouped(const uint16_t* A, const int32_t* offsets,
                                 const uint32_t* const* zeros, uint16_t* C,
                                 int num_groups, int row_capacity, int N, int K,
                                 int group_size, void* stream);
+
+/* The gate / up half of moe_expert_mlp (moe.cpp:185-192) on W4A16 experts,
+ * the hook of moe.hpp:26-28: per group, act = bf16(silu(A@Wg) * (A@Wu)),
+ * silu(v) = v / (1 + exp(-v)), from fp32 accumulators, in one launch.  The
+ * weights of group e are lhq_w4_interleave_gate_up output; act [rows, I]. */
+int lhq_gemm_w4a16_bf16_grouped_swiglu(const uint16_t* A, const int32_t* offsets,
+                                       const uint8_t* const* qweights,
+                                       const uint16_t* const* scales,
+                                       const uint32_t* const* zeros, uint16_t* act,
+                                       int num_groups, int row_capacity, int I, int K,
+                                       int group_size, void* stream);
+
+/* ---- MoE routing: moe.hpp:63-102 / moe.cpp:102-221 ---------------------- */
+/* moe_dispatch (moe.hpp:75-78, moe.cpp:102-140): expert_ids [T, top_k] ->
+ * expert_offsets [E+1], token_idx / slot_idx [T*top_k] (stable: slot order
+ * within each expert), the rows of hidden [T, H] copied to
+ * expert_inputs [T*top_k, H], and slot_pos [T*top_k], the position
+ * (t, k) went to (no reference counterpart: the inverse map combine uses).
+ * An id outside [0, E) is dropped (slot_pos -1; positions past
+ * expert_offsets[E] hold token_idx = slot_idx = -1).  E <= 512. */
+int lhq_moe_dispatch_f32(const float* hidden, const int32_t* expert_ids,
+                         int32_t* expert_offsets, int32_t* token_idx, int32_t* slot_idx,
+                         int32_t* slot_pos, float* expert_inputs, int n_tokens, int hidden_dim,
+                         int n_experts, int top_k, void* stream);
+int lhq_moe_dispatch_bf16(const uint16_t* hidden, const int32_t* expert_ids,
+                          int32_t* expert_offsets, int32_t* token_idx, int32_t* slot_idx,
+                          int32_t* slot_pos, uint16_t* expert_inputs, int n_tokens,
+                          int hidden_dim, int n_experts, int top_k, void* stream);
+/* slot_pos from the reference's dispatch outputs (token_idx, slot_idx must
+ * be the layout moe_dispatch writes: each (t, k) at most once). */
+int lhq_moe_slot_positions(const int32_t* token_idx, const int32_t* slot_idx, int32_t* slot_pos,
+                           int n_tokens, int top_k, void* stream);
+/* moe_combine (moe.hpp:96-102, moe.cpp:198-221): output[t] = sum over t's
+ * slots in position order of gate_weights[t, k] * expert_outputs[pos],
+ * fp32 with the reference's rounding (bit-exact); top_k <= 64.  The bf16
+ * form widens expert_outputs exactly and rounds the sum once. */
+int lhq_moe_combine_f32(const float* expert_outputs, const int32_t* slot_pos,
+                        const float* gate_weights, float* output, int n_tokens, int hidden_dim,
+                        int top_k, void* stream);
+int lhq_moe_combine_bf16(const uint16_t* expert_outputs, const int32_t* slot_pos,
+                         const float* gate_weights, uint16_t* output, int n_tokens,
+                         int hidden_dim, int top_k, void* stream);
+/* moe_expert_mlp (moe.hpp:80-94, moe.cpp:150-196) with W4A16 experts:
+ * lhq_gemm_w4a16_bf16_grouped_swiglu into act [row_capacity, I] (caller's
+ * buffer), then lhq_gemm_w4a16_bf16_grouped with the down weights into
+ * expert_outputs [row_capacity, H], bf16. */
+int lhq_moe_expert_mlp_w4a16_bf16(const uint16_t* expert_inputs, const int32_t* expert_offsets,
+                                  const uint8_t* const* gate_up_qweights,
+                                  const uint16_t* const* gate_up_scales,
+                                  const uint32_t* const* gate_up_zeros,
+                                  const uint8_t* const* down_qweights,
+                                  const uint16_t* const* down_scales,
+                                  const uint32_t* const* down_zeros, uint16_t* act,
+                                  uint16_t* expert_outputs, int n_experts, int row_capacity,
+                                  int hidden_dim, int intermediate_dim, int group_size,
+                                  void* stream);
 
 /* ---- W8A8 GEMM: gemm_quant.hpp:34-45 / gemm_quant.cpp:29-49 ------------ */
 /* Reference semantics, bit-exact: Aq int8 [M,K]; Bt = lhq_b8_prepack(Bq);

@@ -56,6 +56,14 @@ SIGNATURES = {
     "lhq_gemm_w4a16_bf16": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
     "lhq_gemm_w4a16_bf16_batched": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p],
     "lhq_gemm_w4a16_bf16_grouped": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p],
+    "lhq_gemm_w4a16_bf16_grouped_swiglu": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p],
+    "lhq_w4_interleave_gate_up": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _p, _p, _p, _p],
+    "lhq_moe_dispatch_f32": [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
+    "lhq_moe_dispatch_bf16": [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
+    "lhq_moe_slot_positions": [_p, _p, _p, _i, _i, _p],
+    "lhq_moe_combine_f32": [_p, _p, _p, _p, _i, _i, _i, _p],
+    "lhq_moe_combine_bf16": [_p, _p, _p, _p, _i, _i, _i, _p],
+    "lhq_moe_expert_mlp_w4a16_bf16": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p],
     "lhq_gemm_w8a8": [_p, _p, _p, _p, _p, _i, _i, _i, _f, _f, _p],
     "lhq_gemm_w8a8_bf16": [_p, _p, _p, _p, _p, _i, _i, _i, _p],
     "lhq_gemm_w8a8_i32": [_p, _p, _p, _i, _i, _i, _p],

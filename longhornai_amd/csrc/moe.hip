@@ -1,0 +1,357 @@
+// moe.hip -- the MoE routing around the grouped W4A16 GEMM, on gfx950:
+// dispatch (a stable counting sort of the (token, slot) pairs by expert, then
+// the row gather), the gate-weighted combine, and the quantized expert MLP
+// (gate and up projections in one grouped launch with a SwiGLU epilogue,
+// then the down projection).
+//
+// Reference: moe.hpp:63-102, moe.cpp:102-221 -- CPU loops over host arrays.
+// Here the group table `offsets` is produced on the device and consumed by
+// the grouped GEMM on the device: nothing goes back to the host between
+// routing and combine.  All work is integer bookkeeping and byte moves except
+// the combine's fp32 sums, which keep the reference's order and rounding.
+#include "common.hpp"
+
+namespace lhq {
+namespace {
+
+constexpr int kRankThreads = 1024;               // one workgroup ranks every slot
+constexpr int kRankWaves = kRankThreads / 64;
+constexpr int kMaxExperts = 512;                 // LDS: kRankWaves x kMaxExperts counters (32 KiB)
+constexpr int kMaxTopK = 64;                     // the combine's per-token slot list
+
+// Dispatch, step 1 (one workgroup of 16 waves).  Wave w owns the contiguous
+// slot range [w*per, (w+1)*per) of the S = T*topk pairs, slot s = t*topk + k.
+//   a) per-wave counts per expert (LDS atomics: a count does not depend on
+//      order) -- moe.cpp:111-118;
+//   b) offsets = exclusive scan of the per-expert totals (moe.cpp:119-123);
+//      wave w's first position inside expert e = offsets[e] + the counts of
+//      waves 0..w-1 for e;
+//   c) each wave walks its range in order, 64 slots at a time; the lanes that
+//      name one expert take consecutive positions in lane order (ballot +
+//      prefix popcount), so positions follow slot order inside each expert:
+//      the reference's stable placement (moe.cpp:124-139).
+// Writes token_idx, slot_idx, slot_pos; an id outside [0, E) is dropped
+// (slot_pos -1), and positions past offsets[E] get token_idx = slot_idx = -1.
+__global__ __launch_bounds__(kRankThreads) void moe_rank_kernel(const int32_t* __restrict__ ids, int S, int topk,
+                                                                int E, int32_t* __restrict__ offsets,
+                                                                int32_t* __restrict__ token_idx,
+                                                                int32_t* __restrict__ slot_idx,
+                                                                int32_t* __restrict__ slot_pos) {
+    __shared__ int32_t cnt[kRankWaves][kMaxExperts];
+    __shared__ int32_t scan[kMaxExperts];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    for (int i = threadIdx.x; i < kRankWaves * kMaxExperts; i += kRankThreads) (&cnt[0][0])[i] = 0;
+    __syncthreads();
+
+    const int per = (S + kRankWaves - 1) / kRankWaves;
+    const int s0 = min(S, wave * per), s1 = min(S, s0 + per);
+    for (int s = s0 + lane; s < s1; s += 64) {
+        const int e = ids[s];
+        if (e >= 0 && e < E) atomicAdd(&cnt[wave][e], 1);
+    }
+    __syncthreads();
+
+    // b) inclusive scan of the totals (Hillis-Steele; every thread runs the
+    //    same number of rounds, so the barriers are uniform)
+    const int e = threadIdx.x;
+    int total = 0;
+    if (e < E)
+        for (int w = 0; w < kRankWaves; ++w) total += cnt[w][e];
+    if (e < E) scan[e] = total;
+    __syncthreads();
+    for (int d = 1; d < E; d <<= 1) {
+        const int v = (e < E && e >= d) ? scan[e - d] : 0;
+        __syncthreads();
+        if (e < E) scan[e] += v;
+        __syncthreads();
+    }
+    if (e < E) {
+        int run = scan[e] - total;  // exclusive
+        offsets[e] = run;
+        if (e == E - 1) offsets[E] = scan[e];
+        for (int w = 0; w < kRankWaves; ++w) {
+            const int c = cnt[w][e];
+            cnt[w][e] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+
+    // c) positions in slot order
+    for (int base = s0; base < s1; base += 64) {
+        const int s = base + lane;
+        const bool in = s < s1;
+        const int ex = in ? ids[s] : -1;
+        const bool valid = in && ex >= 0 && ex < E;
+        int pos = -1;
+        uint64_t rem = __ballot(valid);
+        while (rem) {
+            const int leader = __builtin_ctzll(rem);
+            const int el = __shfl(ex, leader);
+            const uint64_t m = __ballot(valid && ex == el);
+            const int b = cnt[wave][el];
+            if (valid && ex == el) pos = b + __popcll(m & ((uint64_t{1} << lane) - 1));
+            if (lane == leader) cnt[wave][el] = b + __popcll(m);
+            rem &= ~m;
+        }
+        if (in) {
+            slot_pos[s] = pos;
+            if (valid) {
+                token_idx[pos] = s / topk;
+                slot_idx[pos] = s % topk;
+            }
+        }
+    }
+    const int placed = E > 0 ? scan[E - 1] : 0;
+    for (int s = placed + static_cast<int>(threadIdx.x); s < S; s += kRankThreads) {
+        token_idx[s] = -1;
+        slot_idx[s] = -1;
+    }
+}
+
+// Dispatch, step 2: the row copy (moe.cpp:136-137).  Workgroup (t, y) reads
+// VB-byte units y*256 .. y*256+255 of token t's row once and writes them to
+// each of the token's dispatched positions.
+template <int VB>
+struct VecOf;
+template <>
+struct VecOf<16> { using T = u32x4_t; };
+template <>
+struct VecOf<4> { using T = uint32_t; };
+template <>
+struct VecOf<2> { using T = uint16_t; };
+
+template <int VB>
+__global__ __launch_bounds__(256) void moe_gather_kernel(const uint8_t* __restrict__ hidden,
+                                                         const int32_t* __restrict__ slot_pos,
+                                                         uint8_t* __restrict__ out, int64_t row_bytes, int topk) {
+    using V = typename VecOf<VB>::T;
+    const int64_t t = blockIdx.x;
+    const int64_t off = (static_cast<int64_t>(blockIdx.y) * 256 + threadIdx.x) * VB;
+    if (off >= row_bytes) return;
+    const V v = *reinterpret_cast<const V*>(hidden + t * row_bytes + off);
+    for (int k = 0; k < topk; ++k) {
+        const int pos = slot_pos[t * topk + k];
+        if (pos >= 0) *reinterpret_cast<V*>(out + static_cast<int64_t>(pos) * row_bytes + off) = v;
+    }
+}
+
+// slot_pos from token_idx / slot_idx (the inverse of the dispatch layout):
+// fill with -1, then one store per dispatched slot.
+__global__ void moe_fill_kernel(int32_t* p, int64_t n, int32_t v) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+__global__ void moe_invert_kernel(const int32_t* __restrict__ token_idx, const int32_t* __restrict__ slot_idx,
+                                  int32_t* __restrict__ slot_pos, int T, int topk) {
+    const int64_t s = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (s >= static_cast<int64_t>(T) * topk) return;
+    const int t = token_idx[s], k = slot_idx[s];
+    if (t >= 0 && t < T && k >= 0 && k < topk) slot_pos[static_cast<int64_t>(t) * topk + k] = static_cast<int32_t>(s);
+}
+
+// Combine (moe.cpp:198-221): output[t] = the sum, over t's dispatched slots
+// in position order, of gate[t, k] * y[pos] -- the reference zeroes the
+// output and adds one product per slot in slot order (expert-major), so a
+// token's terms arrive in ascending position.  fp32, product and sum each
+// rounded (contraction off), starting from +0.  Workgroup (t, y):
+// thread 0 sorts the token's positions into LDS, then each thread sums four
+// consecutive elements.  BF16: y and output bf16 (y widened exactly, the sum
+// rounded once); else fp32.
+template <bool BF16>
+__global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict__ y,
+                                                          const int32_t* __restrict__ slot_pos,
+                                                          const float* __restrict__ gates, void* __restrict__ out,
+                                                          int H, int topk) {
+    // hipcc contracts a * b + c into one fused multiply-add by default; the
+    // reference rounds the product and the sum separately
+#pragma clang fp contract(off)
+    __shared__ int32_t sp[kMaxTopK];
+    __shared__ float sg[kMaxTopK];
+    __shared__ int ns;
+    const int64_t t = blockIdx.x;
+    if (threadIdx.x == 0) {
+        int n = 0;
+        for (int k = 0; k < topk; ++k) {
+            const int p = slot_pos[t * topk + k];
+            if (p < 0 || p >= static_cast<int64_t>(gridDim.x) * topk) continue;  // y has T*topk rows
+            const float g = gates[t * topk + k];
+            int j = n++;
+            while (j > 0 && sp[j - 1] > p) {
+                sp[j] = sp[j - 1];
+                sg[j] = sg[j - 1];
+                --j;
+            }
+            sp[j] = p;
+            sg[j] = g;
+        }
+        ns = n;
+    }
+    __syncthreads();
+    const int n = ns;
+    const int i0 = (static_cast<int>(blockIdx.y) * 256 + static_cast<int>(threadIdx.x)) * 4;
+    if (i0 >= H) return;
+    const int cnt = min(4, H - i0);
+    const bool vec = (cnt == 4) && (H % 4 == 0);
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < n; ++j) {
+        const int64_t base = static_cast<int64_t>(sp[j]) * H + i0;
+        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (BF16) {
+            const uint16_t* yp = static_cast<const uint16_t*>(y) + base;
+            if (vec) {
+                const u32x2_t w = *reinterpret_cast<const u32x2_t*>(yp);
+                v[0] = __uint_as_float(w[0] << 16);
+                v[1] = __uint_as_float(w[0] & 0xffff0000u);
+                v[2] = __uint_as_float(w[1] << 16);
+                v[3] = __uint_as_float(w[1] & 0xffff0000u);
+            } else {
+                for (int q = 0; q < cnt; ++q) v[q] = bf16_to_f32(yp[q]);
+            }
+        } else {
+            const float* yp = static_cast<const float*>(y) + base;
+            if (vec) {
+                const f32x4_t w = *reinterpret_cast<const f32x4_t*>(yp);
+                v[0] = w[0];
+                v[1] = w[1];
+                v[2] = w[2];
+                v[3] = w[3];
+            } else {
+                for (int q = 0; q < cnt; ++q) v[q] = yp[q];
+            }
+        }
+        const float g = sg[j];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[q] = acc[q] + g * v[q];
+    }
+    const int64_t ob = t * H + i0;
+    if constexpr (BF16) {
+        uint16_t* op = static_cast<uint16_t*>(out) + ob;
+        if (vec) {
+            *reinterpret_cast<u32x2_t*>(op) = u32x2_t{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
+        } else {
+            for (int q = 0; q < cnt; ++q) op[q] = f32_to_bf16(acc[q]);
+        }
+    } else {
+        float* op = static_cast<float*>(out) + ob;
+        if (vec) {
+            *reinterpret_cast<f32x4_t*>(op) = f32x4_t{acc[0], acc[1], acc[2], acc[3]};
+        } else {
+            for (int q = 0; q < cnt; ++q) op[q] = acc[q];
+        }
+    }
+}
+
+bool aligned(const void* p, unsigned a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+int check_routing(const char* who, int T, int H, int E, int topk) {
+    LHQ_REQUIRE(T >= 0 && H > 0 && E > 0 && topk > 0, "%s: bad dims T=%d H=%d E=%d top_k=%d", who, T, H, E, topk);
+    LHQ_REQUIRE(static_cast<int64_t>(T) * topk < (int64_t{1} << 31), "%s: T*top_k=%lld exceeds int32", who,
+                static_cast<long long>(T) * topk);
+    LHQ_SUPPORTED(E <= kMaxExperts, "%s: n_experts=%d exceeds %d", who, E, kMaxExperts);
+    return LHQ_OK;
+}
+
+int dispatch(const char* who, const void* hidden, int elem, const int32_t* ids, int32_t* offsets,
+             int32_t* token_idx, int32_t* slot_idx, int32_t* slot_pos, void* out, int T, int H, int E, int topk,
+             void* stream) {
+    if (int st = check_routing(who, T, H, E, topk)) return st;
+    LHQ_REQUIRE(offsets && (T == 0 || (hidden && ids && token_idx && slot_idx && slot_pos && out)),
+                "%s: null pointer", who);
+    hipStream_t s = as_stream(stream);
+    const int S = T * topk;
+    moe_rank_kernel<<<1, kRankThreads, 0, s>>>(ids, S, topk, E, offsets, token_idx, slot_idx, slot_pos);
+    if (int st = check_launch(who)) return st;
+    if (T == 0) return LHQ_OK;
+    const int64_t row_bytes = static_cast<int64_t>(H) * elem;
+    const int vb = (row_bytes % 16 == 0 && aligned(hidden, 16) && aligned(out, 16)) ? 16
+                   : (row_bytes % 4 == 0 && aligned(hidden, 4) && aligned(out, 4)) ? 4
+                                                                                   : 2;
+    const int64_t chunks = ceil_div64(row_bytes / vb, 256);
+    LHQ_SUPPORTED(chunks <= 65535, "%s: hidden_dim=%d too large", who, H);
+    const dim3 grid(static_cast<unsigned>(T), static_cast<unsigned>(chunks));
+    const uint8_t* h = static_cast<const uint8_t*>(hidden);
+    uint8_t* o = static_cast<uint8_t*>(out);
+    if (vb == 16) moe_gather_kernel<16><<<grid, 256, 0, s>>>(h, slot_pos, o, row_bytes, topk);
+    else if (vb == 4) moe_gather_kernel<4><<<grid, 256, 0, s>>>(h, slot_pos, o, row_bytes, topk);
+    else moe_gather_kernel<2><<<grid, 256, 0, s>>>(h, slot_pos, o, row_bytes, topk);
+    return check_launch(who);
+}
+
+template <bool BF16>
+int combine(const char* who, const void* y, const int32_t* slot_pos, const float* gates, void* out, int T, int H,
+            int topk, void* stream) {
+    LHQ_REQUIRE(T >= 0 && H > 0 && topk > 0, "%s: bad dims T=%d H=%d top_k=%d", who, T, H, topk);
+    LHQ_SUPPORTED(topk <= kMaxTopK, "%s: top_k=%d exceeds %d", who, topk, kMaxTopK);
+    if (T == 0) return LHQ_OK;
+    LHQ_REQUIRE(y && slot_pos && gates && out, "%s: null pointer", who);
+    LHQ_REQUIRE(H % 4 != 0 || (aligned(y, 8) && aligned(out, 8) && (BF16 || (aligned(y, 16) && aligned(out, 16)))),
+                "%s: y and output must be aligned to their 4-element vectors", who);
+    const dim3 grid(static_cast<unsigned>(T), static_cast<unsigned>(ceil_div(H, 1024)));
+    moe_combine_kernel<BF16><<<grid, 256, 0, as_stream(stream)>>>(y, slot_pos, gates, out, H, topk);
+    return check_launch(who);
+}
+
+}  // namespace
+}  // namespace lhq
+
+using namespace lhq;
+
+extern "C" {
+
+int lhq_moe_dispatch_f32(const float* hidden, const int32_t* expert_ids, int32_t* expert_offsets, int32_t* token_idx,
+                         int32_t* slot_idx, int32_t* slot_pos, float* expert_inputs, int n_tokens, int hidden_dim,
+                         int n_experts, int top_k, void* stream) {
+    return dispatch("moe_dispatch_f32", hidden, 4, expert_ids, expert_offsets, token_idx, slot_idx, slot_pos,
+                    expert_inputs, n_tokens, hidden_dim, n_experts, top_k, stream);
+}
+
+int lhq_moe_dispatch_bf16(const uint16_t* hidden, const int32_t* expert_ids, int32_t* expert_offsets,
+                          int32_t* token_idx, int32_t* slot_idx, int32_t* slot_pos, uint16_t* expert_inputs,
+                          int n_tokens, int hidden_dim, int n_experts, int top_k, void* stream) {
+    return dispatch("moe_dispatch_bf16", hidden, 2, expert_ids, expert_offsets, token_idx, slot_idx, slot_pos,
+                    expert_inputs, n_tokens, hidden_dim, n_experts, top_k, stream);
+}
+
+int lhq_moe_slot_positions(const int32_t* token_idx, const int32_t* slot_idx, int32_t* slot_pos, int n_tokens,
+                           int top_k, void* stream) {
+    LHQ_REQUIRE(n_tokens >= 0 && top_k > 0, "moe_slot_positions: bad dims T=%d top_k=%d", n_tokens, top_k);
+    const int64_t S = static_cast<int64_t>(n_tokens) * top_k;
+    LHQ_REQUIRE(S < (int64_t{1} << 31), "moe_slot_positions: T*top_k exceeds int32");
+    if (S == 0) return LHQ_OK;
+    LHQ_REQUIRE(token_idx && slot_idx && slot_pos, "moe_slot_positions: null pointer");
+    hipStream_t s = as_stream(stream);
+    const unsigned blocks = static_cast<unsigned>(ceil_div64(S, 256));
+    moe_fill_kernel<<<blocks, 256, 0, s>>>(slot_pos, S, -1);
+    moe_invert_kernel<<<blocks, 256, 0, s>>>(token_idx, slot_idx, slot_pos, n_tokens, top_k);
+    return check_launch("moe_slot_positions");
+}
+
+int lhq_moe_combine_f32(const float* expert_outputs, const int32_t* slot_pos, const float* gate_weights,
+                        float* output, int n_tokens, int hidden_dim, int top_k, void* stream) {
+    return combine<false>("moe_combine_f32", expert_outputs, slot_pos, gate_weights, output, n_tokens, hidden_dim,
+                          top_k, stream);
+}
+
+int lhq_moe_combine_bf16(const uint16_t* expert_outputs, const int32_t* slot_pos, const float* gate_weights,
+                         uint16_t* output, int n_tokens, int hidden_dim, int top_k, void* stream) {
+    return combine<true>("moe_combine_bf16", expert_outputs, slot_pos, gate_weights, output, n_tokens, hidden_dim,
+                         top_k, stream);
+}
+
+int lhq_moe_expert_mlp_w4a16_bf16(const uint16_t* expert_inputs, const int32_t* expert_offsets,
+                                  const uint8_t* const* gate_up_qweights, const uint16_t* const* gate_up_scales,
+                                  const uint32_t* const* gate_up_zeros, const uint8_t* const* down_qweights,
+                                  const uint16_t* const* down_scales, const uint32_t* const* down_zeros,
+                                  uint16_t* act, uint16_t* expert_outputs, int n_experts, int row_capacity,
+                                  int hidden_dim, int intermediate_dim, int group_size, void* stream) {
+    if (int st = lhq_gemm_w4a16_bf16_grouped_swiglu(expert_inputs, expert_offsets, gate_up_qweights, gate_up_scales,
+                                                    gate_up_zeros, act, n_experts, row_capacity, intermediate_dim,
+                                                    hidden_dim, group_size, stream))
+        return st;
+    return lhq_gemm_w4a16_bf16_grouped(act, expert_offsets, down_qweights, down_scales, down_zeros, expert_outputs,
+                                       n_experts, row_capacity, hidden_dim, intermediate_dim, group_size, stream);
+}
+
+}  // extern "C"

@@ -98,6 +98,28 @@ __global__ __launch_bounds__(256) void b8_prepack_kernel(const uint8_t* __restri
     }
 }
 
+// Interleave two prepacked W4 tensors by column tile: output block 2i is
+// block i of `a`, block 2i + 1 is block i of `b` (a block is everything one
+// column tile owns: blk16 16-byte units).  One 16-byte copy per thread.
+__global__ void w4_interleave_kernel(const u32x4_t* __restrict__ a, const u32x4_t* __restrict__ b,
+                                     u32x4_t* __restrict__ out, int64_t blk16, int64_t total16) {
+    const int64_t d = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (d >= total16) return;
+    const int64_t blk = d / blk16, off = d - blk * blk16;
+    const u32x4_t* src = (blk & 1) ? b : a;
+    out[d] = src[(blk >> 1) * blk16 + off];
+}
+
+int launch_interleave(const void* a, const void* b, void* out, int64_t blk_bytes, int tiles, hipStream_t s) {
+    const int64_t blk16 = blk_bytes / 16, total16 = 2 * blk16 * tiles;
+    if (total16 == 0) return LHQ_OK;
+    w4_interleave_kernel<<<static_cast<unsigned>(ceil_div64(total16, 256)), 256, 0, s>>>(
+        static_cast<const u32x4_t*>(a), static_cast<const u32x4_t*>(b), static_cast<u32x4_t*>(out), blk16, total16);
+    return check_launch("w4_interleave_gate_up");
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
 bool w4_dims_ok(int K, int N, int G) {
     return K > 0 && N > 0 && G > 0 && (K % G) == 0 && (K % 2) == 0;
 }
@@ -159,6 +181,27 @@ int lhq_w4_prepack_asym(const uint8_t* packed, const uint16_t* scales_f16, const
     w4_prepack_zeros_kernel<<<static_cast<unsigned>(ceil_div64(nz, 256)), 256, 0, s>>>(
         zeros, zeros_out, N, NG, NG8, nz);
     return check_launch("w4_prepack_asym");
+}
+
+int lhq_w4_interleave_gate_up(const uint8_t* gate_qweight, const uint16_t* gate_scales,
+                              const uint32_t* gate_zeros, const uint8_t* up_qweight,
+                              const uint16_t* up_scales, const uint32_t* up_zeros, int K, int I, int G,
+                              uint8_t* qweight, uint16_t* scales_out, uint32_t* zeros_out, void* stream) {
+    LHQ_REQUIRE(gate_qweight && gate_scales && gate_zeros && up_qweight && up_scales && up_zeros && qweight &&
+                    scales_out && zeros_out,
+                "w4_interleave_gate_up: null pointer");
+    LHQ_REQUIRE(w4_dims_ok(K, I, G), "w4_interleave_gate_up: need K,I,G > 0, K even, G | K (K=%d I=%d G=%d)", K, I,
+                G);
+    const void* all[9] = {gate_qweight, gate_scales, gate_zeros, up_qweight, up_scales, up_zeros,
+                          qweight,      scales_out,  zeros_out};
+    for (const void* ptr : all) LHQ_REQUIRE(aligned16(ptr), "w4_interleave_gate_up: pointers must be 16-byte aligned");
+    const int Nt = ceil_div(I, kW4TileN), Kt = ceil_div(K, kW4TileK), NG = K / G, NG8 = ceil_div(NG, 8);
+    hipStream_t s = as_stream(stream);
+    if (int st = launch_interleave(gate_qweight, up_qweight, qweight, static_cast<int64_t>(Kt) * kW4TileBytes, Nt, s))
+        return st;
+    if (int st = launch_interleave(gate_scales, up_scales, scales_out, static_cast<int64_t>(NG) * kW4TileN * 2, Nt, s))
+        return st;
+    return launch_interleave(gate_zeros, up_zeros, zeros_out, static_cast<int64_t>(NG8) * kW4TileN * 4, Nt, s);
 }
 
 int64_t lhq_b8_prepacked_bytes(int K, int N) {

@@ -142,13 +142,25 @@ __device__ __forceinline__ void w4_store(const W4Args& p, int64_t o, float v) {
     }
 }
 
+// SwiGLU of one (gate, up) pair, moe.cpp:144-146 and :191: silu(g) * u with
+// silu(v) = v / (1 + exp(-v)), fp32, IEEE division.
+__device__ __forceinline__ float swiglu(float g, float u) { return g / (1.0f + expf(-g)) * u; }
+
+// SwiGLU epilogue (SWI): the weights interleave the gate and up projections
+// by column tile (lhq_w4_interleave_gate_up): tile 2j holds gate columns
+// 16j .. 16j+15 and tile 2j+1 the same up columns, so the accumulators of
+// one gate column and its up column sit in the same lane of two adjacent
+// tiles.  The kernel then writes act[r][16j + c] = bf16(swiglu(g, u)) with
+// p.N = the intermediate width (act's row length) and p.Nt = 2 ceil(N/16).
+
 // ---------------------------------------------------------------------------
 // Generic kernel.  grid = (ceil(Nt/T), row blocks, batch); a workgroup of
 // WAVES waves owns T column tiles and 16 rows; wave w walks its share of the
 // K tiles.  BPS = 32-wide k blocks per scale segment (min(G,128)/32).
 // ---------------------------------------------------------------------------
-template <bool F32A, bool ASYM, bool F32C, int T, int WAVES, int BPS, bool GROUPED>
+template <bool F32A, bool ASYM, bool F32C, int T, int WAVES, int BPS, bool GROUPED, bool SWI = false>
 __global__ __launch_bounds__(64 * WAVES) void w4_gemv_kernel(W4Args p) {
+    static_assert(!SWI || (T == 2 && !F32C), "SwiGLU pairs the two column tiles of a workgroup");
     constexpr int SEGS = 4 / BPS;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -240,8 +252,35 @@ __global__ __launch_bounds__(64 * WAVES) void w4_gemv_kernel(W4Args p) {
         if (r >= m_end || c >= p.N || nt0 + t >= p.Nt) return;
         w4_store<F32C>(p, z * p.c_bs + static_cast<int64_t>(r) * p.N + c, v);
     };
+    // SWI: tiles nt0 (gate) and nt0 + 1 (up) -> act column tile nt0 / 2
+    auto store_act = [&](int i, int ln, float g, float u) {
+        const int r = m0 + 4 * (ln >> 4) + i;
+        const int c = static_cast<int>(blockIdx.x) * kW4TileN + (ln & 15);
+        if (r >= m_end || c >= p.N) return;
+        static_cast<uint16_t*>(p.C)[z * p.c_bs + static_cast<int64_t>(r) * p.N + c] = f32_to_bf16(swiglu(g, u));
+    };
 
-    if constexpr (WAVES == 1) {
+    if constexpr (SWI && WAVES == 1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) store_act(i, lane, acc[0][i], acc[1][i]);
+    } else if constexpr (SWI) {
+        __shared__ float red[WAVES][2][4][64];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) red[wave][t][i][lane] = acc[t][i];
+        __syncthreads();
+        for (int idx = threadIdx.x; idx < 4 * 64; idx += 64 * WAVES) {
+            const int i = idx >> 6, ln = idx & 63;
+            float g = 0.0f, u = 0.0f;
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) {
+                g += red[w][0][i][ln];
+                u += red[w][1][i][ln];
+            }
+            store_act(i, ln, g, u);
+        }
+    } else if constexpr (WAVES == 1) {
 #pragma unroll
         for (int t = 0; t < T; ++t)
 #pragma unroll
@@ -916,7 +955,7 @@ constexpr int MM_DMA = MM_A_BYTES / 1024 / 4;       // activation DMAs per wave 
 
 #define LHQ_LDS_AS __attribute__((address_space(3)))
 
-template <int BPS, bool GBIG, bool GR>
+template <int BPS, bool GBIG, bool GR, bool SWI>
 __global__ __launch_bounds__(256, 2) void w4_mma_kernel(W4Args p) {
     constexpr int SEGS = 4 / BPS;
     extern __shared__ __attribute__((aligned(1024))) uint8_t mm_lds[];  // 2 x MM_A_BYTES
@@ -1089,6 +1128,24 @@ __global__ __launch_bounds__(256, 2) void w4_mma_kernel(W4Args p) {
     // D element r of block (i, c): row 64*wm + 16*i + 4*(lane >> 4) + r,
     // column of tile (blockIdx.x*8 + 4*wn + c), lane & 15
     uint16_t* C = static_cast<uint16_t*>(p.C) + (GR ? 0 : z * p.c_bs);
+    if constexpr (SWI) {
+        // blocks (c, c + 1) hold a gate tile and its up tile (nt even)
+#pragma unroll
+        for (int c = 0; c < MM_CT; c += 2) {
+            const int nt = static_cast<int>(blockIdx.x) * 2 * MM_CT + wn * MM_CT + c;
+            const int cn = (nt >> 1) * kW4TileN + col;
+            if (nt >= p.Nt || cn >= p.N) continue;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = m0 + wm * 64 + i * 16 + 4 * (lane >> 4) + r;
+                    if (row < m_end)
+                        C[static_cast<int64_t>(row) * p.N + cn] = f32_to_bf16(swiglu(acc[i][c][r], acc[i][c + 1][r]));
+                }
+        }
+        return;
+    }
 #pragma unroll
     for (int c = 0; c < MM_CT; ++c) {
         const int nt = static_cast<int>(blockIdx.x) * 2 * MM_CT + wn * MM_CT + c;
@@ -1162,12 +1219,12 @@ void launch_decode_bps(const W4Args& a, dim3 grid, int S, int bps, size_t lds, h
     else launch_decode_mr<F32A, ASYM, F32C, T, NPW, 4>(a, grid, S, bps, lds, s);
 }
 
-template <bool F32A, bool ASYM, bool F32C, int T, int WAVES, bool GR>
+template <bool F32A, bool ASYM, bool F32C, int T, int WAVES, bool GR, bool SWI>
 void launch_gemv_bps(const W4Args& a, dim3 grid, int bps, hipStream_t s) {
     switch (bps) {
-        case 1: w4_gemv_kernel<F32A, ASYM, F32C, T, WAVES, 1, GR><<<grid, 64 * WAVES, 0, s>>>(a); break;
-        case 2: w4_gemv_kernel<F32A, ASYM, F32C, T, WAVES, 2, GR><<<grid, 64 * WAVES, 0, s>>>(a); break;
-        default: w4_gemv_kernel<F32A, ASYM, F32C, T, WAVES, 4, GR><<<grid, 64 * WAVES, 0, s>>>(a); break;
+        case 1: w4_gemv_kernel<F32A, ASYM, F32C, T, WAVES, 1, GR, SWI><<<grid, 64 * WAVES, 0, s>>>(a); break;
+        case 2: w4_gemv_kernel<F32A, ASYM, F32C, T, WAVES, 2, GR, SWI><<<grid, 64 * WAVES, 0, s>>>(a); break;
+        default: w4_gemv_kernel<F32A, ASYM, F32C, T, WAVES, 4, GR, SWI><<<grid, 64 * WAVES, 0, s>>>(a); break;
     }
 }
 
@@ -1179,23 +1236,23 @@ void launch_i8_mr(const W4Args& a, dim3 grid, int S, size_t lds, hipStream_t s) 
     else w4_decode_i8_kernel<F32A, ASYM, F32C, T, NPW, 4, false, MR><<<grid, 64 * S, lds, s>>>(a);
 }
 
-template <bool F32A, bool ASYM, bool F32C, int T, bool GR>
+template <bool F32A, bool ASYM, bool F32C, int T, bool GR, bool SWI = false>
 void launch_gemv_waves(const W4Args& a, dim3 grid, int W, int bps, hipStream_t s) {
     switch (W) {
-        case 1: launch_gemv_bps<F32A, ASYM, F32C, T, 1, GR>(a, grid, bps, s); break;
-        case 2: launch_gemv_bps<F32A, ASYM, F32C, T, 2, GR>(a, grid, bps, s); break;
-        case 4: launch_gemv_bps<F32A, ASYM, F32C, T, 4, GR>(a, grid, bps, s); break;
-        default: launch_gemv_bps<F32A, ASYM, F32C, T, 8, GR>(a, grid, bps, s); break;
+        case 1: launch_gemv_bps<F32A, ASYM, F32C, T, 1, GR, SWI>(a, grid, bps, s); break;
+        case 2: launch_gemv_bps<F32A, ASYM, F32C, T, 2, GR, SWI>(a, grid, bps, s); break;
+        case 4: launch_gemv_bps<F32A, ASYM, F32C, T, 4, GR, SWI>(a, grid, bps, s); break;
+        default: launch_gemv_bps<F32A, ASYM, F32C, T, 8, GR, SWI>(a, grid, bps, s); break;
     }
 }
 
 // G >= 128 only (one scale group per K tile segment); smaller groups would
 // need four times the activation-sum registers and spill.
-template <bool GR>
+template <bool GR, bool SWI = false>
 void launch_mma(const W4Args& a, dim3 grid, hipStream_t s) {
     constexpr size_t lds = 2 * MM_A_BYTES;
-    if (a.gmul) w4_mma_kernel<4, true, GR><<<grid, 256, lds, s>>>(a);
-    else w4_mma_kernel<4, false, GR><<<grid, 256, lds, s>>>(a);
+    if (a.gmul) w4_mma_kernel<4, true, GR, SWI><<<grid, 256, lds, s>>>(a);
+    else w4_mma_kernel<4, false, GR, SWI><<<grid, 256, lds, s>>>(a);
 }
 
 // The prefill tile kernel serves the bf16 entry points when there are rows
@@ -1216,7 +1273,9 @@ bool mma_applies(const W4Args& a, int64_t rows, double rows_per_block) {
 
 // mblocks: 16-row blocks along grid.y (for a grouped launch, an upper bound
 // on the sum over groups of ceil(rows_e / 16)).
-template <bool F32A, bool ASYM, bool F32C, bool GR = false>
+// SWI (grouped bf16 only): the SwiGLU epilogue, two column tiles per
+// workgroup on the generic kernel.
+template <bool F32A, bool ASYM, bool F32C, bool GR = false, bool SWI = false>
 int launch_w4(W4Args a, int batch, hipStream_t s, int mblocks = -1) {
     static const int env_dec = env_int("LHQ_W4_DECODE");
     static const int env_dt = env_int("LHQ_W4_DEC_T");
@@ -1295,6 +1354,7 @@ int launch_w4(W4Args a, int batch, hipStream_t s, int mblocks = -1) {
 
     int T = (a.Nt >= 1024) ? 2 : 1;
     if (env_t == 1 || env_t == 2) T = env_t;
+    if constexpr (SWI) T = 2;
     // Enough waves to cover 256 CUs several times over, but at least four
     // K tiles per wave so each wave keeps loads in flight.
     const int64_t wgs = static_cast<int64_t>(ceil_div(a.Nt, T)) * mblocks * batch;
@@ -1302,7 +1362,8 @@ int launch_w4(W4Args a, int batch, hipStream_t s, int mblocks = -1) {
     while (W < 8 && wgs * W < 4096 && a.Kt / (2 * W) >= 4) W *= 2;
     if (env_w == 1 || env_w == 2 || env_w == 4 || env_w == 8) W = env_w;
     dim3 grid(ceil_div(a.Nt, T), mblocks, batch);
-    if (T == 1) launch_gemv_waves<F32A, ASYM, F32C, 1, GR>(a, grid, W, bps, s);
+    if constexpr (SWI) launch_gemv_waves<F32A, ASYM, F32C, 2, GR, true>(a, grid, W, bps, s);
+    else if (T == 1) launch_gemv_waves<F32A, ASYM, F32C, 1, GR>(a, grid, W, bps, s);
     else launch_gemv_waves<F32A, ASYM, F32C, 2, GR>(a, grid, W, bps, s);
     return check_launch("w4a16 gemv");
 }
@@ -1329,6 +1390,38 @@ W4Args make_args(const void* A, const uint8_t* qw, const void* sc, const uint32_
     a.gmul = (G > kW4TileK) ? static_cast<uint32_t>(((1ull << 32) + G / kW4TileK - 1) / (G / kW4TileK)) : 0u;
     a.alpha = alpha; a.beta = beta;
     return a;
+}
+
+// Ragged grouped launch (device-side group table).  SWI: N is the
+// intermediate width I, the weights hold 2 ceil(I/16) interleaved gate / up
+// column tiles, and C is act [rows, I].
+template <bool SWI>
+int grouped_w4(const char* who, const uint16_t* A, const int32_t* offsets, const uint8_t* const* qweights,
+               const uint16_t* const* scales, const uint32_t* const* zeros, uint16_t* C, int num_groups,
+               int row_capacity, int N, int K, int G, void* stream) {
+    if (int st = check_w4_shape(who, row_capacity, N, K, G)) return st;
+    LHQ_REQUIRE(num_groups >= 0, "%s: negative num_groups", who);
+    LHQ_REQUIRE(offsets && qweights && scales && zeros && C && (A || row_capacity == 0), "%s: null pointer", who);
+    if (num_groups == 0 || row_capacity == 0) return LHQ_OK;
+    W4Args a = make_args(A, nullptr, nullptr, nullptr, C, row_capacity, N, K, G, 1.0f, 0.0f);
+    if constexpr (SWI) a.Nt = 2 * ceil_div(N, kW4TileN);
+    a.offsets = offsets;
+    a.qws = qweights;
+    a.scs = reinterpret_cast<const void* const*>(scales);
+    a.zss = zeros;
+    a.num_groups = num_groups;
+    a.row_capacity = row_capacity;
+    if (mma_applies(a, row_capacity, static_cast<double>(row_capacity) / num_groups)) {
+        // sum_e ceil(rows_e / 128) <= ceil(row_capacity / 128) + num_groups
+        const int64_t tiles = ceil_div64(row_capacity, MM_BM) + num_groups;
+        LHQ_SUPPORTED(tiles <= 65535, "%s: %lld row tiles exceed the grid limit", who, static_cast<long long>(tiles));
+        launch_mma<true, SWI>(a, dim3(ceil_div(a.Nt, 2 * MM_CT), static_cast<unsigned>(tiles), 1), as_stream(stream));
+        return check_launch(who);
+    }
+    // sum_e ceil(rows_e / 16) <= ceil(row_capacity / 16) + num_groups
+    const int64_t mblocks = ceil_div64(row_capacity, 16) + num_groups;
+    LHQ_SUPPORTED(mblocks <= 65535, "%s: %lld row blocks exceed the grid limit", who, static_cast<long long>(mblocks));
+    return launch_w4<false, true, false, true, SWI>(a, 1, as_stream(stream), static_cast<int>(mblocks));
 }
 
 }  // namespace
@@ -1386,31 +1479,15 @@ int lhq_gemm_w4a16_bf16_batched(const uint16_t* A, const uint8_t* qweight, const
 int lhq_gemm_w4a16_bf16_grouped(const uint16_t* A, const int32_t* offsets, const uint8_t* const* qweights,
                                 const uint16_t* const* scales, const uint32_t* const* zeros, uint16_t* C,
                                 int num_groups, int row_capacity, int N, int K, int G, void* stream) {
-    if (int st = check_w4_shape("gemm_w4a16_bf16_grouped", row_capacity, N, K, G)) return st;
-    LHQ_REQUIRE(num_groups >= 0, "gemm_w4a16_bf16_grouped: negative num_groups");
-    LHQ_REQUIRE(offsets && qweights && scales && zeros && C && (A || row_capacity == 0),
-                "gemm_w4a16_bf16_grouped: null pointer");
-    if (num_groups == 0 || row_capacity == 0) return LHQ_OK;
-    W4Args a = make_args(A, nullptr, nullptr, nullptr, C, row_capacity, N, K, G, 1.0f, 0.0f);
-    a.offsets = offsets;
-    a.qws = qweights;
-    a.scs = reinterpret_cast<const void* const*>(scales);
-    a.zss = zeros;
-    a.num_groups = num_groups;
-    a.row_capacity = row_capacity;
-    if (mma_applies(a, row_capacity, static_cast<double>(row_capacity) / num_groups)) {
-        // sum_e ceil(rows_e / 128) <= ceil(row_capacity / 128) + num_groups
-        const int64_t tiles = ceil_div64(row_capacity, MM_BM) + num_groups;
-        LHQ_SUPPORTED(tiles <= 65535, "gemm_w4a16_bf16_grouped: %lld row tiles exceed the grid limit",
-                      static_cast<long long>(tiles));
-        launch_mma<true>(a, dim3(ceil_div(a.Nt, 2 * MM_CT), static_cast<unsigned>(tiles), 1), as_stream(stream));
-        return check_launch("w4a16 prefill grouped");
-    }
-    // sum_e ceil(rows_e / 16) <= ceil(row_capacity / 16) + num_groups
-    const int64_t mblocks = ceil_div64(row_capacity, 16) + num_groups;
-    LHQ_SUPPORTED(mblocks <= 65535, "gemm_w4a16_bf16_grouped: %lld row blocks exceed the grid limit",
-                  static_cast<long long>(mblocks));
-    return launch_w4<false, true, false, true>(a, 1, as_stream(stream), static_cast<int>(mblocks));
+    return grouped_w4<false>("gemm_w4a16_bf16_grouped", A, offsets, qweights, scales, zeros, C, num_groups,
+                             row_capacity, N, K, G, stream);
+}
+
+int lhq_gemm_w4a16_bf16_grouped_swiglu(const uint16_t* A, const int32_t* offsets, const uint8_t* const* qweights,
+                                       const uint16_t* const* scales, const uint32_t* const* zeros, uint16_t* act,
+                                       int num_groups, int row_capacity, int I, int K, int G, void* stream) {
+    return grouped_w4<true>("gemm_w4a16_bf16_grouped_swiglu", A, offsets, qweights, scales, zeros, act,
+                            num_groups, row_capacity, I, K, G, stream);
 }
 
 }  // extern "C"

@@ -138,6 +138,26 @@ def prepack_w4_asym(packed: torch.Tensor, scales_f16: torch.Tensor, zeros_u8: to
     return W4Weights(q, s, z, K, N, G, True)
 
 
+def interleave_gate_up(wg: W4Weights, wu: W4Weights) -> W4Weights:
+    """Gate and up projections [K, I] (asymmetric, prepacked) -> one tensor
+    with 2 ceil(I/16) interleaved column tiles; N stays I."""
+    if (wg.K, wg.N, wg.G, wg.asym) != (wu.K, wu.N, wu.G, wu.asym) or not wg.asym:
+        raise ValueError("gate and up must be asymmetric W4 of one shape")
+    q = empty((2 * wg.qweight.numel(),), np.uint8)
+    s = empty((2 * wg.scales.numel(),), np.int16)
+    z = empty((2 * wg.zeros.numel(),), np.int32)
+    lib().call("lhq_w4_interleave_gate_up", P(wg.qweight), P(wg.scales), P(wg.zeros), P(wu.qweight),
+               P(wu.scales), P(wu.zeros), wg.K, wg.N, wg.G, P(q), P(s), P(z), stream())
+    return W4Weights(q, s, z, wg.K, wg.N, wg.G, True)
+
+
+def pointer_tables(ws: list[W4Weights]):
+    """Device arrays of the per-group qweight / scales / zeros pointers."""
+    def tab(ts):
+        return torch.tensor([t.data_ptr() for t in ts], dtype=torch.int64, device="cuda")
+    return tab([w.qweight for w in ws]), tab([w.scales for w in ws]), tab([w.zeros for w in ws])
+
+
 def prepack_b8(B: torch.Tensor, K: int, N: int) -> torch.Tensor:
     nbytes = lib().lhq_b8_prepacked_bytes(K, N)
     Bt = empty((nbytes,), np.uint8)

@@ -84,6 +84,17 @@ _ORACLE_ONLY = {
     "gemm_w4a16_asym": (None, [_u16p, _u8p, _u16p, _u8p, _f32p, _i, _i, _i, _i]),
     "gemm_w4a16_asym_grouped": (None, [_u16p, _i32p, _u8p, _u16p, _u8p, _f32p, _i, _i, _i, _i]),
     "moe_dispatch_table": (None, [_i32p, _i, _i, _i, _i32p, _i32p, _i32p]),
+    "moe_dispatch": (None, [C.c_void_p, _i64, _i32p, _i, _i, _i, _i32p, _i32p, _i32p, _i32p,
+                            C.c_void_p]),
+    "swiglu_bf16": (None, [_f32p, _f32p, _u16p, _i64]),
+    "moe_combine_f32": (None, [_f32p, _i32p, _i32p, _f32p, _f32p, _i, _i, _i]),
+    "moe_combine_bf16": (None, [_u16p, _i32p, _i32p, _f32p, _u16p, _i, _i, _i]),
+}
+# the reference's MoE functions (moe.hpp:75-102), exported by ref_shim.cpp
+_REF_ONLY = {
+    "moe_dispatch": (None, [_f32p, _i32p, _i32p, _i32p, _i32p, _f32p, _i, _i, _i, _i]),
+    "moe_expert_mlp": (None, [_f32p, _i32p, _f32p, _f32p, _f32p, _f32p, _i, _i, _i]),
+    "moe_combine": (None, [_f32p, _i32p, _i32p, _i32p, _f32p, _f32p, _i, _i, _i, _i]),
 }
 
 
@@ -336,12 +347,82 @@ class Oracle(_Checker):
         self.fn["moe_dispatch_table"](ids, T, topk, E, off, tok, slot)
         return off, tok, slot
 
+    def moe_dispatch(self, hidden, expert_ids, E):
+        """moe.cpp:102-140 with the row copy; hidden is [T, H] of any dtype
+        (rows are copied as bytes).  Returns offsets, token_idx, slot_idx,
+        slot_pos and the dispatched rows [T*topk, H]."""
+        ids = _c(expert_ids, np.int32); T, topk = ids.shape
+        hidden = np.ascontiguousarray(hidden); assert hidden.shape[0] == T
+        out = np.zeros((T * topk,) + hidden.shape[1:], hidden.dtype)
+        off = np.empty(E + 1, np.int32)
+        tok = np.empty(T * topk, np.int32); slot = np.empty(T * topk, np.int32)
+        pos = np.empty(T * topk, np.int32)
+        rb = hidden.strides[0] if T else 0
+        self.fn["moe_dispatch"](hidden.ctypes.data, rb, ids, T, topk, E, off, tok, slot, pos,
+                                out.ctypes.data)
+        return off, tok, slot, pos, out
+
+    def swiglu_bf16(self, g, u):
+        g = _c(g, np.float32); u = _c(u, np.float32); act = np.empty(g.shape, np.uint16)
+        self.fn["swiglu_bf16"](g, u, act, g.size)
+        return act
+
+    def moe_combine_f32(self, y, token_idx, slot_idx, gates):
+        gates = _c(gates, np.float32); T, topk = gates.shape; H = y.shape[1]
+        out = np.empty((T, H), np.float32)
+        self.fn["moe_combine_f32"](_c(y, np.float32), _c(token_idx, np.int32), _c(slot_idx, np.int32),
+                                   gates, out, T, H, topk)
+        return out
+
+    def moe_combine_bf16(self, y, token_idx, slot_idx, gates):
+        gates = _c(gates, np.float32); T, topk = gates.shape; H = y.shape[1]
+        out = np.empty((T, H), np.uint16)
+        self.fn["moe_combine_bf16"](_c(y, np.uint16), _c(token_idx, np.int32), _c(slot_idx, np.int32),
+                                    gates, out, T, H, topk)
+        return out
+
+    def moe_expert_mlp_w4a16(self, X, offsets, gate, up, down, H, I, G):
+        """The quantized expert MLP (moe.cpp:150-196 with W4A16 experts, the
+        hook of moe.hpp:26-28): per expert, gate and up projections in fp32,
+        act = bf16(silu(g) * u), then the down projection, output rounded to
+        bf16.  gate / up / down are (packed, scales, zeros) stacks over the
+        experts in the lho_q4a layout.  Returns (act, y) as bf16 bits; rows
+        past offsets[E] are zero."""
+        g = self.gemm_w4a16_asym_grouped(X, offsets, *gate, I, G)
+        u = self.gemm_w4a16_asym_grouped(X, offsets, *up, I, G)
+        act = self.swiglu_bf16(g, u)
+        y = self.gemm_w4a16_asym_grouped(act, offsets, *down, H, G)
+        return act, self.f32_to_bf16_n(y)
+
 
 class Ref(_Checker):
     """The reference's own sources, compiled in oracle/_ref (optional)."""
 
     def __init__(self, so_path: str = REF_SO):
-        super().__init__(so_path, "ref_", _COMMON)
+        super().__init__(so_path, "ref_", {**_COMMON, **_REF_ONLY})
+
+    def moe_dispatch(self, hidden, expert_ids, E):
+        ids = _c(expert_ids, np.int32); T, topk = ids.shape
+        hidden = _c(hidden, np.float32); H = hidden.shape[1]
+        off = np.empty(E + 1, np.int32)
+        tok = np.empty(T * topk, np.int32); slot = np.empty(T * topk, np.int32)
+        out = np.empty((T * topk, H), np.float32)
+        self.fn["moe_dispatch"](hidden, ids, off, tok, slot, out, T, H, E, topk)
+        return off, tok, slot, out
+
+    def moe_expert_mlp(self, X, offsets, Wg, Wu, Wd):
+        X = _c(X, np.float32); E, H, I = Wg.shape
+        y = np.zeros((X.shape[0], H), np.float32)
+        self.fn["moe_expert_mlp"](X, _c(offsets, np.int32), _c(Wg, np.float32), _c(Wu, np.float32),
+                                  _c(Wd, np.float32), y, H, I, E)
+        return y
+
+    def moe_combine(self, y, offsets, token_idx, slot_idx, gates):
+        gates = _c(gates, np.float32); T, topk = gates.shape; H = y.shape[1]
+        out = np.empty((T, H), np.float32)
+        self.fn["moe_combine"](_c(y, np.float32), _c(offsets, np.int32), _c(token_idx, np.int32),
+                               _c(slot_idx, np.int32), gates, out, T, H, len(offsets) - 1, topk)
+        return out
 
 
 def ref_available() -> bool:

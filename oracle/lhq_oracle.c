@@ -657,24 +657,101 @@ EXPORT void lho_gemm_w4a16_asym_grouped(const uint16_t* A, const int32_t* offset
     }
 }
 
-/* moe.cpp:102-140 steps 1-3 without the activation copy: counts per expert,
- * exclusive prefix sum into offsets[E+1], then a stable placement that keeps
- * token order inside each expert.  token_idx/slot_idx have T*topk entries. */
-EXPORT void lho_moe_dispatch_table(const int32_t* expert_ids, int T, int topk,
-                                   int E, int32_t* offsets, int32_t* token_idx,
-                                   int32_t* slot_idx) {
-    int32_t* cursor = (int32_t*)calloc((size_t)E, sizeof(int32_t));
+/* ---------------------------------------------------------------------- */
+/* MoE dispatch, SwiGLU and combine (moe.cpp:102-221)                      */
+
+/* moe.cpp:102-140: count the T*topk (token, slot) pairs per expert (:111-118),
+ * exclusive prefix sum into offsets[E+1] (:119-123), then place each pair at
+ * offsets[e] + cursor[e]++ in (token, slot) order, recording token_idx and
+ * slot_idx and copying the token's row (:124-139).  Rows are row_bytes wide:
+ * fp32 rows in the reference, bf16 rows in the benchmark pipeline (hidden and
+ * out may be NULL when row_bytes == 0).
+ * Extensions: slot_pos[t*topk + k] (may be NULL) receives the position pair
+ * (t, k) went to -- the inverse map that moe_combine's slot loop
+ * (moe.cpp:213-220) walks implicitly.  An id outside [0, E) is dropped (the
+ * reference would index past `counts`): it gets slot_pos -1, is not counted,
+ * and positions offsets[E] .. T*topk-1 hold token_idx = slot_idx = -1. */
+EXPORT void lho_moe_dispatch(const void* hidden, int64_t row_bytes,
+                             const int32_t* expert_ids, int T, int topk,
+                             int E, int32_t* offsets, int32_t* token_idx,
+                             int32_t* slot_idx, int32_t* slot_pos, void* out) {
+    int32_t* cursor = (int32_t*)calloc((size_t)E + 1, sizeof(int32_t));
     for (int t = 0; t < T; ++t)
-        for (int k = 0; k < topk; ++k) cursor[expert_ids[t * topk + k]]++;
+        for (int k = 0; k < topk; ++k) {
+            int e = expert_ids[t * topk + k];
+            if (e >= 0 && e < E) cursor[e]++;
+        }
     offsets[0] = 0;
     for (int e = 0; e < E; ++e) offsets[e + 1] = offsets[e] + cursor[e];
     for (int e = 0; e < E; ++e) cursor[e] = 0;
     for (int t = 0; t < T; ++t)
         for (int k = 0; k < topk; ++k) {
             int e = expert_ids[t * topk + k];
+            if (e < 0 || e >= E) {
+                if (slot_pos) slot_pos[t * topk + k] = -1;
+                continue;
+            }
             int pos = offsets[e] + cursor[e]++;
             token_idx[pos] = t;
             slot_idx[pos] = k;
+            if (slot_pos) slot_pos[t * topk + k] = pos;
+            if (row_bytes > 0)
+                memcpy((char*)out + (int64_t)pos * row_bytes,
+                       (const char*)hidden + (int64_t)t * row_bytes, (size_t)row_bytes);
         }
+    for (int64_t s = offsets[E]; s < (int64_t)T * topk; ++s) token_idx[s] = slot_idx[s] = -1;
     free(cursor);
+}
+
+/* moe.cpp:102-140 steps 1-3 without the activation copy. */
+EXPORT void lho_moe_dispatch_table(const int32_t* expert_ids, int T, int topk,
+                                   int E, int32_t* offsets, int32_t* token_idx,
+                                   int32_t* slot_idx) {
+    lho_moe_dispatch(NULL, 0, expert_ids, T, topk, E, offsets, token_idx, slot_idx, NULL, NULL);
+}
+
+/* moe.cpp:144-146 and :187-192: act = silu(g) * u with
+ * silu(v) = v / (1 + exp(-v)), in fp32; BASELINE extension: the product is
+ * rounded to bf16, the activation the down projection reads. */
+EXPORT void lho_swiglu_bf16(const float* g, const float* u, uint16_t* act, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) {
+        float s = g[i] / (1.0f + expf(-g[i]));
+        act[i] = lho_f32_to_bf16(s * u[i]);
+    }
+}
+
+/* moe.cpp:198-221: output zeroed (:207-208), then one pass over the
+ * dispatched slots in order, output[t] += gate[t, k] * y[s] with
+ * t = token_idx[s], k = slot_idx[s] (:213-220); fp32, each product and sum
+ * rounded.  Slots with token_idx < 0 (dropped ids) are skipped. */
+EXPORT void lho_moe_combine_f32(const float* y, const int32_t* token_idx,
+                                const int32_t* slot_idx, const float* gates,
+                                float* out, int T, int H, int topk) {
+    for (int64_t i = 0; i < (int64_t)T * H; ++i) out[i] = 0.0f;
+    for (int64_t s = 0; s < (int64_t)T * topk; ++s) {
+        int t = token_idx[s], k = slot_idx[s];
+        if (t < 0) continue;
+        float gate = gates[(int64_t)t * topk + k];
+        const float* ys = y + s * H;
+        float* o = out + (int64_t)t * H;
+        for (int i = 0; i < H; ++i) o[i] += gate * ys[i];
+    }
+}
+
+/* BASELINE extension: the same sum over bf16 expert outputs (widened
+ * exactly), rounded to bf16 once at the end. */
+EXPORT void lho_moe_combine_bf16(const uint16_t* y, const int32_t* token_idx,
+                                 const int32_t* slot_idx, const float* gates,
+                                 uint16_t* out, int T, int H, int topk) {
+    float* acc = (float*)calloc((size_t)T * (size_t)H + 1, sizeof(float));
+    for (int64_t s = 0; s < (int64_t)T * topk; ++s) {
+        int t = token_idx[s], k = slot_idx[s];
+        if (t < 0) continue;
+        float gate = gates[(int64_t)t * topk + k];
+        const uint16_t* ys = y + s * H;
+        float* o = acc + (int64_t)t * H;
+        for (int i = 0; i < H; ++i) o[i] += gate * lho_bf16_to_f32(ys[i]);
+    }
+    for (int64_t i = 0; i < (int64_t)T * H; ++i) out[i] = lho_f32_to_bf16(acc[i]);
+    free(acc);
 }

@@ -5,12 +5,14 @@
 // and lets bench.py time the reference CPU path.  Nothing here is shipped.
 //
 // Each wrapper forwards to one lh:: function with unchanged arguments:
-//   quant.hpp:31-94, gemm_quant.hpp:42-70, gemm.hpp:14-29, dtypes.hpp:17-269.
+//   quant.hpp:31-94, gemm_quant.hpp:42-70, gemm.hpp:14-29, dtypes.hpp:17-269,
+//   moe.hpp:75-102 (dispatch, expert MLP, combine; MoEConfig moe.hpp:39-49).
 #include <cstdint>
 
 #include "kernels/dtypes.hpp"
 #include "kernels/gemm.hpp"
 #include "kernels/gemm_quant.hpp"
+#include "kernels/moe.hpp"
 #include "kernels/quant.hpp"
 
 static_assert(sizeof(lh::fp8_e4m3) == 1, "fp8_e4m3 must be one byte");
@@ -87,6 +89,28 @@ void ref_gemm(const float* A, const float* B, float* C, int M, int N, int K, flo
 void ref_gemm_batched(const float* A, const float* B, float* C, int batch, int M, int N, int K,
                       float alpha, float beta) {
     lh::gemm_batched(A, B, C, batch, M, N, K, alpha, beta);
+}
+
+static lh::MoEConfig moe_cfg(int T, int H, int I, int E, int K) {
+    lh::MoEConfig c;
+    c.n_tokens = T;
+    c.hidden_dim = H;
+    c.intermediate_dim = I;
+    c.n_experts = E;
+    c.top_k = K;
+    return c;
+}
+void ref_moe_dispatch(const float* hidden, const int32_t* ids, int32_t* offsets, int32_t* tok,
+                      int32_t* slot, float* out, int T, int H, int E, int K) {
+    lh::moe_dispatch(hidden, ids, offsets, tok, slot, out, moe_cfg(T, H, 0, E, K));
+}
+void ref_moe_expert_mlp(const float* x, const int32_t* offsets, const float* Wg, const float* Wu,
+                        const float* Wd, float* y, int H, int I, int E) {
+    lh::moe_expert_mlp(x, offsets, Wg, Wu, Wd, y, moe_cfg(0, H, I, E, 1));
+}
+void ref_moe_combine(const float* y, const int32_t* offsets, const int32_t* tok, const int32_t* slot,
+                     const float* gates, float* out, int T, int H, int E, int K) {
+    lh::moe_combine(y, offsets, tok, slot, gates, out, moe_cfg(T, H, 0, E, K));
 }
 
 }  // extern "C"
