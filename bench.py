@@ -229,6 +229,101 @@ def bench_moe(ops, steps, warmup, seed=0, T=512, E=8, topk=2, K=4096, N=14336, G
     return res
 
 
+def bench_moe_layer(ops, steps, warmup, seed=0, T=512, E=8, topk=2, H=4096, I=14336, G=128):
+    """Config 4's MoE layer end to end on the device (moe.cpp:102-221 with
+    W4A16 experts): dispatch -> gate/up projection with the SwiGLU epilogue
+    -> down projection -> combine, Mixtral shapes.  Each stage is timed on its
+    own (HIP graphs of `steps` launches), then the chain."""
+    import numpy as np
+    import torch
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    scores = torch.rand((T, E), generator=gen, device="cuda")
+    top = torch.topk(scores, topk, dim=1)
+    ids = top.indices.to(torch.int32).contiguous()
+    gates = torch.softmax(top.values, dim=1).contiguous()
+    S = T * topk
+    x = torch.randn((T, H), generator=gen, device="cuda").to(torch.bfloat16).view(torch.int16)
+    gate = make_w4_sets(ops, H, I, G, E, seed + 1)
+    up = make_w4_sets(ops, H, I, G, E, seed + 2)
+    gu = [ops.interleave_gate_up(a, b) for a, b in zip(gate, up)]
+    del gate, up
+    down = make_w4_sets(ops, I, H, G, E, seed + 3)
+    guq, gus, guz = ops.pointer_tables(gu)
+    dq, ds, dz = ops.pointer_tables(down)
+    off = ops.zeros((E + 1,), np.int32)
+    tok, slot, pos = (ops.zeros((S,), np.int32) for _ in range(3))
+    xs = ops.empty((S, H), np.int16)
+    act = ops.empty((S, I), np.int16)
+    y = ops.empty((S, H), np.int16)
+    out = ops.empty((T, H), np.int16)
+    L = ops.lib()
+    st = ops.stream
+
+    def chk(name, status):
+        if status:
+            raise RuntimeError(f"{name}: {L.last_error()}")
+
+    def dispatch(_i):
+        chk("dispatch", L.cdll.lhq_moe_dispatch_bf16(x.data_ptr(), ids.data_ptr(), off.data_ptr(), tok.data_ptr(),
+                                                     slot.data_ptr(), pos.data_ptr(), xs.data_ptr(), T, H, E, topk,
+                                                     st()))
+
+    def gate_up(_i):
+        chk("gate_up", L.cdll.lhq_gemm_w4a16_bf16_grouped_swiglu(xs.data_ptr(), off.data_ptr(), guq.data_ptr(),
+                                                                 gus.data_ptr(), guz.data_ptr(), act.data_ptr(), E,
+                                                                 S, I, H, G, st()))
+
+    def down_proj(_i):
+        chk("down", L.cdll.lhq_gemm_w4a16_bf16_grouped(act.data_ptr(), off.data_ptr(), dq.data_ptr(), ds.data_ptr(),
+                                                       dz.data_ptr(), y.data_ptr(), E, S, H, I, G, st()))
+
+    def combine(_i):
+        chk("combine", L.cdll.lhq_moe_combine_bf16(y.data_ptr(), pos.data_ptr(), gates.data_ptr(), out.data_ptr(),
+                                                   T, H, topk, st()))
+
+    def layer(i):
+        dispatch(i)
+        gate_up(i)
+        down_proj(i)
+        combine(i)
+
+    dispatch(0)
+    torch.cuda.synchronize()
+    rows = (off[1:] - off[:-1]).cpu().numpy().tolist()
+    wbytes = lambda K, N: E * (K * N // 2 + (K // G) * N * 2 + (K // G) * N // 2)  # noqa: E731
+    stages = {
+        "dispatch": (dispatch, 0, T * H * 2 + S * H * 2 + T * topk * 4 * 4),
+        "gate_up_swiglu": (gate_up, 2 * S * H * 2 * I, wbytes(H, 2 * I) + S * H * 2 + S * I * 2),
+        "down": (down_proj, 2 * S * I * H, wbytes(I, H) + S * I * 2 + S * H * 2),
+        "combine": (combine, 0, S * H * 2 + T * H * 2 + T * topk * 8),
+    }
+    res = {"tokens": T, "experts": E, "top_k": topk, "hidden": H, "intermediate": I, "G": G,
+           "rows_per_expert": rows, "stages": {}}
+    total_flops = total_bytes = 0
+    for name, (fn, flops, byts) in stages.items():
+        n = steps if flops else 4 * steps
+        ms, _ = GraphTimer(fn, 1, chunk=16).time(n, max(2, warmup))
+        us = ms * 1e3 / n
+        r = {"us": round(us, 2), "gbs": round(byts / (us * 1e-6) / 1e9, 1),
+             "hbm_frac": round(byts / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "bytes": byts}
+        if flops:
+            tf = flops / (us * 1e-6) / 1e12
+            r.update({"tflops": round(tf, 1), "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4), "flops": flops})
+        res["stages"][name] = r
+        total_flops += flops
+        total_bytes += byts
+    ms, _ = GraphTimer(layer, 1, chunk=8).time(steps, max(2, warmup))
+    us = ms * 1e3 / steps
+    res.update({"layer_us": round(us, 2), "tokens_per_s": round(T / (us * 1e-6), 1),
+                "layer_tflops": round(total_flops / (us * 1e-6) / 1e12, 1),
+                "layer_gbs": round(total_bytes / (us * 1e-6) / 1e9, 1)})
+    del gu, down, x, xs, act, y, out
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_w8a8(ops, M, K, N, steps, warmup, seed=0):
     import numpy as np
     import torch
@@ -403,7 +498,18 @@ def prefill_legs(ops):
     log(f"  {r['us_per_call']:.1f} us/call  {r['tflops']:.0f} TFLOPS ({100 * r['mfma_frac']:.1f}% of bf16 peak), "
         f"{r['gbs']:.0f} GB/s")
     out.append({"leg": "moe_grouped_w4a16", **{k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}})
+    out.append(moe_layer_leg(ops))
     return out
+
+
+def moe_layer_leg(ops):
+    log("moe layer (config 4, Mixtral shapes): dispatch, gate/up + SwiGLU, down, combine")
+    r = bench_moe_layer(ops, 100, 10)
+    for name, st in r["stages"].items():
+        extra = f"  {st['tflops']:.0f} TFLOPS ({100 * st['mfma_frac']:.1f}%)" if "tflops" in st else ""
+        log(f"  {name}: {st['us']:.1f} us  {st['gbs']:.0f} GB/s{extra}")
+    log(f"  layer: {r['layer_us']:.1f} us ({r['tokens_per_s'] / 1e6:.2f} M tokens/s)")
+    return {"leg": "moe_layer_w4a16", **r}
 
 
 def main() -> int:
@@ -418,7 +524,7 @@ def main() -> int:
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a 1 GiB device copy (PMC calibration kernel)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the W4A16 prefill and MoE legs")
-    ap.add_argument("--only", choices=["w4a16", "w8a8", "prefill"], default=None,
+    ap.add_argument("--only", choices=["w4a16", "w8a8", "prefill", "moe"], default=None,
                     help="run one leg only (profiling); prints that leg's summary, not the bench line")
     args = ap.parse_args()
 
@@ -445,6 +551,9 @@ def main() -> int:
         for m in (4096, 2048):
             r = bench_w8a8(ops, m, 4096, 14336, args.w8a8_steps, max(10, args.w8a8_steps // 10))
             print(json.dumps({"leg": "w8a8_prefill", **r}), flush=True)
+        return 0
+    if args.only == "moe":
+        print(json.dumps(moe_layer_leg(ops)), flush=True)
         return 0
     if args.only == "prefill":
         for r in prefill_legs(ops):

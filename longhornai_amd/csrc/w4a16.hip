@@ -927,10 +927,18 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512) void w4_decode_i8_kernel(W4Arg
 // ---------------------------------------------------------------------------
 // Prefill tile kernel: bf16 activations and output, asymmetric int4 weights,
 // many rows (plain, uniform batches, ragged groups).  A 256-thread
-// workgroup owns a 128 x 128 output tile; wave (wm, wn) owns rows
-// 64*wm .. +63 and columns 64*wn .. +63 as 4 x 4 blocks of 16x16x32 MFMA
-// accumulators.  Per 128-deep K tile:
-//   - the workgroup's 128 activation rows x 128 k (32 KiB) go global -> LDS
+// workgroup owns an output tile in one of three layouts (L):
+//   L = 0: 128 x 128, waves (wm, wn) in 2 x 2;
+//   L = 1:  64 x 256, waves wn = 0..3 on the same 64 rows (a ragged group's
+//           rows are padded to 64, not 128);
+//   L = 2:  64 x 128 with K split in two, waves (ks, wn) in 2 x 2: half ks
+//           walks K tiles ks*ceil(Kt/2) .. and half 1 hands its accumulators
+//           to half 0 through LDS at the end (a fixed order: deterministic);
+//           twice the workgroups of L = 1 where those cannot fill the chip.
+// A wave owns 64 rows x 64 columns (4 column tiles) as 4 x 4 blocks of
+// 16x16x32 MFMA accumulators in every layout.  Per 128-deep K tile:
+//   - the workgroup's activations (64 rows x 128 k per row group or K half)
+//     go global -> LDS
 //     by DMA into one of two buffers; 16-byte chunk c of row r sits in slot
 //     c ^ (r & 15), so the 16 rows of a fragment read hit 16 different bank
 //     groups;
@@ -947,21 +955,30 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512) void w4_decode_i8_kernel(W4Arg
 // row; column tiles past Nt re-read the last one).  Requires K % 128 == 0
 // (the activations are not zero-padded in LDS).
 // ---------------------------------------------------------------------------
-constexpr int MM_BM = 128;                          // rows per workgroup tile
-constexpr int MM_CT = 4;                            // column tiles per wave
-constexpr int MM_BN = 2 * MM_CT * kW4TileN;         // columns per workgroup tile (128)
-constexpr int MM_A_BYTES = MM_BM * kW4TileK * 2;    // one activation buffer (32 KiB)
-constexpr int MM_DMA = MM_A_BYTES / 1024 / 4;       // activation DMAs per wave per tile (8)
+constexpr int MM_CT = 4;  // column tiles per wave
+// rows per workgroup tile: L == 0 ? 128 : 64; column tiles per workgroup:
+// (L == 1 ? 4 : 2) * MM_CT; one activation buffer: (L == 1 ? 64 : 128) rows of
+// 128 k x 2 bytes
 
 #define LHQ_LDS_AS __attribute__((address_space(3)))
 
-template <int BPS, bool GBIG, bool GR, bool SWI>
+template <int BPS, bool GBIG, bool GR, bool SWI, int L>
 __global__ __launch_bounds__(256, 2) void w4_mma_kernel(W4Args p) {
     constexpr int SEGS = 4 / BPS;
-    extern __shared__ __attribute__((aligned(1024))) uint8_t mm_lds[];  // 2 x MM_A_BYTES
+    constexpr int BM = (L == 0) ? 128 : 64, WN = (L == 1) ? 4 : 2;
+    constexpr int A_BYTES = ((L == 1) ? 64 : 128) * kW4TileK * 2;
+    constexpr int DMA = A_BYTES / 1024 / 4;  // activation DMAs per wave per K tile
+    extern __shared__ __attribute__((aligned(1024))) uint8_t mm_lds[];  // 2 x A_BYTES
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    // this wave's LDS activation region (row group or K half), row group,
+    // K half and column group
+    const int wr = (L == 1) ? 0 : (wave >> 1);
+    const int wm = (L == 0) ? wr : 0;
+    const int ks = (L == 2) ? wr : 0;
+    const int wn = (L == 1) ? wave : (wave & 1);
+    const int kh = (L == 2) ? (p.Kt + 1) / 2 : p.Kt;  // K tiles per half
+    const int kofs = ks * kh;                           // this wave's first K tile
     const int z = blockIdx.z;
     int m0, m_end;
     const uint8_t* qw;
@@ -969,12 +986,12 @@ __global__ __launch_bounds__(256, 2) void w4_mma_kernel(W4Args p) {
     const uint32_t* zs;
     if constexpr (GR) {
         int e;
-        if (!resolve_group<MM_BM>(p, blockIdx.y, e, m0, m_end)) return;  // uniform per workgroup
+        if (!resolve_group<BM>(p, blockIdx.y, e, m0, m_end)) return;  // uniform per workgroup
         qw = p.qws[e];
         sc = static_cast<const uint16_t*>(p.scs[e]);
         zs = p.zss[e];
     } else {
-        m0 = blockIdx.y * MM_BM;
+        m0 = blockIdx.y * BM;
         m_end = p.M;
         qw = p.qw + z * p.qw_bs;
         sc = static_cast<const uint16_t*>(p.scales) + z * p.s_bs;
@@ -986,19 +1003,23 @@ __global__ __launch_bounds__(256, 2) void w4_mma_kernel(W4Args p) {
     // activation DMA q of this wave: chunk idx = (8*wave + q)*64 + lane is
     // row idx >> 4, LDS slot idx & 15, global chunk slot ^ (row & 15);
     // element offsets are 32-bit (the launcher bounds rows * K)
-    uint32_t a_off[MM_DMA];
+    // (a fixed bound: a bound that depends on a template parameter, with the
+    // array captured by the lambdas below, makes hipcc's host pass drop the
+    // kernel's launch stub without a diagnostic; entries past DMA are unused)
+    static_assert(DMA <= 8, "activation DMAs per wave");
+    uint32_t a_off[8];
 #pragma unroll
-    for (int q = 0; q < MM_DMA; ++q) {
-        const int idx = (MM_DMA * wave + q) * 64 + lane;
-        const int r = idx >> 4, slot = idx & 15;
-        const int row = min(m0 + r, m_end - 1);
+    for (int q = 0; q < DMA; ++q) {
+        const int idx = (DMA * wave + q) * 64 + lane;
+        const int r = idx >> 4, slot = idx & 15;  // LDS row r: region r >> 6 (this wave's, wr)
+        const int row = min(m0 + ((L == 2) ? (r & 63) : r), m_end - 1);
         a_off[q] = static_cast<uint32_t>(row) * static_cast<uint32_t>(p.K) + static_cast<uint32_t>((slot ^ (r & 15)) * 8);
     }
     // this wave's column tiles (clamped to the last one) and their bases
     uint32_t w_base[MM_CT], s_base[MM_CT], z_base[MM_CT];
 #pragma unroll
     for (int c = 0; c < MM_CT; ++c) {
-        const int nt = min(static_cast<int>(blockIdx.x) * 2 * MM_CT + wn * MM_CT + c, p.Nt - 1);
+        const int nt = min(static_cast<int>(blockIdx.x) * WN * MM_CT + wn * MM_CT + c, p.Nt - 1);
         w_base[c] = static_cast<uint32_t>(nt * p.Kt) * kW4TileBytes + static_cast<uint32_t>(lane * 16);
         s_base[c] = static_cast<uint32_t>(nt * p.NG * 16 + (col & ~1));  // fp16 pair holding this column
         z_base[c] = static_cast<uint32_t>(nt * p.NG8 * 16 + col);
@@ -1012,11 +1033,11 @@ __global__ __launch_bounds__(256, 2) void w4_mma_kernel(W4Args p) {
     };
     // all loads of K tile kt (clamped) into LDS buffer buf and registers R
     auto issue = [&](uint8_t* buf, Regs& R, int kt_in) {
-        const int kt = min(kt_in, p.Kt - 1);
+        const int kt = min(kt_in + kofs, p.Kt - 1);
         const uint32_t k0 = static_cast<uint32_t>(kt * kW4TileK);
 #pragma unroll
-        for (int q = 0; q < MM_DMA; ++q)
-            __builtin_amdgcn_global_load_lds(A + (a_off[q] + k0), (LHQ_LDS_AS void*)(buf + (MM_DMA * wave + q) * 1024),
+        for (int q = 0; q < DMA; ++q)
+            __builtin_amdgcn_global_load_lds(A + (a_off[q] + k0), (LHQ_LDS_AS void*)(buf + (DMA * wave + q) * 1024),
                                              16, 0, 0);
 #pragma unroll
         for (int c = 0; c < MM_CT; ++c) {
@@ -1035,17 +1056,18 @@ __global__ __launch_bounds__(256, 2) void w4_mma_kernel(W4Args p) {
 #pragma unroll
         for (int c = 0; c < MM_CT; ++c) acc[i][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     const u32x4_t ones = {kOnesBf16x2, kOnesBf16x2, kOnesBf16x2, kOnesBf16x2};
-    // fragment (row block i, k block j): row 64*wm + 16*i + (lane & 15), k
+    // fragment (row block i, k block j): LDS row 64*wr + 16*i + (lane & 15), k
     // chunk 4j + (lane >> 4), stored in slot chunk ^ (lane & 15)
-    const uint32_t a_frag = static_cast<uint32_t>((wm * 64 + col) * 256);
+    const uint32_t a_frag = static_cast<uint32_t>((wr * 64 + col) * 256);
 
     // a wave whose 64 rows all lie past the block's last row (a ragged
     // group's tail block, or M <= 64) has nothing to compute; it still
     // takes part in the loads and rendezvous, and its SIMD time goes to
     // the other waves resident there
     const bool live = m0 + 64 * wm < m_end;
-    auto compute = [&](const uint8_t* buf, const Regs& R, int kt) {
-        if (!live) return;
+    auto compute = [&](const uint8_t* buf, const Regs& R, int kt_in) {
+        const int kt = kt_in + kofs;
+        if (!live || kt >= p.Kt) return;  // the second K half may be one tile short
         u32x4_t a[4][4];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -1107,11 +1129,11 @@ __global__ __launch_bounds__(256, 2) void w4_mma_kernel(W4Args p) {
     };
 
     uint8_t* const buf0 = mm_lds;
-    uint8_t* const buf1 = mm_lds + MM_A_BYTES;
+    uint8_t* const buf1 = mm_lds + A_BYTES;
     Regs ra, rb;
     issue(buf0, ra, 0);
     int kt = 0;
-    for (; kt + 2 <= p.Kt; kt += 2) {
+    for (; kt + 2 <= kh; kt += 2) {
         rendezvous();
         issue(buf1, rb, kt + 1);
         compute(buf0, ra, kt);
@@ -1119,11 +1141,35 @@ __global__ __launch_bounds__(256, 2) void w4_mma_kernel(W4Args p) {
         issue(buf0, ra, kt + 2);  // clamped past the end: never used
         compute(buf1, rb, kt + 1);
     }
-    if (kt < p.Kt) {
+    if (kt < kh) {
         rendezvous();
         compute(buf0, ra, kt);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    if constexpr (L == 2) {
+        // K half 1 hands its accumulators to half 0 through LDS: after the
+        // barrier every wave's loads have landed and no wave reads the
+        // activation buffers again
+        __syncthreads();
+        f32x4_t* red = reinterpret_cast<f32x4_t*>(mm_lds) + wn * (4 * MM_CT * 64);
+        if (ks == 1) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int c = 0; c < MM_CT; ++c) red[(i * MM_CT + c) * 64 + lane] = acc[i][c];
+        }
+        __syncthreads();
+        if (ks == 1) return;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int c = 0; c < MM_CT; ++c) {
+                const f32x4_t h = red[(i * MM_CT + c) * 64 + lane];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[i][c][r] += h[r];
+            }
+    }
 
     // D element r of block (i, c): row 64*wm + 16*i + 4*(lane >> 4) + r,
     // column of tile (blockIdx.x*8 + 4*wn + c), lane & 15
@@ -1132,7 +1178,7 @@ __global__ __launch_bounds__(256, 2) void w4_mma_kernel(W4Args p) {
         // blocks (c, c + 1) hold a gate tile and its up tile (nt even)
 #pragma unroll
         for (int c = 0; c < MM_CT; c += 2) {
-            const int nt = static_cast<int>(blockIdx.x) * 2 * MM_CT + wn * MM_CT + c;
+            const int nt = static_cast<int>(blockIdx.x) * WN * MM_CT + wn * MM_CT + c;
             const int cn = (nt >> 1) * kW4TileN + col;
             if (nt >= p.Nt || cn >= p.N) continue;
 #pragma unroll
@@ -1148,7 +1194,7 @@ __global__ __launch_bounds__(256, 2) void w4_mma_kernel(W4Args p) {
     }
 #pragma unroll
     for (int c = 0; c < MM_CT; ++c) {
-        const int nt = static_cast<int>(blockIdx.x) * 2 * MM_CT + wn * MM_CT + c;
+        const int nt = static_cast<int>(blockIdx.x) * WN * MM_CT + wn * MM_CT + c;
         const int cn = nt * kW4TileN + col;
         if (nt >= p.Nt || cn >= p.N) continue;
 #pragma unroll
@@ -1248,11 +1294,50 @@ void launch_gemv_waves(const W4Args& a, dim3 grid, int W, int bps, hipStream_t s
 
 // G >= 128 only (one scale group per K tile segment); smaller groups would
 // need four times the activation-sum registers and spill.
+template <bool GR, bool SWI, int L>
+void launch_mma_l(const W4Args& a, unsigned row_tiles, unsigned batch, hipStream_t s) {
+    constexpr size_t lds = 2 * ((L == 1) ? 64 : 128) * kW4TileK * 2;
+    const dim3 grid(ceil_div(a.Nt, ((L == 1) ? 4 : 2) * MM_CT), row_tiles, batch);
+    if (a.gmul) w4_mma_kernel<4, true, GR, SWI, L><<<grid, 256, lds, s>>>(a);
+    else w4_mma_kernel<4, false, GR, SWI, L><<<grid, 256, lds, s>>>(a);
+}
+
+int device_cus() {
+    static const int cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            return 0;
+        return n;
+    }();
+    return cus;
+}
+
+// The tile kernel over `rows` rows (dense / batched), or over a ragged group
+// table of `groups` groups holding `rows` rows in all: each group adds at
+// most one partial row tile.  Layout 1 (64 x 256) unless its grid holds
+// fewer than two workgroups per CU (two fit, by LDS and registers) and K is
+// long: then layout 2 splits K for twice the workgroups.  Measured on MI355X:
+// 64 x 256 beat 128 x 128 on every shape tried (M=4096 K=8192 N=28672 2104
+// vs 2215 us; config 4's grouped GEMM 196 vs 229 us).  LHQ_W4_MMA_L (0|1|2)
+// forces a layout.
 template <bool GR, bool SWI = false>
-void launch_mma(const W4Args& a, dim3 grid, hipStream_t s) {
-    constexpr size_t lds = 2 * MM_A_BYTES;
-    if (a.gmul) w4_mma_kernel<4, true, GR, SWI><<<grid, 256, lds, s>>>(a);
-    else w4_mma_kernel<4, false, GR, SWI><<<grid, 256, lds, s>>>(a);
+int launch_mma(const W4Args& a, int64_t rows, int groups, int batch, hipStream_t s, const char* who) {
+    static const int env_l = [] {
+        const char* v = std::getenv("LHQ_W4_MMA_L");
+        return v ? std::atoi(v) : -1;
+    }();
+    int l = 1;
+    const int64_t wgs1 = static_cast<int64_t>(ceil_div(a.Nt, 4 * MM_CT)) * (ceil_div64(rows, 64) + groups) * batch;
+    if (wgs1 < 2 * static_cast<int64_t>(device_cus()) && a.Kt >= 16) l = 2;
+    if (env_l >= 0 && env_l <= 2) l = env_l;
+    const int64_t tiles = ceil_div64(rows, l == 0 ? 128 : 64) + groups;
+    LHQ_SUPPORTED(tiles <= 65535, "%s: %lld row tiles exceed the grid limit", who, static_cast<long long>(tiles));
+    const unsigned t = static_cast<unsigned>(tiles), b = static_cast<unsigned>(batch);
+    if (l == 0) launch_mma_l<GR, SWI, 0>(a, t, b, s);
+    else if (l == 1) launch_mma_l<GR, SWI, 1>(a, t, b, s);
+    else launch_mma_l<GR, SWI, 2>(a, t, b, s);
+    return check_launch(who);
 }
 
 // The prefill tile kernel serves the bf16 entry points when there are rows
@@ -1316,13 +1401,7 @@ int launch_w4(W4Args a, int batch, hipStream_t s, int mblocks = -1) {
     // workgroups fit one per CU (measured: M=4, K=11008, N=4096 12.1 -> 9.1 us
     // against the generic kernel; at 128 KiB, or with more workgroups than
     // CUs, the generic kernel stays faster).
-    static const int cus = [] {
-        int dev = 0, n = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-            return 0;
-        return n;
-    }();
+    const int cus = device_cus();
     const int64_t dec_wgs = static_cast<int64_t>(ceil_div(a.Nt, a.Nt >= 1024 ? 2 : 1)) * batch;
     const bool dec_fits = dec_lds <= static_cast<size_t>(kDecodeMaxLds) ||
                           (dec_lds <= static_cast<size_t>(kDecodeBigLds) && dec_wgs <= cus);
@@ -1411,13 +1490,9 @@ int grouped_w4(const char* who, const uint16_t* A, const int32_t* offsets, const
     a.zss = zeros;
     a.num_groups = num_groups;
     a.row_capacity = row_capacity;
-    if (mma_applies(a, row_capacity, static_cast<double>(row_capacity) / num_groups)) {
-        // sum_e ceil(rows_e / 128) <= ceil(row_capacity / 128) + num_groups
-        const int64_t tiles = ceil_div64(row_capacity, MM_BM) + num_groups;
-        LHQ_SUPPORTED(tiles <= 65535, "%s: %lld row tiles exceed the grid limit", who, static_cast<long long>(tiles));
-        launch_mma<true, SWI>(a, dim3(ceil_div(a.Nt, 2 * MM_CT), static_cast<unsigned>(tiles), 1), as_stream(stream));
-        return check_launch(who);
-    }
+    if (mma_applies(a, row_capacity, static_cast<double>(row_capacity) / num_groups))
+        // sum_e ceil(rows_e / BM) <= ceil(row_capacity / BM) + num_groups
+        return launch_mma<true, SWI>(a, row_capacity, num_groups, 1, as_stream(stream), who);
     // sum_e ceil(rows_e / 16) <= ceil(row_capacity / 16) + num_groups
     const int64_t mblocks = ceil_div64(row_capacity, 16) + num_groups;
     LHQ_SUPPORTED(mblocks <= 65535, "%s: %lld row blocks exceed the grid limit", who, static_cast<long long>(mblocks));
@@ -1447,11 +1522,7 @@ int lhq_gemm_w4a16_bf16(const uint16_t* A, const uint8_t* qweight, const uint16_
     LHQ_REQUIRE(qweight && scales && zeros && C && (A || M == 0), "gemm_w4a16_bf16: null pointer");
     if (M == 0) return LHQ_OK;
     W4Args a = make_args(A, qweight, scales, zeros, C, M, N, K, G, 1.0f, 0.0f);
-    if (mma_applies(a, M, M)) {
-        LHQ_SUPPORTED(ceil_div(M, MM_BM) <= 65535, "gemm_w4a16_bf16: M=%d exceeds the grid limit", M);
-        launch_mma<false>(a, dim3(ceil_div(a.Nt, 2 * MM_CT), ceil_div(M, MM_BM), 1), as_stream(stream));
-        return check_launch("w4a16 prefill");
-    }
+    if (mma_applies(a, M, M)) return launch_mma<false>(a, M, 0, 1, as_stream(stream), "w4a16 prefill");
     return launch_w4<false, true, false>(a, 1, as_stream(stream));
 }
 
@@ -1468,11 +1539,7 @@ int lhq_gemm_w4a16_bf16_batched(const uint16_t* A, const uint8_t* qweight, const
     a.qw_bs = lhq_w4_qweight_bytes(K, N);
     a.s_bs = static_cast<int64_t>(a.Nt) * a.NG * 16;
     a.z_bs = static_cast<int64_t>(a.Nt) * a.NG8 * 16;
-    if (mma_applies(a, M, M)) {
-        LHQ_SUPPORTED(ceil_div(M, MM_BM) <= 65535, "gemm_w4a16_bf16_batched: M=%d exceeds the grid limit", M);
-        launch_mma<false>(a, dim3(ceil_div(a.Nt, 2 * MM_CT), ceil_div(M, MM_BM), batch), as_stream(stream));
-        return check_launch("w4a16 prefill batched");
-    }
+    if (mma_applies(a, M, M)) return launch_mma<false>(a, M, 0, batch, as_stream(stream), "w4a16 prefill batched");
     return launch_w4<false, true, false>(a, batch, as_stream(stream));
 }
 
