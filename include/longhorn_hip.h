@@ -122,6 +122,21 @@ int lhq_w4_interleave_gate_up(const uint8_t* gate_qweight, const uint16_t* gate_
                               const uint16_t* up_scales, const uint32_t* up_zeros, int K, int I,
                               int group_size, uint8_t* qweight, uint16_t* scales_out,
                               uint32_t* zeros_out, void* stream);
+/* Prepacked W4 weights on disk (no reference counterpart: the reference keeps
+ * weights in caller memory and plans safetensors loaders, PLAN.md:326-333).
+ * The file is safetensors: tensors "qweight" U8, "scales" F16 (asymmetric,
+ * fp16_scales = 1, with "zeros" U32) or F32 (symmetric), in the layout above;
+ * metadata format = "lhq-w4-prepacked", version = "1", layout =
+ * "w4-tile16x128-v1", K, N, group_size and fnv1a64 (16 hex digits over the
+ * data section).  Loading checks every field, size and the checksum before
+ * any copy; save and load are synchronous on `stream` and use host memory
+ * only.  lhq_w4_file_info reads and checks a file without touching a GPU. */
+int lhq_w4_save(const char* path, const uint8_t* qweight, const void* scales,
+                const uint32_t* zeros, int K, int N, int group_size, int fp16_scales,
+                void* stream);
+int lhq_w4_file_info(const char* path, int* K, int* N, int* group_size, int* fp16_scales);
+int lhq_w4_load(const char* path, uint8_t* qweight, void* scales, uint32_t* zeros, int K, int N,
+                int group_size, int fp16_scales, void* stream);
 /* 8-bit B operand (int8 or fp8 e4m3) [K, N] -> k-contiguous Bt [Np][Kp]
  * with Np = N rounded up to 256 and Kp = K rounded up to 128, zero padded. */
 int64_t lhq_b8_prepacked_bytes(int K, int N);

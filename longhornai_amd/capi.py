@@ -57,6 +57,9 @@ SIGNATURES = {
     "lhq_gemm_w4a16_bf16_batched": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p],
     "lhq_gemm_w4a16_bf16_grouped": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p],
     "lhq_gemm_w4a16_bf16_grouped_swiglu": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p],
+    "lhq_w4_save": [C.c_char_p, _p, _p, _p, _i, _i, _i, _i, _p],
+    "lhq_w4_file_info": [C.c_char_p, _p, _p, _p, _p],
+    "lhq_w4_load": [C.c_char_p, _p, _p, _p, _i, _i, _i, _i, _p],
     "lhq_w4_interleave_gate_up": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _p, _p, _p, _p],
     "lhq_moe_dispatch_f32": [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
     "lhq_moe_dispatch_bf16": [_p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
