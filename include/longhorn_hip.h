@@ -213,6 +213,17 @@ int lhq_moe_combine_f32(const float* expert_outputs, const int32_t* slot_pos,
 int lhq_moe_combine_bf16(const uint16_t* expert_outputs, const int32_t* slot_pos,
                          const float* gate_weights, uint16_t* output, int n_tokens,
                          int hidden_dim, int top_k, void* stream);
+/* moe_combine followed by q8_quantize_per_row (quant.cpp:52-63) on its fp32
+ * sums, fused: the combine's epilogue quantizes each token's row to int8
+ * with one fp32 scale per token -- the per-token activations a W8A8 layer
+ * reads next (no reference counterpart as one call; bit-exact with the two
+ * reference functions composed).  hidden_dim <= 16384. */
+int lhq_moe_combine_q8_f32(const float* expert_outputs, const int32_t* slot_pos,
+                           const float* gate_weights, int8_t* q_out, float* scales_out,
+                           int n_tokens, int hidden_dim, int top_k, void* stream);
+int lhq_moe_combine_q8_bf16(const uint16_t* expert_outputs, const int32_t* slot_pos,
+                            const float* gate_weights, int8_t* q_out, float* scales_out,
+                            int n_tokens, int hidden_dim, int top_k, void* stream);
 /* moe_expert_mlp (moe.hpp:80-94, moe.cpp:150-196) with W4A16 experts:
  * lhq_gemm_w4a16_bf16_grouped_swiglu into act [row_capacity, I] (caller's
  * buffer), then lhq_gemm_w4a16_bf16_grouped with the down weights into

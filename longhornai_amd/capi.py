@@ -66,6 +66,8 @@ SIGNATURES = {
     "lhq_moe_slot_positions": [_p, _p, _p, _i, _i, _p],
     "lhq_moe_combine_f32": [_p, _p, _p, _p, _i, _i, _i, _p],
     "lhq_moe_combine_bf16": [_p, _p, _p, _p, _i, _i, _i, _p],
+    "lhq_moe_combine_q8_f32": [_p, _p, _p, _p, _p, _i, _i, _i, _p],
+    "lhq_moe_combine_q8_bf16": [_p, _p, _p, _p, _p, _i, _i, _i, _p],
     "lhq_moe_expert_mlp_w4a16_bf16": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p],
     "lhq_gemm_w8a8": [_p, _p, _p, _p, _p, _i, _i, _i, _f, _f, _p],
     "lhq_gemm_w8a8_bf16": [_p, _p, _p, _p, _p, _i, _i, _i, _p],

@@ -155,21 +155,29 @@ __global__ void moe_invert_kernel(const int32_t* __restrict__ token_idx, const i
 // in position order, of gate[t, k] * y[pos] -- the reference zeroes the
 // output and adds one product per slot in slot order (expert-major), so a
 // token's terms arrive in ascending position.  fp32, product and sum each
-// rounded (contraction off), starting from +0.  Workgroup (t, y):
-// thread 0 sorts the token's positions into LDS, then each thread sums four
-// consecutive elements.  BF16: y and output bf16 (y widened exactly, the sum
-// rounded once); else fp32.
-template <bool BF16>
+// rounded (contraction off), starting from +0.  Workgroup (t, y): thread 0
+// sorts the token's positions into LDS, then each thread sums four
+// consecutive elements per 1024-element chunk.  BF16: y bf16 (widened
+// exactly); the output is bf16 (the sum rounded once) or, without Q8, the
+// type of y.
+// Q8 (one workgroup per token, grid.y = 1): the output row is quantized to
+// int8 per token in the epilogue -- q8_quantize_per_row (quant.cpp:52-63)
+// applied to the fp32 sums, which stay in LDS: max-abs (a NaN never wins,
+// quant.cpp:21-28), scale = m / 127 (1 when m == 0), inv = 1 / scale,
+// q = saturate-then-round-to-nearest-even(x * inv).
+template <bool BF16, bool Q8>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict__ y,
                                                           const int32_t* __restrict__ slot_pos,
                                                           const float* __restrict__ gates, void* __restrict__ out,
-                                                          int H, int topk) {
+                                                          float* __restrict__ scales, int H, int topk) {
     // hipcc contracts a * b + c into one fused multiply-add by default; the
     // reference rounds the product and the sum separately
 #pragma clang fp contract(off)
     __shared__ int32_t sp[kMaxTopK];
     __shared__ float sg[kMaxTopK];
     __shared__ int ns;
+    __shared__ float wmax[4];
+    extern __shared__ float qrow[];  // Q8: the token's fp32 row
     const int64_t t = blockIdx.x;
     if (threadIdx.x == 0) {
         int n = 0;
@@ -190,56 +198,92 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const void* __restrict
     }
     __syncthreads();
     const int n = ns;
-    const int i0 = (static_cast<int>(blockIdx.y) * 256 + static_cast<int>(threadIdx.x)) * 4;
-    if (i0 >= H) return;
-    const int cnt = min(4, H - i0);
-    const bool vec = (cnt == 4) && (H % 4 == 0);
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int j = 0; j < n; ++j) {
-        const int64_t base = static_cast<int64_t>(sp[j]) * H + i0;
-        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        if constexpr (BF16) {
-            const uint16_t* yp = static_cast<const uint16_t*>(y) + base;
-            if (vec) {
-                const u32x2_t w = *reinterpret_cast<const u32x2_t*>(yp);
-                v[0] = __uint_as_float(w[0] << 16);
-                v[1] = __uint_as_float(w[0] & 0xffff0000u);
-                v[2] = __uint_as_float(w[1] << 16);
-                v[3] = __uint_as_float(w[1] & 0xffff0000u);
+    const bool vec = (H % 4 == 0);  // then every chunk holds 4 elements
+    const int step = static_cast<int>(gridDim.y) * 1024;
+    float m = 0.0f;
+    for (int i0 = (static_cast<int>(blockIdx.y) * 256 + static_cast<int>(threadIdx.x)) * 4; i0 < H; i0 += step) {
+        const int cnt = min(4, H - i0);
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < n; ++j) {
+            const int64_t base = static_cast<int64_t>(sp[j]) * H + i0;
+            float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if constexpr (BF16) {
+                const uint16_t* yp = static_cast<const uint16_t*>(y) + base;
+                if (vec) {
+                    const u32x2_t w = *reinterpret_cast<const u32x2_t*>(yp);
+                    v[0] = __uint_as_float(w[0] << 16);
+                    v[1] = __uint_as_float(w[0] & 0xffff0000u);
+                    v[2] = __uint_as_float(w[1] << 16);
+                    v[3] = __uint_as_float(w[1] & 0xffff0000u);
+                } else {
+                    for (int q = 0; q < cnt; ++q) v[q] = bf16_to_f32(yp[q]);
+                }
             } else {
-                for (int q = 0; q < cnt; ++q) v[q] = bf16_to_f32(yp[q]);
+                const float* yp = static_cast<const float*>(y) + base;
+                if (vec) {
+                    const f32x4_t w = *reinterpret_cast<const f32x4_t*>(yp);
+                    v[0] = w[0];
+                    v[1] = w[1];
+                    v[2] = w[2];
+                    v[3] = w[3];
+                } else {
+                    for (int q = 0; q < cnt; ++q) v[q] = yp[q];
+                }
             }
-        } else {
-            const float* yp = static_cast<const float*>(y) + base;
-            if (vec) {
-                const f32x4_t w = *reinterpret_cast<const f32x4_t*>(yp);
-                v[0] = w[0];
-                v[1] = w[1];
-                v[2] = w[2];
-                v[3] = w[3];
-            } else {
-                for (int q = 0; q < cnt; ++q) v[q] = yp[q];
-            }
-        }
-        const float g = sg[j];
+            const float g = sg[j];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) acc[q] = acc[q] + g * v[q];
+            for (int q = 0; q < 4; ++q) acc[q] = acc[q] + g * v[q];
+        }
+        const int64_t ob = t * H + i0;
+        if constexpr (Q8) {
+            for (int q = 0; q < cnt; ++q) {
+                qrow[i0 + q] = acc[q];
+                const float a = fabsf(acc[q]);
+                m = (a > m) ? a : m;
+            }
+        } else if constexpr (BF16) {
+            uint16_t* op = static_cast<uint16_t*>(out) + ob;
+            if (vec) {
+                *reinterpret_cast<u32x2_t*>(op) = u32x2_t{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
+            } else {
+                for (int q = 0; q < cnt; ++q) op[q] = f32_to_bf16(acc[q]);
+            }
+        } else {
+            float* op = static_cast<float*>(out) + ob;
+            if (vec) {
+                *reinterpret_cast<f32x4_t*>(op) = f32x4_t{acc[0], acc[1], acc[2], acc[3]};
+            } else {
+                for (int q = 0; q < cnt; ++q) op[q] = acc[q];
+            }
+        }
     }
-    const int64_t ob = t * H + i0;
-    if constexpr (BF16) {
-        uint16_t* op = static_cast<uint16_t*>(out) + ob;
-        if (vec) {
-            *reinterpret_cast<u32x2_t*>(op) = u32x2_t{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
-        } else {
-            for (int q = 0; q < cnt; ++q) op[q] = f32_to_bf16(acc[q]);
+    if constexpr (Q8) {
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            const float o = __shfl_xor(m, off, 64);
+            m = (o > m) ? o : m;
         }
-    } else {
-        float* op = static_cast<float*>(out) + ob;
-        if (vec) {
-            *reinterpret_cast<f32x4_t*>(op) = f32x4_t{acc[0], acc[1], acc[2], acc[3]};
-        } else {
-            for (int q = 0; q < cnt; ++q) op[q] = acc[q];
+        if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = m;
+        __syncthreads();
+        m = wmax[0];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) m = (wmax[w] > m) ? wmax[w] : m;
+        const float scale = (m > 0.0f) ? m / 127.0f : 1.0f;
+        const float inv = 1.0f / scale;
+        int8_t* op = static_cast<int8_t*>(out) + t * H;
+        // each thread quantizes the elements it summed (its own LDS entries)
+        for (int i0 = static_cast<int>(threadIdx.x) * 4; i0 < H; i0 += 1024) {
+            if (vec) {
+                uint32_t w = 0;
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    w |= static_cast<uint32_t>(static_cast<uint8_t>(sat_rint(qrow[i0 + q] * inv, 127))) << (8 * q);
+                *reinterpret_cast<uint32_t*>(op + i0) = w;
+            } else {
+                for (int q = 0; q < min(4, H - i0); ++q) op[i0 + q] = static_cast<int8_t>(sat_rint(qrow[i0 + q] * inv, 127));
+            }
         }
+        if (threadIdx.x == 0) scales[t] = scale;
     }
 }
 
@@ -279,17 +323,23 @@ int dispatch(const char* who, const void* hidden, int elem, const int32_t* ids, 
     return check_launch(who);
 }
 
-template <bool BF16>
-int combine(const char* who, const void* y, const int32_t* slot_pos, const float* gates, void* out, int T, int H,
-            int topk, void* stream) {
+constexpr int kQ8MaxH = 16384;  // Q8 keeps the row in LDS (64 KiB)
+
+template <bool BF16, bool Q8>
+int combine(const char* who, const void* y, const int32_t* slot_pos, const float* gates, void* out, float* scales,
+            int T, int H, int topk, void* stream) {
     LHQ_REQUIRE(T >= 0 && H > 0 && topk > 0, "%s: bad dims T=%d H=%d top_k=%d", who, T, H, topk);
     LHQ_SUPPORTED(topk <= kMaxTopK, "%s: top_k=%d exceeds %d", who, topk, kMaxTopK);
+    LHQ_SUPPORTED(!Q8 || H <= kQ8MaxH, "%s: hidden_dim=%d exceeds %d", who, H, kQ8MaxH);
     if (T == 0) return LHQ_OK;
-    LHQ_REQUIRE(y && slot_pos && gates && out, "%s: null pointer", who);
-    LHQ_REQUIRE(H % 4 != 0 || (aligned(y, 8) && aligned(out, 8) && (BF16 || (aligned(y, 16) && aligned(out, 16)))),
+    LHQ_REQUIRE(y && slot_pos && gates && out && (scales || !Q8), "%s: null pointer", who);
+    // vector loads of y (8 bytes bf16, 16 bytes fp32) and stores of the output
+    const unsigned ya = BF16 ? 8 : 16, oa = Q8 ? 4 : ya;
+    LHQ_REQUIRE(H % 4 != 0 || (aligned(y, ya) && aligned(out, oa)),
                 "%s: y and output must be aligned to their 4-element vectors", who);
-    const dim3 grid(static_cast<unsigned>(T), static_cast<unsigned>(ceil_div(H, 1024)));
-    moe_combine_kernel<BF16><<<grid, 256, 0, as_stream(stream)>>>(y, slot_pos, gates, out, H, topk);
+    const dim3 grid(static_cast<unsigned>(T), Q8 ? 1u : static_cast<unsigned>(ceil_div(H, 1024)));
+    const size_t lds = Q8 ? static_cast<size_t>(H) * sizeof(float) : 0;
+    moe_combine_kernel<BF16, Q8><<<grid, 256, lds, as_stream(stream)>>>(y, slot_pos, gates, out, scales, H, topk);
     return check_launch(who);
 }
 
@@ -330,14 +380,26 @@ int lhq_moe_slot_positions(const int32_t* token_idx, const int32_t* slot_idx, in
 
 int lhq_moe_combine_f32(const float* expert_outputs, const int32_t* slot_pos, const float* gate_weights,
                         float* output, int n_tokens, int hidden_dim, int top_k, void* stream) {
-    return combine<false>("moe_combine_f32", expert_outputs, slot_pos, gate_weights, output, n_tokens, hidden_dim,
-                          top_k, stream);
+    return combine<false, false>("moe_combine_f32", expert_outputs, slot_pos, gate_weights, output, nullptr,
+                                 n_tokens, hidden_dim, top_k, stream);
 }
 
 int lhq_moe_combine_bf16(const uint16_t* expert_outputs, const int32_t* slot_pos, const float* gate_weights,
                          uint16_t* output, int n_tokens, int hidden_dim, int top_k, void* stream) {
-    return combine<true>("moe_combine_bf16", expert_outputs, slot_pos, gate_weights, output, n_tokens, hidden_dim,
-                         top_k, stream);
+    return combine<true, false>("moe_combine_bf16", expert_outputs, slot_pos, gate_weights, output, nullptr,
+                                n_tokens, hidden_dim, top_k, stream);
+}
+
+int lhq_moe_combine_q8_f32(const float* expert_outputs, const int32_t* slot_pos, const float* gate_weights,
+                           int8_t* q_out, float* scales_out, int n_tokens, int hidden_dim, int top_k, void* stream) {
+    return combine<false, true>("moe_combine_q8_f32", expert_outputs, slot_pos, gate_weights, q_out, scales_out,
+                                n_tokens, hidden_dim, top_k, stream);
+}
+
+int lhq_moe_combine_q8_bf16(const uint16_t* expert_outputs, const int32_t* slot_pos, const float* gate_weights,
+                            int8_t* q_out, float* scales_out, int n_tokens, int hidden_dim, int top_k, void* stream) {
+    return combine<true, true>("moe_combine_q8_bf16", expert_outputs, slot_pos, gate_weights, q_out, scales_out,
+                               n_tokens, hidden_dim, top_k, stream);
 }
 
 int lhq_moe_expert_mlp_w4a16_bf16(const uint16_t* expert_inputs, const int32_t* expert_offsets,

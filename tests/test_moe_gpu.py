@@ -143,6 +143,40 @@ def test_combine_bitexact(oracle, ops, T, E, K, H, kind, dtype):
         assert np.array_equal(ops.host(out, np.uint16), want)
 
 
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("T,E,K,H,kind", [
+    (512, 8, 2, 4096, "uniform"),   # config 4
+    (41, 16, 4, 7, "uniform"),      # H % 4 != 0
+    (300, 16, 3, 16384, "dropped"),  # the longest row the fused kernel holds
+    (64, 8, 2, 1000, "repeat"),
+])
+def test_combine_q8_bitexact(oracle, ops, T, E, K, H, kind, dtype):
+    """combine + per-token int8 quantization in one kernel == q8_quantize_per_row
+    (quant.cpp:52-63) of the fp32 combine; token 0 sums to an all-zero row
+    (scale 1) and one expert output holds a NaN (it never wins the max and
+    quantizes to 0)."""
+    ids = _routing(T, E, K, 6000 + T, kind)
+    _, tok, slot, pos, _ = oracle.moe_dispatch(np.zeros((T, 1), np.float32), ids, E)
+    gates = D.uniform((T, K), 0.0, 1.0, 6001)
+    gates[0] = 0.0
+    y = D.normal((T * K, H), 1.0, 6002)
+    y[T * K // 2, H // 2] = np.nan
+    if dtype == "bf16":
+        y = D.to_bf16_bits(oracle, y)
+        yf = D.bf16_bits_to_f32(y)
+        name = "lhq_moe_combine_q8_bf16"
+    else:
+        yf = y
+        name = "lhq_moe_combine_q8_f32"
+    wq, ws = oracle.q8_quantize_per_row(oracle.moe_combine_f32(yf, tok, slot, gates))
+    q = ops.zeros((T, H), np.int8)
+    sc = ops.zeros((T,), np.float32)
+    ops.run(name, y, pos, gates, q, sc, T, H, K)
+    assert np.array_equal(ops.host(q), wq)
+    assert np.array_equal(ops.host(sc).view(np.uint32), ws.view(np.uint32))
+    assert ws[0] == 1.0 and not wq[0].any()
+
+
 def test_combine_order_is_slot_order(oracle, ops):
     """2^24 + (-2^24) + 1 in expert-major slot order is 1 (top-k order would give 0)."""
     ids = np.array([[2, 0, 1]], np.int32)
