@@ -44,6 +44,7 @@ if ROOT not in sys.path:
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, published
 INT8_PEAK_TOPS = 5000.0     # MI355X dense int8 MFMA, published
 BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA, published
+FP8_PEAK_TFLOPS = 5000.0    # MI355X dense fp8 MFMA, published
 INFINITY_CACHE_BYTES = 256 << 20
 
 
@@ -227,6 +228,45 @@ def bench_moe(ops, steps, warmup, seed=0, T=512, E=8, topk=2, K=4096, N=14336, G
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     return res
+
+
+def bench_fp8(ops, M, K, N, steps, warmup, seed=0):
+    """gemm_fp8_e4m3 (gemm_quant.cpp:87-104): e4m3 A [M,K] and B [K,N] quantized
+    per tensor on the device from N(0,1) / N(0,0.02), fp32 C = sA*sB*acc."""
+    import numpy as np
+    import torch
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    L = ops.lib()
+    W = torch.randn((K, N), generator=gen, device="cuda") * 0.02
+    B8 = ops.empty((K, N), np.uint8)
+    sB = ops.empty((1,), np.float32)
+    L.call("lhq_fp8_quantize_per_tensor", W.data_ptr(), B8.data_ptr(), sB.data_ptr(), K * N, ops.stream())
+    del W
+    Bt = ops.prepack_b8(B8, K, N)
+    del B8
+    X = torch.randn((M, K), generator=gen, device="cuda")
+    A8 = ops.empty((M, K), np.uint8)
+    sA = ops.empty((1,), np.float32)
+    L.call("lhq_fp8_quantize_per_tensor", X.data_ptr(), A8.data_ptr(), sA.data_ptr(), M * K, ops.stream())
+    del X
+    C = ops.empty((M, N), np.float32)
+    fn = L.cdll.lhq_gemm_fp8_e4m3
+
+    def launch(_i):
+        st = fn(A8.data_ptr(), Bt.data_ptr(), sA.data_ptr(), sB.data_ptr(), C.data_ptr(), M, N, K, 1.0, 0.0,
+                ops.stream())
+        if st:
+            raise RuntimeError(f"lhq_gemm_fp8_e4m3: {L.last_error()}")
+
+    ms, _ = GraphTimer(launch, 1, chunk=16).time(steps, warmup)
+    us = ms * 1e3 / steps
+    tf = 2 * M * K * N / (us * 1e-6) / 1e12
+    del Bt, A8, C
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return {"leg": "fp8_e4m3_gemm", "M": M, "K": K, "N": N, "us_per_call": round(us, 2), "tflops": round(tf, 1),
+            "peak": FP8_PEAK_TFLOPS, "mfma_frac": round(tf / FP8_PEAK_TFLOPS, 4)}
 
 
 def bench_moe_layer(ops, steps, warmup, seed=0, T=512, E=8, topk=2, H=4096, I=14336, G=128):
@@ -524,7 +564,7 @@ def main() -> int:
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a 1 GiB device copy (PMC calibration kernel)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the W4A16 prefill and MoE legs")
-    ap.add_argument("--only", choices=["w4a16", "w8a8", "prefill", "moe"], default=None,
+    ap.add_argument("--only", choices=["w4a16", "w8a8", "prefill", "moe", "fp8"], default=None,
                     help="run one leg only (profiling); prints that leg's summary, not the bench line")
     args = ap.parse_args()
 
@@ -552,6 +592,13 @@ def main() -> int:
             r = bench_w8a8(ops, m, 4096, 14336, args.w8a8_steps, max(10, args.w8a8_steps // 10))
             print(json.dumps({"leg": "w8a8_prefill", **r}), flush=True)
         return 0
+    if args.only == "fp8":
+        for m in (4096, 2048):
+            r = bench_fp8(ops, m, 4096, 14336, args.w8a8_steps, max(10, args.w8a8_steps // 10))
+            log(f"fp8 e4m3 GEMM M={m} K=4096 N=14336: {r['us_per_call']:.1f} us  {r['tflops']:.0f} TFLOPS "
+                f"({100 * r['mfma_frac']:.1f}% of fp8 peak)")
+            print(json.dumps(r), flush=True)
+        return 0
     if args.only == "moe":
         print(json.dumps(moe_layer_leg(ops)), flush=True)
         return 0
@@ -576,6 +623,13 @@ def main() -> int:
             log(f"  {r['us_per_call']:.1f} us/call  {r['tops']:.0f} TOPS ({100 * r['mfma_frac']:.1f}% of int8 peak); "
                 f"act quant {r['act_quant_us']:.1f} us ({r['act_quant_gbs']:.0f} GB/s)")
             w8.append(r)
+
+    fp8 = []
+    if not args.no_w8a8:
+        log(f"fp8 e4m3 GEMM M=4096 K=4096 N=14336: {args.w8a8_steps} steps")
+        r = bench_fp8(ops, 4096, 4096, 14336, args.w8a8_steps, max(10, args.w8a8_steps // 10))
+        log(f"  {r['us_per_call']:.1f} us/call  {r['tflops']:.0f} TFLOPS ({100 * r['mfma_frac']:.1f}% of fp8 peak)")
+        fp8.append(r)
 
     pre = [] if args.no_prefill else prefill_legs(ops)
 
@@ -619,6 +673,7 @@ def main() -> int:
              "frac": round(r["mfma_frac"], 4), "act_quant_us": round(r["act_quant_us"], 2)}
             for r in w8],
         "w8a8_cpu_baseline": cpu_w8,
+        "fp8_gemm": fp8,
         "w4a16_prefill": pre,
         "cpu_baseline": cpu,
     }

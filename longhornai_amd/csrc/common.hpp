@@ -45,6 +45,16 @@ __device__ __forceinline__ i32x4_t mfma_i8_16x16x64(u32x4_t a, u32x4_t b, i32x4_
     return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4_t, a),
                                                  __builtin_bit_cast(i32x4_t, b), c, 0, 0, 0);
 }
+// gfx950's 32x32x64 MFMA of the f8f6f4 family with both operands e4m3
+// (format 0) and unit block scales (E8M0 127 = 2^0): 32 bytes of k per lane,
+// given here as two 16-byte halves.
+typedef __attribute__((ext_vector_type(8))) int i32x8_t;
+__device__ __forceinline__ f32x16_t mfma_fp8_32x32x64(u32x4_t a_lo, u32x4_t a_hi, u32x4_t b_lo, u32x4_t b_hi,
+                                                      f32x16_t c) {
+    const i32x8_t a = __builtin_bit_cast(i32x8_t, __builtin_shufflevector(a_lo, a_hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    const i32x8_t b = __builtin_bit_cast(i32x8_t, __builtin_shufflevector(b_lo, b_hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+}
 __device__ __forceinline__ f32x4_t mfma_fp8_16x16x32(u32x2_t a, u32x2_t b, f32x4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_fp8_fp8(__builtin_bit_cast(long, a),
                                                       __builtin_bit_cast(long, b), c, 0, 0, 0);

@@ -731,6 +731,115 @@ __global__ __launch_bounds__(NTHREADS) void gemm8_dma_kernel(Gemm8Args p) {
 }
 
 // ---------------------------------------------------------------------------
+// FP8 (e4m3) kernel on the LDS-DMA pipeline: gemm_fp8_e4m3
+// (gemm_quant.cpp:87-104) with fp32 accumulation on gfx950's
+// v_mfma_scale_f32_32x32x64_f8f6f4.  Same tile, waves, buffers, swizzle and
+// DMA schedule as the int8 tile above; a stage's 64 k bytes are ONE MFMA per
+// 32x32 block instead of two: a lane's two 16-byte fragments of the stage
+// (k chunks (lane >> 5) and 2 + (lane >> 5)) form its 32-byte operand.  The
+// instruction assigns k to lanes differently, but A and B are read with the
+// same lane -> k mapping, so the 64 products of a block are the same ones.
+// The whole next stage is read into the fragment registers in place, each
+// fragment as soon as the current stage's last MFMA on it has issued (A
+// block i after block row i, B block j in the last row), so one register set
+// serves; the rendezvous opens each stage (the next stage has landed, every
+// wave has read the current buffer, which then takes its DMA STAGES stages
+// ahead).  Requires K % 128 == 0: no padded k reaches the MFMA (a padded A
+// byte could be the NaN code, and NaN times the zero padding of B is NaN).
+// Rows past M read row M-1; those rows are never stored.
+// ---------------------------------------------------------------------------
+template <int STAGES>
+__device__ __forceinline__ void dma_tile_fp8(const Gemm8Args& p, uint8_t* ds_lds, int m0, int n0,
+                                             f32x16_t (&acc)[4][4]) {
+    constexpr int DPS = 8;  // DMAs per wave per stage: 4 of A, 4 of B
+    static_assert(STAGES >= 3 && DPS * (STAGES - 2) <= 63, "vmcnt range");
+    auto stage_buf = [&](int u) { return ds_lds + u * 2 * DS_OP_BYTES; };
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    uint32_t a_row[4], b_src[4];
+    int kca[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = (4 * wave + i) * 64 + lane;
+        const int r = c >> 2;
+        kca[i] = ((c & 3) ^ ((r >> 2) & 3)) * 16;
+        a_row[i] = static_cast<uint32_t>(min(m0 + r, p.M - 1)) * static_cast<uint32_t>(p.K);
+        b_src[i] = static_cast<uint32_t>(n0 + r) * static_cast<uint32_t>(p.Kp) + static_cast<uint32_t>(kca[i]);
+    }
+    const int nk = p.Kp / DS_BK;
+    // DMA d of stage s (clamped to the last stage) into buf: A and B alternate
+    auto dma = [&](uint8_t* buf, int s, int d) {
+        const uint32_t k0 = static_cast<uint32_t>(min(s, nk - 1) * DS_BK);
+        const int i = d >> 1;
+        if (!(d & 1))
+            __builtin_amdgcn_global_load_lds(p.A + (a_row[i] + k0 + static_cast<uint32_t>(kca[i])),
+                                             (LHQ_LDS_AS void*)(buf + (4 * wave + i) * 1024), 16, 0, 0);
+        else
+            __builtin_amdgcn_global_load_lds(p.Bt + (b_src[i] + k0),
+                                             (LHQ_LDS_AS void*)(buf + DS_OP_BYTES + (4 * wave + i) * 1024), 16, 0,
+                                             0);
+    };
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x16_t{};
+
+    const int swz = ((lane & 31) >> 2) & 3;
+    const int a_base = (wm * 128 + (lane & 31)) * DS_BK;
+    const int b_base = DS_OP_BYTES + (wn * 128 + (lane & 31)) * DS_BK;
+    u32x4_t f[8][2];  // [A blocks 0..3, B blocks 0..3][k half]
+    auto read = [&](const uint8_t* buf, int x) {
+        const int base = x < 4 ? a_base + x * 32 * DS_BK : b_base + (x - 4) * 32 * DS_BK;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+            f[x][kk] = *reinterpret_cast<const u32x4_t*>(buf + base + (((2 * kk + (lane >> 5)) ^ swz) * 16));
+    };
+    auto rendezvous = [&]() {
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(DPS * (STAGES - 2)) : "memory");
+    };
+    // stage s from buffer cur; fragments already in f; next: the buffer of s + 1
+    auto step = [&](uint8_t* cur, const uint8_t* next, int s) {
+        rendezvous();
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            const int i = t >> 2, j = t & 3;
+            acc[i][j] = mfma_fp8_32x32x64(f[4 + j][0], f[4 + j][1], f[i][0], f[i][1], acc[i][j]);
+            if (t < 8) dma(cur, s + STAGES, t);
+            if (j == 3 && i < 3) read(next, i);  // A block i is done
+            if (i == 3) {
+                read(next, 4 + j);               // B block j is done
+                if (j == 3) read(next, 3);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+#pragma unroll
+    for (int u = 0; u < STAGES; ++u)
+#pragma unroll
+        for (int d = 0; d < DPS; ++d) dma(stage_buf(u), u, d);
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(DPS * (STAGES - 1)) : "memory");
+#pragma unroll
+    for (int x = 0; x < 8; ++x) read(stage_buf(0), x);
+    for (int s = 0; s < nk; s += STAGES) {
+#pragma unroll
+        for (int u = 0; u < STAGES; ++u)
+            if (u == 0 || s + u < nk) step(stage_buf(u), stage_buf((u + 1) % STAGES), s + u);
+    }
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    gemm8_epilogue<OP_FP8, EPI_F32>(p, acc, m0, n0, wm, wn, lane);
+}
+
+template <int STAGES>
+__global__ __launch_bounds__(NTHREADS) void gemm8_fp8_dma_kernel(Gemm8Args p) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t ds_lds[];
+    int tm, tn;
+    tile_of(blockIdx.x, p, tm, tn);
+    f32x16_t acc[4][4];
+    dma_tile_fp8<STAGES>(p, ds_lds, tm * BM, tn * BN, acc);
+}
+
+// ---------------------------------------------------------------------------
 // Skinny int8 kernel (W8A8 with M <= 16, e.g. the M = 1 GEMV of config 1).
 // The 256x256 tile kernel would spend 255/256 of its MFMA work and all but
 // N/256 of its workgroups on nothing there.  Here a 256-thread workgroup
@@ -848,6 +957,18 @@ int launch_dma(const Gemm8Args& p, int tiles, void* stream, const char* who) {
     return check_launch(who);
 }
 
+template <int STAGES>
+int launch_fp8_dma(const Gemm8Args& p, int tiles, void* stream, const char* who) {
+    constexpr size_t lds = static_cast<size_t>(STAGES) * 2 * DS_OP_BYTES;
+    static const hipError_t attr =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm8_fp8_dma_kernel<STAGES>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (attr != hipSuccess)
+        return set_error(LHQ_ERR_HIP, "%s: dynamic LDS attribute: %s", who, hipGetErrorString(attr));
+    gemm8_fp8_dma_kernel<STAGES><<<tiles, NTHREADS, lds, as_stream(stream)>>>(p);
+    return check_launch(who);
+}
+
 template <int OP, int EPI>
 int launch_gemm8(const uint8_t* A, const uint8_t* Bt, const float* As, const float* Bs, void* C, int M,
                  int N, int K, float alpha, float beta, void* stream, const char* who) {
@@ -871,10 +992,14 @@ int launch_gemm8(const uint8_t* A, const uint8_t* Bt, const float* As, const flo
     p.c_vec = (reinterpret_cast<uintptr_t>(C) % 16) == 0;
     const int tiles = p.tiles_m * p.tiles_n;
     // int8: the LDS-DMA pipeline (LHQ_GEMM8_DMA=0 selects the register-
-    // staged kernel); fp8 always uses the register-staged kernel, which zeroes
-    // the K padding of A before it reaches the MFMA
+    // staged kernel); fp8: the LDS-DMA pipeline when K % 128 == 0 (no K
+    // padding), else the register-staged kernel, which zeroes the K padding
+    // of A before it reaches the MFMA
     static const int use_dma = env_int("LHQ_GEMM8_DMA", 1);
     static const int use_skinny = env_int("LHQ_GEMM8_SKINNY", 1);
+    if constexpr (OP == OP_FP8) {
+        if (use_dma && K % BK == 0) return launch_fp8_dma<DS_STAGES>(p, tiles, stream, who);
+    }
     if constexpr (OP == OP_I8) {
         if (use_skinny && M <= 16) {
             gemm8_skinny_kernel<EPI><<<ceil_div(N, 16), 64 * SK_WAVES, 0, as_stream(stream)>>>(p);

@@ -144,6 +144,36 @@ def test_fp8_matches_oracle(oracle, ops, M, K, N, alpha, beta):
     assert rel_frobenius(ops.host(C), want) <= 1e-4
 
 
+@pytest.mark.parametrize("M,K,N", [
+    (300, 1024, 520),   # ragged M and N
+    (64, 128, 64),      # two k stages, fewer than the pipeline's buffers
+    (257, 384, 1000),   # six k stages: a partial last round of buffers
+    (512, 4096, 256),
+])
+@pytest.mark.parametrize("alpha,beta", [(1.0, 0.0), (0.5, 2.0)])
+def test_fp8_dma_path(oracle, ops, M, K, N, alpha, beta):
+    """K % 128 == 0 runs the LDS-DMA kernel on the 32x32x64 f8f6f4 MFMA.  A NaN
+    code in A (0x7f) and in B (0xff) make exactly their row / column NaN,
+    as in the reference's fp32 loop."""
+    A = D.normal((M, K), 1.0, 70 + M)
+    B = D.normal((K, N), 0.05, 71 + N)
+    a8, sa = oracle.fp8_quantize_per_tensor(A)
+    b8, sb = oracle.fp8_quantize_per_tensor(B)
+    a8[M // 3, K - 1] = 0x7F
+    b8[K // 2, N - 2] = 0xFF
+    C0 = D.uniform((M, N), -1, 1, 72)
+    want = oracle.gemm_fp8_e4m3(a8, b8, sa, sb, C0, alpha, beta)
+    Bt = ops.prepack_b8(ops.dev(b8), K, N)
+    C = ops.dev(C0)
+    ops.run("lhq_gemm_fp8_e4m3", a8, Bt, np.array([sa], np.float32), np.array([sb], np.float32),
+            C, M, N, K, alpha, beta)
+    got = ops.host(C)
+    nan = np.isnan(want)
+    assert nan[M // 3].all() and nan[:, N - 2].all() and nan.sum() == M + N - 1
+    assert np.array_equal(np.isnan(got), nan)
+    assert rel_frobenius(np.where(nan, 0, got), np.where(nan, 0, want)) <= 1e-4
+
+
 @pytest.mark.parametrize("M,K,N,batch", [(32, 64, 48, 1), (17, 100, 33, 1), (8, 16, 8, 3)])
 @pytest.mark.parametrize("ref", [False, True])
 def test_gemm_f32(oracle, ops, M, K, N, batch, ref):
