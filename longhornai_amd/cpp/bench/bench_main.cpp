@@ -250,6 +250,37 @@ void add_w8(lh_bench::BenchSuite& suite, int M, int K, int N, bool gemv_c1, int 
     suite.add(std::move(s));
 }
 
+// FP8 e4m3 GEMM (gemm_quant.cpp:87-104) at config 3's shape: random e4m3
+// codes below the NaN code, per-tensor scales, fp32 C.
+void add_fp8(lh_bench::BenchSuite& suite, int M, int K, int N) {
+    auto codes = [](size_t n, uint32_t seed) {
+        auto v = rand_bytes(n, seed);
+        for (auto& b : v)
+            if ((b & 0x7F) == 0x7F) b ^= 1;  // 0x7f / 0xff are NaN in e4m3
+        return v;
+    };
+    auto B = upload(codes(size_t(K) * N, 500).data(), size_t(K) * N);
+    auto Bt = std::make_shared<DevBuf>(lhq_b8_prepacked_bytes(K, N));
+    check(lhq_b8_prepack(B->as<uint8_t>(), K, N, Bt->as<uint8_t>(), nullptr), "lhq_b8_prepack");
+    if (hipDeviceSynchronize() != hipSuccess) die("fp8 prepack");  // B is freed on return
+    auto A = upload(codes(size_t(M) * K, 501).data(), size_t(M) * K);
+    const float sc[2] = {0.01f, 0.02f};
+    auto S = upload(sc, sizeof(sc));
+    auto C = std::make_shared<DevBuf>(size_t(M) * N * 4);
+    lh_bench::BenchSpec s;
+    s.name = "fp8/gemm_e4m3[" + std::to_string(M) + "x" + std::to_string(K) + "x" + std::to_string(N) + "]";
+    s.flops = 2.0 * M * K * N;
+    s.bytes = double(M) * K + double(K) * N + 4.0 * M * N;
+    s.peak_flops = lh_bench::kFp8PeakFlops;
+    s.iters = 50;
+    s.dev_fn = [=](hipStream_t st, int) {
+        check(lhq_gemm_fp8_e4m3(A->as<uint8_t>(), Bt->as<uint8_t>(), S->as<float>(), S->as<float>() + 1,
+                                C->as<float>(), M, N, K, 1.0f, 0.0f, st),
+              "lhq_gemm_fp8_e4m3");
+    };
+    suite.add(std::move(s));
+}
+
 void add_act_quant(lh_bench::BenchSuite& suite, int M, int K) {
     auto Ab = upload(rand_bf16(size_t(M) * K, 400).data(), size_t(M) * K * 2);
     auto Aq = std::make_shared<DevBuf>(size_t(M) * K);
@@ -365,6 +396,7 @@ int main(int argc, char** argv) {
             add_w8(suite, 2048, 4096, 14336, false, 50);
             add_w8(suite, 4096, 4096, 14336, false, 50);
         }
+        if (want("fp8/")) add_fp8(suite, 4096, 4096, 14336);
         if (want("quant/")) add_act_quant(suite, 4096, 4096);
     } else {
         add_host(suite);

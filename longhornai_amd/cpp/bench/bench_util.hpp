@@ -32,6 +32,7 @@ namespace lh_bench {
 constexpr double kHbmPeakBytes = 8.0e12;
 constexpr double kBf16PeakFlops = 2.5e15;
 constexpr double kInt8PeakOps = 5.0e15;
+constexpr double kFp8PeakFlops = 5.0e15;
 
 enum class Timing { Host, Hip };
 
