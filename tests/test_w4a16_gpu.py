@@ -105,6 +105,51 @@ def test_w4a16_bf16_matches_oracle(oracle, ops, M, K, N):
     assert (np.abs(got - want_b) <= ulp).mean() > 0.999
 
 
+CONFIG2 = [(m, k, n) for m in (1, 4, 16) for k, n in ((4096, 4096), (4096, 11008), (11008, 4096))]
+
+
+@pytest.mark.parametrize("M,K,N", CONFIG2)
+def test_w4a16_config2_all_shapes(oracle, ops, M, K, N):
+    """Benchmark config 2 (Llama-7B projections, M in {1, 4, 16}) at full size:
+    all nine shapes, every output against the oracle."""
+    got, want = _asym_case(oracle, ops, M, K, N, 128, seed=900 + M + K)
+    assert rel_frobenius(got, want) <= TOL_BF16
+    want_b = D.bf16_bits_to_f32(D.to_bf16_bits(oracle, want))
+    assert (np.abs(got - want_b) <= np.abs(want_b) * 2.0 ** -7 + 1e-30).mean() > 0.999
+
+
+CONFIG5_KN = [(8192, 10240), (8192, 8192), (8192, 57344), (28672, 8192)]  # qkv, o, gate_up, down
+
+
+@pytest.mark.parametrize("M", [1, 8, 64, 4096])
+@pytest.mark.parametrize("K,N", CONFIG5_KN)
+def test_w4a16_config5_full_sampled(oracle, ops, M, K, N):
+    """Benchmark config 5 (Llama-3-70B linears) at full size.  The weights are
+    random codes, fp16 scales and zero points (a GEMM does not care how they
+    were made); the GPU computes the whole [M, N] output, and a sample of rows
+    x columns is checked against the oracle run on the same codes sliced to
+    those columns (the int4 format is per column, so the slice is exact)."""
+    import torch
+    G = 128
+    g = D.rng(1000 + M + N)
+    p = g.integers(0, 256, (K // 2, N), dtype=np.uint8)
+    s = oracle.f32_to_f16_n(g.uniform(0.0005, 0.004, (K // G, N)).astype(np.float32))
+    z = g.integers(0, 16, (K // G, N), dtype=np.uint8)
+    A = D.to_bf16_bits(oracle, g.standard_normal((M, K)).astype(np.float32))
+    w = ops.prepack_w4_asym(ops.dev(p), ops.dev(s), ops.dev(z), K, N, G)
+    C = ops.host(ops.gemm_w4a16_bf16(ops.dev(A), w), np.uint16)
+    del w
+    torch.cuda.empty_cache()
+    rows = np.unique(np.concatenate([g.choice(M, min(M, 12), replace=False), [0, M - 1]]))
+    cols = np.unique(np.concatenate([g.choice(N, 48, replace=False), [0, N - 1]]))
+    want = oracle.gemm_w4a16_asym(np.ascontiguousarray(A[rows]), np.ascontiguousarray(p[:, cols]),
+                                  np.ascontiguousarray(s[:, cols]), np.ascontiguousarray(z[:, cols]), len(cols), G)
+    got = D.bf16_bits_to_f32(C[np.ix_(rows, cols)])
+    assert rel_frobenius(got, want) <= TOL_BF16
+    want_b = D.bf16_bits_to_f32(D.to_bf16_bits(oracle, want))
+    assert (np.abs(got - want_b) <= np.abs(want_b) * 2.0 ** -7 + 1e-30).mean() > 0.99
+
+
 @pytest.mark.parametrize("G", [32, 64, 256])
 def test_w4a16_bf16_group_sizes(oracle, ops, G):
     got, want = _asym_case(oracle, ops, 3, 1024, 96, G, seed=G)
