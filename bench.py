@@ -542,6 +542,31 @@ def prefill_legs(ops):
     return out
 
 
+def config_sweep(ops, name, ms, kns, G=128):
+    """W4A16 bf16 over a benchmark config's shapes: each (M, K, N) timed like
+    the decode leg (rotating weight sets where one set fits in the Infinity
+    Cache), reported against the HBM roofline (algorithmic bytes) and the
+    bf16 MFMA roofline (2*M*K*N)."""
+    out = []
+    for m in ms:
+        for k, n in kns:
+            flops = 2 * m * k * n
+            steps = 200 if m <= 64 else max(10, int(2e14 // flops))
+            r = bench_w4a16(ops, m, k, n, G, steps, max(5, steps // 10))
+            tf = flops / (r["us_per_call"] * 1e-6) / 1e12
+            bound = "hbm" if r["gbs"] / HBM_PEAK_GBS >= tf / BF16_PEAK_TFLOPS else "mfma"
+            out.append({"M": m, "K": k, "N": n, "us_per_call": round(r["us_per_call"], 2),
+                        "gbs": round(r["gbs"], 1), "hbm_frac": round(r["hbm_frac"], 4),
+                        "tflops": round(tf, 1), "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4), "bound": bound})
+            log(f"  {name} M={m} K={k} N={n}: {r['us_per_call']:.1f} us  {r['gbs']:.0f} GB/s "
+                f"({100 * r['hbm_frac']:.1f}% HBM)  {tf:.0f} TFLOPS ({100 * tf / BF16_PEAK_TFLOPS:.1f}% bf16)")
+    return out
+
+
+CONFIG2 = ((1, 4, 16), ((4096, 4096), (4096, 11008), (11008, 4096)))
+CONFIG5 = ((1, 8, 64, 4096), ((8192, 10240), (8192, 8192), (8192, 57344), (28672, 8192)))
+
+
 def moe_layer_leg(ops):
     log("moe layer (config 4, Mixtral shapes): dispatch, gate/up + SwiGLU, down, combine")
     r = bench_moe_layer(ops, 100, 10)
@@ -564,7 +589,7 @@ def main() -> int:
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a 1 GiB device copy (PMC calibration kernel)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the W4A16 prefill and MoE legs")
-    ap.add_argument("--only", choices=["w4a16", "w8a8", "prefill", "moe", "fp8"], default=None,
+    ap.add_argument("--only", choices=["w4a16", "w8a8", "prefill", "moe", "fp8", "configs"], default=None,
                     help="run one leg only (profiling); prints that leg's summary, not the bench line")
     args = ap.parse_args()
 
@@ -598,6 +623,10 @@ def main() -> int:
             log(f"fp8 e4m3 GEMM M={m} K=4096 N=14336: {r['us_per_call']:.1f} us  {r['tflops']:.0f} TFLOPS "
                 f"({100 * r['mfma_frac']:.1f}% of fp8 peak)")
             print(json.dumps(r), flush=True)
+        return 0
+    if args.only == "configs":
+        print(json.dumps({"leg": "w4a16_config2", "shapes": config_sweep(ops, "config 2", *CONFIG2)}), flush=True)
+        print(json.dumps({"leg": "w4a16_config5", "shapes": config_sweep(ops, "config 5", *CONFIG5)}), flush=True)
         return 0
     if args.only == "moe":
         print(json.dumps(moe_layer_leg(ops)), flush=True)
