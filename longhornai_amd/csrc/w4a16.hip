@@ -1435,10 +1435,20 @@ int launch_w4(W4Args a, int batch, hipStream_t s, int mblocks = -1) {
     if (env_t == 1 || env_t == 2) T = env_t;
     if constexpr (SWI) T = 2;
     // Enough waves to cover 256 CUs several times over, but at least four
-    // K tiles per wave so each wave keeps loads in flight.
-    const int64_t wgs = static_cast<int64_t>(ceil_div(a.Nt, T)) * mblocks * batch;
+    // K tiles per wave so each wave keeps loads in flight.  A grouped launch
+    // sizes this by the row blocks that can hold rows, ceil(rows / 16) plus
+    // one partial block per group that has rows, not by its grid bound (with
+    // a few tokens over many experts most of the grid exits at once, and
+    // measured at 2 rows over 8 experts, K=14336, N=4096: 2 waves walking 56
+    // K tiles each took 46.6 us).
+    const int64_t live_blocks = GR ? std::min<int64_t>(mblocks, ceil_div(a.M, 16) + std::min(a.num_groups, a.M))
+                                   : mblocks;
+    const int64_t wgs = static_cast<int64_t>(ceil_div(a.Nt, T)) * live_blocks * batch;
+    // Also split K further while a wave would walk more than 16 K tiles:
+    // the kernel does not prefetch across its K loop, so a long walk by a
+    // few waves waits out the memory latency once per tile.
     int W = 2;
-    while (W < 8 && wgs * W < 4096 && a.Kt / (2 * W) >= 4) W *= 2;
+    while (W < 8 && (wgs * W < 4096 || a.Kt > 16 * W) && a.Kt / (2 * W) >= 4) W *= 2;
     if (env_w == 1 || env_w == 2 || env_w == 4 || env_w == 8) W = env_w;
     dim3 grid(ceil_div(a.Nt, T), mblocks, batch);
     if constexpr (SWI) launch_gemv_waves<F32A, ASYM, F32C, 2, GR, true>(a, grid, W, bps, s);
