@@ -1351,9 +1351,16 @@ bool mma_applies(const W4Args& a, int64_t rows, double rows_per_block) {
     }();
     if (env == 0) return false;
     if (a.G < kW4TileK || a.K % kW4TileK != 0 || rows * a.K >= (int64_t{1} << 31)) return false;
-    // measured at K=8192, N=28672: M=32 is faster on the 16-row GEMV (72 vs
-    // 123 us), M=64 on the tile kernel (123 vs 143 us)
-    return env == 1 || rows_per_block >= 48.0;
+    // The 16-row kernel re-reads the activation rows for every column tile
+    // (rows * K * 2 bytes per 16 columns, from L2), the tile kernel once per
+    // 256 columns through LDS; the tile kernel has fewer workgroups.
+    // Measured on MI355X (us, 16-row kernel vs tile kernel):
+    //   rows 16: K=8192 N=8192 20 vs 48, N=57344 74 vs 87;
+    //   rows 32: N=8192 35 vs 48, N=28672 112 vs 55, N=57344 214 vs 90,
+    //            K=28672 N=8192 114 vs 155;
+    //   rows 48: N=8192 58 vs 50, N=28672 184 vs 57.
+    // (columns counted as the launch sees them: 2 x I for the SwiGLU launch)
+    return env == 1 || rows_per_block >= 48.0 || (rows_per_block > 16.0 && a.Nt * kW4TileN >= 16384);
 }
 
 // mblocks: 16-row blocks along grid.y (for a grouped launch, an upper bound
