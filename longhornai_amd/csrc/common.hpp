@@ -183,6 +183,21 @@ __device__ __forceinline__ u32x4_t w4_operand(uint32_t d) {
     return b;
 }
 
+// The same with the zero point folded in: zb holds 16 - z in each byte, so
+// every code byte becomes u + 16 - z (1..31, no carry between bytes) and the
+// operands are the exact bf16 integers 144 + u - z.
+__device__ __forceinline__ u32x4_t w4_operand_z(uint32_t d, uint32_t zb) {
+    const uint32_t lo = (d & 0x0F0F0F0Fu) + zb;
+    const uint32_t hi = ((d >> 4) & 0x0F0F0F0Fu) + zb;
+    constexpr uint32_t kExp = 0x43434343u;
+    u32x4_t b;
+    b[0] = __builtin_amdgcn_perm(kExp, lo, 0x04010400u);
+    b[1] = __builtin_amdgcn_perm(kExp, lo, 0x04030402u);
+    b[2] = __builtin_amdgcn_perm(kExp, hi, 0x04010400u);
+    b[3] = __builtin_amdgcn_perm(kExp, hi, 0x04030402u);
+    return b;
+}
+
 }  // namespace lhq
 
 // ---------------------------------------------------------------------------

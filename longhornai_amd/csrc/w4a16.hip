@@ -34,6 +34,7 @@ namespace lhq {
 namespace {
 
 constexpr uint32_t kOnesBf16x2 = 0x3F803F80u;  // bf16 pair (1.0, 1.0)
+constexpr uint32_t kM144Bf16x2 = 0xC310C310u;  // bf16 pair (-144.0, -144.0), exact
 
 struct W4Args {
     const void* A;
@@ -1055,7 +1056,7 @@ __global__ __launch_bounds__(256, 2) void w4_mma_kernel(W4Args p) {
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int c = 0; c < MM_CT; ++c) acc[i][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    const u32x4_t ones = {kOnesBf16x2, kOnesBf16x2, kOnesBf16x2, kOnesBf16x2};
+    const u32x4_t m144 = {kM144Bf16x2, kM144Bf16x2, kM144Bf16x2, kM144Bf16x2};
     // fragment (row block i, k block j): LDS row 64*wr + 16*i + (lane & 15), k
     // chunk 4j + (lane >> 4), stored in slot chunk ^ (lane & 15)
     const uint32_t a_frag = static_cast<uint32_t>((wr * 64 + col) * 256);
@@ -1075,47 +1076,49 @@ __global__ __launch_bounds__(256, 2) void w4_mma_kernel(W4Args p) {
             for (int j = 0; j < 4; ++j)
                 a[i][j] = *reinterpret_cast<const u32x4_t*>(buf + a_frag + i * 16 * 256 +
                                                             (((4 * j + (lane >> 4)) ^ col) * 16));
-        f32x4_t xs[4][SEGS];
+        // xs = -144 * sum_k x (the MFMA against a -144 operand), per row
+        // block; it seeds every t chain of the K tile (below)
+        static_assert(SEGS == 1, "one scale segment per K tile");
+        f32x4_t xs[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i) {
+            xs[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int s = 0; s < SEGS; ++s) {
-                xs[i][s] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int jj = 0; jj < BPS; ++jj) xs[i][s] = mfma_bf16_16x16x32(a[i][s * BPS + jj], ones, xs[i][s]);
-            }
+            for (int j = 0; j < 4; ++j) xs[i] = mfma_bf16_16x16x32(a[i][j], m144, xs[i]);
+        }
+        // The zero point enters the weight operand: each code byte gets
+        // 16 - z added before it becomes a bf16 integer, which is then
+        // 144 + u - z (exact), so the chain seeded with -144 * sum x yields
+        // t = sum_k x * (u - z) and the group's correction is acc += s * t.
         // Software pipeline over (column tile, row block) units: the t chain
         // of unit k is issued before the correction of unit k-1, which does
         // not depend on it, so the correction VALU runs while the matrix core
         // works instead of waiting on each chain.
-        static_assert(SEGS == 1, "one scale segment per K tile");
         f32x4_t tp = {0.f, 0.f, 0.f, 0.f};
-        float sp = 0.f, zp = 0.f;
-        auto correct = [&](int c, int i, const f32x4_t& t, float sc, float zc) {
+        float sp = 0.f;
+        auto correct = [&](int c, int i, const f32x4_t& t, float sc) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-                acc[i][c][r] = __builtin_fmaf(sc, __builtin_fmaf(-zc, xs[i][0][r], t[r]), acc[i][c][r]);
+            for (int r = 0; r < 4; ++r) acc[i][c][r] = __builtin_fmaf(sc, t[r], acc[i][c][r]);
         };
 #pragma unroll
         for (int c = 0; c < MM_CT; ++c) {
+            const int g = group_of_c<BPS, GBIG>(kt, 0, p.gmul);
+            const uint32_t zb = (16u - ((R.zw[c] >> (4 * (g & 7))) & 15u)) * 0x01010101u;
             u32x4_t b[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) b[j] = w4_operand(R.w[c][j]);
-            const int g = group_of_c<BPS, GBIG>(kt, 0, p.gmul);
+            for (int j = 0; j < 4; ++j) b[j] = w4_operand_z(R.w[c][j], zb);
             const float sc = f16_to_f32(static_cast<uint16_t>(R.sw[c][0] >> s_half));
-            const float zc = kW4Bias + static_cast<float>((R.zw[c] >> (4 * (g & 7))) & 15u);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                f32x4_t t = {0.f, 0.f, 0.f, 0.f};
+                f32x4_t t = xs[i];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) t = mfma_bf16_16x16x32(a[i][j], b[j], t);
-                if (c > 0 || i > 0) correct(i == 0 ? c - 1 : c, i == 0 ? 3 : i - 1, tp, sp, zp);
+                if (c > 0 || i > 0) correct(i == 0 ? c - 1 : c, i == 0 ? 3 : i - 1, tp, sp);
                 tp = t;
                 sp = sc;
-                zp = zc;
             }
         }
-        correct(MM_CT - 1, 3, tp, sp, zp);
+        correct(MM_CT - 1, 3, tp, sp);
     };
     // all of this wave's loads have landed and every wave is done with the
     // buffer the next DMA overwrites.  Builtins, not inline asm: the
