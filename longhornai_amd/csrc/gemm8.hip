@@ -218,8 +218,13 @@ __device__ __forceinline__ void gemm8_store(const Gemm8Args& p, const Acc (&acc)
 // 256x256 tile; 2: a 128x64 quadrant of a 256x128 half tile).
 constexpr int STAGED_PITCH = 4 * (128 + 4);
 
-template <int EPI, bool EDGE, int JB = 4>
-__device__ __forceinline__ void gemm8_store_staged(const Gemm8Args& p, const i32x16_t (&acc)[4][4], int m0, int n0,
+// FP8: fp32 accumulators (staged as their bit patterns) and the per-tensor
+// scales of gemm_fp8_e4m3 (gemm_quant.cpp:95-101: combined = (alpha * sA) * sB,
+// C = beta-applied C + combined * acc; with beta = 0, 0 + x is kept as an
+// add: an fp32 accumulator can be small enough for the product to underflow,
+// where fma(s, acc, +0) could return -0).
+template <int EPI, bool EDGE, int JB = 4, bool FP8 = false, typename Acc = i32x16_t>
+__device__ __forceinline__ void gemm8_store_staged(const Gemm8Args& p, const Acc (&acc)[4][4], int m0, int n0,
                                                    int wm, int wn, int lane, const float* ls, uint8_t* area) {
     constexpr int WQ = 32 * JB;                   // quadrant width
     constexpr int CPL = EPI == EPI_BF16 ? 8 : 4;  // columns per lane (16 output bytes)
@@ -228,7 +233,10 @@ __device__ __forceinline__ void gemm8_store_staged(const Gemm8Args& p, const i32
     const int lr = lane & 31, lh = lane >> 5;
     const int rsub = lane / LPR, cl = lane % LPR;
     float bsc[CPL];  // B_s of the lane's columns
-    if constexpr (EPI != EPI_I32) {
+    if constexpr (FP8) {
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) bsc[c] = p.Bs[0];
+    } else if constexpr (EPI != EPI_I32) {
 #pragma unroll
         for (int c = 0; c < CPL; c += 4) {
             const f32x4_t v = *reinterpret_cast<const f32x4_t*>(ls + BM + wn * WQ + cl * CPL + c);
@@ -236,6 +244,8 @@ __device__ __forceinline__ void gemm8_store_staged(const Gemm8Args& p, const i32
             for (int r = 0; r < 4; ++r) bsc[c + r] = v[r];
         }
     }
+    // an accumulator as fp32: int8 converts the int32, FP8 reinterprets bits
+    auto accf = [](int32_t v) { return FP8 ? __int_as_float(v) : static_cast<float>(v); };
     // this wave's quadrant of C, 32-bit element offsets from its first element
     const size_t quad_off = static_cast<size_t>(m0 + wm * 128) * p.N + n0 + wn * WQ;
     const bool beta0 = p.beta == 0.0f;
@@ -248,7 +258,8 @@ __device__ __forceinline__ void gemm8_store_staged(const Gemm8Args& p, const i32
 #pragma unroll
             for (int q = 0; q < 4; ++q)
                 *reinterpret_cast<i32x4_t*>(area + lr * STAGED_PITCH + (j * 32 + 4 * lh + 8 * q) * 4) =
-                    i32x4_t{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                    __builtin_bit_cast(i32x4_t, decltype(acc[i][j].xyzw){acc[i][j][4 * q], acc[i][j][4 * q + 1],
+                                                                          acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]});
     };
     auto wave_sync = [&]() {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -274,7 +285,8 @@ __device__ __forceinline__ void gemm8_store_staged(const Gemm8Args& p, const i32
 #pragma unroll
                 for (int r = 0; r < 4; ++r) ab[t][c + r] = v[r];
             }
-            if constexpr (EPI != EPI_I32) rsb[t] = ls[wm * 128 + i * 32 + R];
+            if constexpr (FP8) rsb[t] = p.As[0];
+            else if constexpr (EPI != EPI_I32) rsb[t] = ls[wm * 128 + i * 32 + R];
         }
         // block i + 1 goes to LDS while block i is scaled and stored: a
         // wave's LDS operations execute in order, so these writes land after
@@ -304,7 +316,7 @@ __device__ __forceinline__ void gemm8_store_staged(const Gemm8Args& p, const i32
                 if constexpr (EPI == EPI_BF16) {
                     // C = 0 + rescaled, rounded to bf16
 #pragma unroll
-                    for (int c = 0; c < CPL; ++c) f[c] = __builtin_fmaf(rs * bsc[c], static_cast<float>(a[c]), 0.0f);
+                    for (int c = 0; c < CPL; ++c) f[c] = __builtin_fmaf(rs * bsc[c], accf(a[c]), 0.0f);
                     const u32x4_t v = {pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
                                        pack_bf16x2(f[6], f[7])};
                     uint16_t* Cp = static_cast<uint16_t*>(p.C) + quad_off + o;
@@ -324,11 +336,15 @@ __device__ __forceinline__ void gemm8_store_staged(const Gemm8Args& p, const i32
                         for (int c = 0; c < 4; ++c) {
                             if (c >= cols_left) continue;
                             float x;
-                            if (beta0) {
-                                x = __builtin_fmaf(rs * bsc[c], static_cast<float>(a[c]), 0.0f);
+                            if (beta0 && !FP8) {
+                                x = __builtin_fmaf(rs * bsc[c], accf(a[c]), 0.0f);
+                            } else if (beta0) {
+                                f[c] = rs * bsc[c];
+                                f[c] = f[c] * accf(a[c]);
+                                x = 0.0f + f[c];
                             } else {
                                 f[c] = rs * bsc[c];
-                                f[c] = f[c] * static_cast<float>(a[c]);
+                                f[c] = f[c] * accf(a[c]);
                                 const float base = (p.beta == 1.0f) ? Cp[c] : Cp[c] * p.beta;
                                 x = base + f[c];
                             }
@@ -336,16 +352,23 @@ __device__ __forceinline__ void gemm8_store_staged(const Gemm8Args& p, const i32
                         }
                         continue;
                     }
-                    if (beta0) {
+                    if (beta0 && !FP8) {
 #pragma unroll
-                        for (int c = 0; c < 4; ++c) c4[c] = __builtin_fmaf(rs * bsc[c], static_cast<float>(a[c]), 0.0f);
+                        for (int c = 0; c < 4; ++c) c4[c] = __builtin_fmaf(rs * bsc[c], accf(a[c]), 0.0f);
+                    } else if (beta0) {
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            f[c] = rs * bsc[c];
+                            f[c] = f[c] * accf(a[c]);
+                            c4[c] = 0.0f + f[c];
+                        }
                     } else {
                         // apply_beta (gemm_quant.cpp:12-21), then C += rescaled
                         c4 = *reinterpret_cast<const f32x4_t*>(Cp);
 #pragma unroll
                         for (int c = 0; c < 4; ++c) {
                             f[c] = rs * bsc[c];
-                            f[c] = f[c] * static_cast<float>(a[c]);
+                            f[c] = f[c] * accf(a[c]);
                             const float base = (p.beta == 1.0f) ? c4[c] : c4[c] * p.beta;
                             c4[c] = base + f[c];
                         }
@@ -827,7 +850,15 @@ __device__ __forceinline__ void dma_tile_fp8(const Gemm8Args& p, uint8_t* ds_lds
             if (u == 0 || s + u < nk) step(stage_buf(u), stage_buf((u + 1) % STAGES), s + u);
     }
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-    gemm8_epilogue<OP_FP8, EPI_F32>(p, acc, m0, n0, wm, wn, lane);
+    // every wave's DMAs have landed and no wave reads the stage buffers again:
+    // the epilogue stages its accumulators there
+    __syncthreads();
+    uint8_t* const area = ds_lds + wave * 32 * STAGED_PITCH;
+    static_assert(4 * 32 * STAGED_PITCH <= STAGES * 2 * DS_OP_BYTES, "epilogue staging fits the stages");
+    if (m0 + BM <= p.M && n0 + BN <= p.N && p.N % 8 == 0 && p.c_vec)
+        gemm8_store_staged<EPI_F32, false, 4, true>(p, acc, m0, n0, wm, wn, lane, nullptr, area);
+    else
+        gemm8_store_staged<EPI_F32, true, 4, true>(p, acc, m0, n0, wm, wn, lane, nullptr, area);
 }
 
 template <int STAGES>
