@@ -88,18 +88,40 @@ __device__ __forceinline__ int seg_group(int kt, int s, const W4Args& p) {
 // Map blockIdx.y of a grouped launch to (group, first row, row end): groups
 // take ceil(rows/RB) row blocks each, in order.  Offsets are clamped to
 // [0, row_capacity] so a malformed table can never index outside A or C.
+// The wave resolves 64 groups per step: lane i takes group e0 + i, a prefix
+// sum over the lanes gives each group's first block, and a ballot finds the
+// group holding block y (4 steps for 256 experts, where a serial walk of the
+// table by every workgroup cost milliseconds per layer).  The results are
+// the same in every lane and wave (y is uniform): the return is uniform per
+// workgroup.
 template <int RB = 16>
 __device__ __forceinline__ bool resolve_group(const W4Args& p, int y, int& e, int& m0, int& m_end) {
-    for (e = 0; e < p.num_groups; ++e) {
-        const int r0 = min(max(p.offsets[e], 0), p.row_capacity);
-        const int r1 = min(max(p.offsets[e + 1], r0), p.row_capacity);
+    const int lane = threadIdx.x & 63;
+    int base = 0;  // row blocks of the groups before this step's
+    for (int e0 = 0; e0 < p.num_groups; e0 += 64) {
+        const int g = e0 + lane;
+        int r0 = 0, r1 = 0;
+        if (g < p.num_groups) {
+            r0 = min(max(p.offsets[g], 0), p.row_capacity);
+            r1 = min(max(p.offsets[g + 1], r0), p.row_capacity);
+        }
         const int nb = (r1 - r0 + RB - 1) / RB;
-        if (y < nb) {
-            m0 = r0 + RB * y;
-            m_end = r1;
+        int incl = nb;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int v = __shfl_up(incl, d, 64);
+            if (lane >= d) incl += v;
+        }
+        const int excl = incl - nb;
+        const uint64_t hit = __ballot(y >= base + excl && y < base + incl);
+        if (hit) {
+            const int src = __builtin_ctzll(hit);
+            e = __builtin_amdgcn_readfirstlane(e0 + src);
+            m0 = __builtin_amdgcn_readfirstlane(__shfl(r0, src, 64) + RB * (y - base - __shfl(excl, src, 64)));
+            m_end = __builtin_amdgcn_readfirstlane(__shfl(r1, src, 64));
             return true;
         }
-        y -= nb;
+        base += __shfl(incl, 63, 64);
     }
     return false;
 }

@@ -273,6 +273,18 @@ def test_w4a16_grouped_small(oracle, ops):
     assert rel_frobenius(got, want) <= TOL_BF16
 
 
+@pytest.mark.parametrize("T,E,topk,K,N", [
+    (300, 200, 2, 256, 48),    # 200 groups of ~3 rows: the 16-row kernel, 4 steps of 64 groups
+    (1750, 70, 2, 256, 64),    # 70 groups of ~50 rows: the tile kernel, 2 steps of 64 groups
+])
+def test_w4a16_grouped_many_groups(oracle, ops, T, E, topk, K, N):
+    """More groups than one wave resolves at once (workgroups find their
+    group 64 groups at a time)."""
+    got, want, off = _grouped(oracle, ops, T=T, E=E, topk=topk, K=K, N=N, G=128, seed=E)
+    assert off[-1] == T * topk
+    assert rel_frobenius(got, want) <= TOL_BF16
+
+
 def test_w4a16_grouped_empty_expert(oracle, ops):
     got, want, off = _grouped(oracle, ops, T=20, E=4, topk=1, K=128, N=48, G=64, seed=3, empty_expert=2)
     assert off[3] == off[2]
