@@ -57,6 +57,7 @@ struct W4Args {
     const void* const* scs;
     const uint32_t* const* zss;
     int num_groups, row_capacity;
+    int group_rb;  // rows per row block of a grouped decode launch
 };
 
 // Scale group of segment s of K tile kt; a segment is BPS 32-wide k blocks
@@ -93,9 +94,9 @@ __device__ __forceinline__ int seg_group(int kt, int s, const W4Args& p) {
 // group holding block y (4 steps for 256 experts, where a serial walk of the
 // table by every workgroup cost milliseconds per layer).  The results are
 // the same in every lane and wave (y is uniform): the return is uniform per
-// workgroup.
-template <int RB = 16>
-__device__ __forceinline__ bool resolve_group(const W4Args& p, int y, int& e, int& m0, int& m_end) {
+// workgroup.  rb: rows per block (a compile-time constant through
+// resolve_group<RB>; a run-time one for the grouped decode kernel).
+__device__ __forceinline__ bool resolve_group_rows(const W4Args& p, int y, int rb, int& e, int& m0, int& m_end) {
     const int lane = threadIdx.x & 63;
     int base = 0;  // row blocks of the groups before this step's
     for (int e0 = 0; e0 < p.num_groups; e0 += 64) {
@@ -105,7 +106,7 @@ __device__ __forceinline__ bool resolve_group(const W4Args& p, int y, int& e, in
             r0 = min(max(p.offsets[g], 0), p.row_capacity);
             r1 = min(max(p.offsets[g + 1], r0), p.row_capacity);
         }
-        const int nb = (r1 - r0 + RB - 1) / RB;
+        const int nb = (r1 - r0 + rb - 1) / rb;
         int incl = nb;
 #pragma unroll
         for (int d = 1; d < 64; d <<= 1) {
@@ -117,13 +118,17 @@ __device__ __forceinline__ bool resolve_group(const W4Args& p, int y, int& e, in
         if (hit) {
             const int src = __builtin_ctzll(hit);
             e = __builtin_amdgcn_readfirstlane(e0 + src);
-            m0 = __builtin_amdgcn_readfirstlane(__shfl(r0, src, 64) + RB * (y - base - __shfl(excl, src, 64)));
+            m0 = __builtin_amdgcn_readfirstlane(__shfl(r0, src, 64) + rb * (y - base - __shfl(excl, src, 64)));
             m_end = __builtin_amdgcn_readfirstlane(__shfl(r1, src, 64));
             return true;
         }
         base += __shfl(incl, 63, 64);
     }
     return false;
+}
+template <int RB = 16>
+__device__ __forceinline__ bool resolve_group(const W4Args& p, int y, int& e, int& m0, int& m_end) {
+    return resolve_group_rows(p, y, RB, e, m0, m_end);
 }
 
 // Eight activations (row `off / K`, k = off % K .. +7) as bf16 MFMA operands.
@@ -351,10 +356,17 @@ __global__ __launch_bounds__(64 * WAVES) void w4_gemv_kernel(W4Args p) {
 // Launch bounds: one-column-tile bf16-activation variants are held to four
 // waves per SIMD (<= 128 VGPRs; they need ~90).  Two-column-tile variants
 // need ~136 and would spill inside the loop under that bound.
-template <bool F32A, bool ASYM, bool F32C, int T, int NPW, int BPS, bool GBIG, int MR>
+// GR: ragged groups (bf16 activations and output, fp16 scales): grid.y
+// walks row blocks of p.group_rb rows over the groups (resolve_group_rows),
+// each staged whole; SWI adds the SwiGLU epilogue on the two column tiles
+// of a workgroup (gate 2j, up 2j + 1).
+template <bool F32A, bool ASYM, bool F32C, int T, int NPW, int BPS, bool GBIG, int MR, bool GR = false,
+          bool SWI = false>
 __global__ __launch_bounds__(T == 1 ? 1024 : 512, (F32A || T == 2) ? 1 : 4) void w4_decode_kernel(W4Args p) {
     static_assert(NPW == 4 || NPW == 8, "passes start at multiples of NPW tiles");
     static_assert(MR == 1 || MR == 4, "one row or all four");
+    static_assert(!GR || (!F32A && ASYM && !F32C && MR == 4), "grouped: bf16 in and out, fp16 scales");
+    static_assert(!SWI || (GR && T == 2), "SwiGLU pairs the two column tiles of a workgroup");
     constexpr int SEGS = 4 / BPS;
     // zero words (8 groups each) per pass: G < 128 -> the pass's words
     // (passes start at multiples of 8 tiles); G == 128 -> one shared word;
@@ -370,7 +382,18 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512, (F32A || T == 2) ? 1 : 4) void
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int z = blockIdx.z;
-    const int Ml = min(p.M, 16);
+    const uint8_t* qw = p.qw + z * p.qw_bs;
+    const char* scales = static_cast<const char*>(p.scales) + z * p.s_bs * (ASYM ? 2 : 4);
+    const uint32_t* zeros = ASYM ? p.zeros + z * p.z_bs : nullptr;
+    int m0 = 0, Ml = min(p.M, 16);  // first row and row count of this workgroup
+    if constexpr (GR) {
+        int e, m_end;
+        if (!resolve_group_rows(p, blockIdx.y, p.group_rb, e, m0, m_end)) return;  // uniform per workgroup
+        qw = p.qws[e];
+        scales = static_cast<const char*>(p.scs[e]);
+        zeros = p.zss[e];
+        Ml = min(m_end - m0, p.group_rb);
+    }
     const int col = lane & 15;
     const int Kp = p.Kt * kW4TileK;
 
@@ -383,9 +406,9 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512, (F32A || T == 2) ? 1 : 4) void
 #pragma unroll
     for (int t = 0; t < T; ++t) {
         const int64_t nt = min(static_cast<int>(blockIdx.x) * T + t, p.Nt - 1);
-        qwb[t] = p.qw + z * p.qw_bs + nt * p.Kt * kW4TileBytes;
-        scb[t] = static_cast<const char*>(p.scales) + (z * p.s_bs + nt * p.NG * 16) * (ASYM ? 2 : 4);
-        zwb[t] = ASYM ? reinterpret_cast<const char*>(p.zeros + z * p.z_bs + nt * p.NG8 * 16) : nullptr;
+        qwb[t] = qw + nt * p.Kt * kW4TileBytes;
+        scb[t] = scales + nt * p.NG * 16 * (ASYM ? 2 : 4);
+        zwb[t] = ASYM ? reinterpret_cast<const char*>(zeros + nt * p.NG8 * 16) : nullptr;
     }
     // fp16 scales are fetched as the aligned dword holding columns
     // (col & ~1, col | 1); the lane's half is selected at use
@@ -434,7 +457,7 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512, (F32A || T == 2) ? 1 : 4) void
     const int span = S * NPW;  // tiles per pass over the workgroup
     const int rc = Kp >> 3;    // 8-element chunks per padded row
     const int chunks = Ml * rc;
-    const char* A = static_cast<const char*>(p.A) + z * p.a_bs * (F32A ? 4 : 2);
+    const char* A = static_cast<const char*>(p.A) + (z * p.a_bs + static_cast<int64_t>(m0) * p.K) * (F32A ? 4 : 2);
     constexpr int B = 4;  // chunks per thread per staging batch
     u32x4_t av[B], av2[B];
     auto stage_load = [&](int c0) {
@@ -581,8 +604,8 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512, (F32A || T == 2) ? 1 : 4) void
         const int r = 4 * (ln >> 4) + r_in;
         const int ntt = static_cast<int>(blockIdx.x) * T + t;
         const int c = ntt * kW4TileN + (ln & 15);
-        if (r >= p.M || c >= p.N || ntt >= p.Nt) return;
-        w4_store<F32C>(p, z * p.c_bs + static_cast<int64_t>(r) * p.N + c, v);
+        if (r >= Ml || c >= p.N || ntt >= p.Nt) return;
+        w4_store<F32C>(p, z * p.c_bs + static_cast<int64_t>(m0 + r) * p.N + c, v);
     };
     // red[wave][t][r][lane], r < MR, in the activation area once every
     // wave is done reading it
@@ -593,11 +616,27 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512, (F32A || T == 2) ? 1 : 4) void
 #pragma unroll
         for (int r = 0; r < MR; ++r) red[((wave * T + t) * MR + r) * 64 + lane] = acc[t][r];
     __syncthreads();
-    for (int idx = threadIdx.x; idx < T * MR * 64; idx += 64 * S) {
-        const int t = idx / (MR * 64), r = (idx / 64) % MR, ln = idx & 63;
-        float sum = 0.0f;
-        for (int w2 = 0; w2 < S; ++w2) sum += red[((w2 * T + t) * MR + r) * 64 + ln];
-        store(t, r, ln, sum);
+    if constexpr (SWI) {
+        // tiles 2j (gate) and 2j + 1 (up) -> act column tile j = blockIdx.x
+        for (int idx = threadIdx.x; idx < MR * 64; idx += 64 * S) {
+            const int r_in = idx / 64, ln = idx & 63;
+            float g = 0.0f, u = 0.0f;
+            for (int w2 = 0; w2 < S; ++w2) {
+                g += red[((w2 * T + 0) * MR + r_in) * 64 + ln];
+                u += red[((w2 * T + 1) * MR + r_in) * 64 + ln];
+            }
+            const int r = 4 * (ln >> 4) + r_in;
+            const int c = static_cast<int>(blockIdx.x) * kW4TileN + (ln & 15);
+            if (r < Ml && c < p.N)
+                static_cast<uint16_t*>(p.C)[static_cast<int64_t>(m0 + r) * p.N + c] = f32_to_bf16(swiglu(g, u));
+        }
+    } else {
+        for (int idx = threadIdx.x; idx < T * MR * 64; idx += 64 * S) {
+            const int t = idx / (MR * 64), r = (idx / 64) % MR, ln = idx & 63;
+            float sum = 0.0f;
+            for (int w2 = 0; w2 < S; ++w2) sum += red[((w2 * T + t) * MR + r) * 64 + ln];
+            store(t, r, ln, sum);
+        }
     }
 }
 
@@ -1284,6 +1323,31 @@ void launch_decode_mr(const W4Args& a, dim3 grid, int S, int bps, size_t lds, hi
     }
 }
 
+// Grouped decode (bf16, fp16 scales, four K tiles per wave per pass).
+template <int T, bool SWI>
+void launch_decode_grouped(const W4Args& a, dim3 grid, int S, int bps, size_t lds, hipStream_t s) {
+    lds = std::max(lds, static_cast<size_t>(S) * T * 4 * 64 * sizeof(float));  // the reduction reuses it
+    switch (bps) {
+        case 1:
+            allow_cu_lds<&w4_decode_kernel<false, true, false, T, 4, 1, false, 4, true, SWI>>();
+            w4_decode_kernel<false, true, false, T, 4, 1, false, 4, true, SWI><<<grid, 64 * S, lds, s>>>(a);
+            break;
+        case 2:
+            allow_cu_lds<&w4_decode_kernel<false, true, false, T, 4, 2, false, 4, true, SWI>>();
+            w4_decode_kernel<false, true, false, T, 4, 2, false, 4, true, SWI><<<grid, 64 * S, lds, s>>>(a);
+            break;
+        default:
+            if (a.gmul) {
+                allow_cu_lds<&w4_decode_kernel<false, true, false, T, 4, 4, true, 4, true, SWI>>();
+                w4_decode_kernel<false, true, false, T, 4, 4, true, 4, true, SWI><<<grid, 64 * S, lds, s>>>(a);
+            } else {
+                allow_cu_lds<&w4_decode_kernel<false, true, false, T, 4, 4, false, 4, true, SWI>>();
+                w4_decode_kernel<false, true, false, T, 4, 4, false, 4, true, SWI><<<grid, 64 * S, lds, s>>>(a);
+            }
+            break;
+    }
+}
+
 template <bool F32A, bool ASYM, bool F32C, int T, int NPW>
 void launch_decode_bps(const W4Args& a, dim3 grid, int S, int bps, size_t lds, hipStream_t s) {
     if (a.M == 1) launch_decode_mr<F32A, ASYM, F32C, T, NPW, 1>(a, grid, S, bps, lds, s);
@@ -1463,6 +1527,42 @@ int launch_w4(W4Args a, int batch, hipStream_t s, int mblocks = -1) {
         return check_launch("w4a16 decode");
     }
 
+    // Grouped decode: few rows per group (decode-time MoE), each group's
+    // rows staged in LDS in blocks of rb rows.  Taken when the groups average
+    // at most one row; rb = 4 (or as many rows as 64 KiB holds, if fewer)
+    // keeps a workgroup's LDS small enough for three per CU at K = 4096
+    // while a group of up to four rows still streams its weights once.
+    if constexpr (GR && !F32A && ASYM && !F32C) {
+        static const int env_grb = env_int("LHQ_W4_GRB");
+        const int64_t row_bytes = static_cast<int64_t>(a.Kt) * kW4TileK * 2;
+        const int rb_max = static_cast<int>(std::min<int64_t>(16, kDecodeMaxLds / row_bytes));
+        const int rb = (env_grb >= 1) ? std::min(env_grb, rb_max) : std::min(4, rb_max);
+        if (env_dec >= 0 && rb >= 1 && (a.M <= a.num_groups || env_grb >= 1)) {
+            a.group_rb = rb;
+            const int T = (SWI || a.Nt >= 1024) ? 2 : 1;
+            // at most min(groups, rows) groups hold rows: sum_e ceil(rows_e / rb)
+            // <= ceil(rows / rb) + min(groups, rows)
+            const int64_t blocks = ceil_div64(a.M, rb) + std::min(a.num_groups, a.M);
+            const int smax = (T == 1) ? 16 : 8;  // the kernel's launch bounds
+            const int64_t cols = static_cast<int64_t>(ceil_div(a.Nt, T)) * blocks;
+            // as the ungrouped decode, and at most 16 K tiles per wave
+            // (measured at K=14336, N=4096, 2 rows over 8 groups: 16.8 us
+            // with 4 waves, 14.2 with 8)
+            int S = 4;
+            while (S < smax && (cols * S < 2048 || a.Kt > 16 * S)) S *= 2;
+            S = max(1, min(S, ceil_div(a.Kt, 4)));
+            if (env_ds >= 1 && env_ds <= smax) S = env_ds;
+            if (blocks <= 65535) {
+                const size_t lds = static_cast<size_t>(std::min(a.M, rb)) * row_bytes;
+                dim3 grid(ceil_div(a.Nt, T), static_cast<unsigned>(blocks), 1);
+                if constexpr (SWI) launch_decode_grouped<2, true>(a, grid, S, bps, lds, s);
+                else if (T == 1) launch_decode_grouped<1, false>(a, grid, S, bps, lds, s);
+                else launch_decode_grouped<2, false>(a, grid, S, bps, lds, s);
+                return check_launch("w4a16 grouped decode");
+            }
+        }
+    }
+
     int T = (a.Nt >= 1024) ? 2 : 1;
     if (env_t == 1 || env_t == 2) T = env_t;
     if constexpr (SWI) T = 2;
@@ -1532,11 +1632,12 @@ int grouped_w4(const char* who, const uint16_t* A, const int32_t* offsets, const
     a.zss = zeros;
     a.num_groups = num_groups;
     a.row_capacity = row_capacity;
+    // at most min(num_groups, row_capacity) groups hold rows, so
+    // sum_e ceil(rows_e / B) <= ceil(row_capacity / B) + live_groups for row blocks of B
+    const int live_groups = std::min(num_groups, row_capacity);
     if (mma_applies(a, row_capacity, static_cast<double>(row_capacity) / num_groups))
-        // sum_e ceil(rows_e / BM) <= ceil(row_capacity / BM) + num_groups
-        return launch_mma<true, SWI>(a, row_capacity, num_groups, 1, as_stream(stream), who);
-    // sum_e ceil(rows_e / 16) <= ceil(row_capacity / 16) + num_groups
-    const int64_t mblocks = ceil_div64(row_capacity, 16) + num_groups;
+        return launch_mma<true, SWI>(a, row_capacity, live_groups, 1, as_stream(stream), who);
+    const int64_t mblocks = ceil_div64(row_capacity, 16) + live_groups;
     LHQ_SUPPORTED(mblocks <= 65535, "%s: %lld row blocks exceed the grid limit", who, static_cast<long long>(mblocks));
     return launch_w4<false, true, false, true, SWI>(a, 1, as_stream(stream), static_cast<int>(mblocks));
 }
