@@ -239,6 +239,11 @@ def _swiglu_case(oracle, ops, T, E, K, H, I, G, seed, kind="uniform"):
     (200, 4, 2, 512, 256, 128, "uniform"),  # ~100 rows per expert: 128x128 tile kernel
     (300, 8, 2, 384, 200, 128, "skewed"),   # tile kernel, I % 128 != 0, empty experts
     (512, 8, 2, 1024, 512, 128, "uniform"),  # config 4's routing
+    # at most one row per expert on average: the grouped decode kernel
+    (1, 8, 2, 4096, 256, 128, "uniform"),   # one token, two experts
+    (5, 8, 1, 512, 72, 64, "uniform"),      # G = 64, I % 16 != 0
+    (10, 16, 1, 384, 48, 32, "skewed"),     # 7 rows of one expert: two row blocks; G = 32
+    (6, 12, 2, 1024, 40, 256, "dropped"),   # G = 256, ids outside [0, E) dropped
 ])
 def test_grouped_swiglu(oracle, ops, T, E, K, H, I, G, kind):
     got, want = _swiglu_case(oracle, ops, T, E, K, H, I, G, 3000 + T, kind)
@@ -249,6 +254,7 @@ def test_grouped_swiglu(oracle, ops, T, E, K, H, I, G, kind):
 @pytest.mark.parametrize("T,E,K,H,I,G", [
     (40, 4, 2, 256, 384, 128),     # 16-row kernels
     (512, 8, 2, 512, 1024, 128),   # config 4's routing on the tile kernels
+    (2, 8, 2, 1024, 384, 128),     # 4 rows over 8 experts: the grouped decode kernels
 ])
 def test_expert_mlp(oracle, ops, T, E, K, H, I, G):
     ids = _routing(T, E, K, 4000 + T)

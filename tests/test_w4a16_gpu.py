@@ -285,6 +285,21 @@ def test_w4a16_grouped_many_groups(oracle, ops, T, E, topk, K, N):
     assert rel_frobenius(got, want) <= TOL_BF16
 
 
+@pytest.mark.parametrize("T,E,topk,K,N,G", [
+    (1, 8, 2, 4096, 256, 128),    # one token over 8 experts
+    (2, 4, 1, 256, 16400, 128),   # two column tiles per workgroup, N % 16 != 0
+    (8, 8, 1, 512, 200, 64),      # G = 64
+    (3, 4, 1, 1024, 96, 256),     # G = 256
+    (6, 12, 2, 384, 48, 32),      # G = 32, 3 K tiles
+])
+def test_w4a16_grouped_decode(oracle, ops, T, E, topk, K, N, G):
+    """At most one row per group on average: the grouped decode kernel, each
+    group's rows staged in LDS in blocks of up to 4."""
+    got, want, off = _grouped(oracle, ops, T=T, E=E, topk=topk, K=K, N=N, G=G, seed=50 + T)
+    assert off[-1] == T * topk <= E
+    assert rel_frobenius(got, want) <= TOL_BF16
+
+
 def test_w4a16_grouped_empty_expert(oracle, ops):
     got, want, off = _grouped(oracle, ops, T=20, E=4, topk=1, K=128, N=48, G=64, seed=3, empty_expert=2)
     assert off[3] == off[2]
