@@ -1006,10 +1006,11 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512) void w4_decode_i8_kernel(W4Arg
 //     groups;
 //   - each wave loads its four 1 KiB weight tiles and their scales / zero
 //     words straight into registers, one K tile ahead of their use;
-//   - per scale group segment: t = sum_k x*(128 + u) (MFMA on the exact
-//     bf16 integers of w4_operand), xs = sum_k x (MFMA against ones), and
-//     acc += s * (t - (128 + z) * xs) -- the decode kernel's arithmetic, with
-//     each weight tile decoded once per 64 rows instead of once per 16.
+//   - per K tile and row block: xs = -144 * sum_k x (an MFMA against a -144
+//     operand) seeds each column tile's chain t = xs + sum_k x*(144 + u - z)
+//     (MFMA on exact bf16 integers, the zero point folded into the codes),
+//     so t = sum_k x*(u - z) and the group correction is acc += s * t; each
+//     weight tile is decoded once per 64 rows instead of once per 16.
 // The K loop alternates two register sets (A buffer and weights of the tile
 // in flight vs the tile in use) and meets at one `s_waitcnt vmcnt(0)` +
 // `s_barrier` per tile: before it, only the tile about to be used is in
@@ -1019,28 +1020,31 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512) void w4_decode_i8_kernel(W4Arg
 // ---------------------------------------------------------------------------
 constexpr int MM_CT = 4;  // column tiles per wave
 // rows per workgroup tile: L == 0 ? 128 : 64; column tiles per workgroup:
-// (L == 1 ? 4 : 2) * MM_CT; one activation buffer: (L == 1 ? 64 : 128) rows of
-// 128 k x 2 bytes
+// (L == 1 ? 4 : 2) * MM_CT; K parts: 2 (L == 2) or 4 (L == 3, eight waves);
+// one activation buffer: 64 rows (L == 1), 128 (L == 0, 2) or 256 (L == 3)
+// of 128 k x 2 bytes
 
 #define LHQ_LDS_AS __attribute__((address_space(3)))
 
 template <int BPS, bool GBIG, bool GR, bool SWI, int L>
-__global__ __launch_bounds__(256, 2) void w4_mma_kernel(W4Args p) {
+__global__ __launch_bounds__(L == 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_kernel(W4Args p) {
     constexpr int SEGS = 4 / BPS;
+    constexpr int NW = (L == 3) ? 8 : 4;                   // waves
+    constexpr int NK = (L == 2) ? 2 : (L == 3) ? 4 : 1;  // K parts
     constexpr int BM = (L == 0) ? 128 : 64, WN = (L == 1) ? 4 : 2;
-    constexpr int A_BYTES = ((L == 1) ? 64 : 128) * kW4TileK * 2;
-    constexpr int DMA = A_BYTES / 1024 / 4;  // activation DMAs per wave per K tile
+    constexpr int A_BYTES = ((L == 1) ? 64 : (L == 3) ? 256 : 128) * kW4TileK * 2;
+    constexpr int DMA = A_BYTES / 1024 / NW;  // activation DMAs per wave per K tile
     extern __shared__ __attribute__((aligned(1024))) uint8_t mm_lds[];  // 2 x A_BYTES
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    // this wave's LDS activation region (row group or K half), row group,
-    // K half and column group
+    // this wave's LDS activation region (row group or K part), row group,
+    // K part and column group
     const int wr = (L == 1) ? 0 : (wave >> 1);
     const int wm = (L == 0) ? wr : 0;
-    const int ks = (L == 2) ? wr : 0;
+    const int ks = (NK > 1) ? wr : 0;
     const int wn = (L == 1) ? wave : (wave & 1);
-    const int kh = (L == 2) ? (p.Kt + 1) / 2 : p.Kt;  // K tiles per half
-    const int kofs = ks * kh;                           // this wave's first K tile
+    const int kh = (p.Kt + NK - 1) / NK;  // K tiles per part
+    const int kofs = ks * kh;             // this wave's first K tile
     const int z = blockIdx.z;
     int m0, m_end;
     const uint8_t* qw;
@@ -1074,7 +1078,7 @@ __global__ __launch_bounds__(256, 2) void w4_mma_kernel(W4Args p) {
     for (int q = 0; q < DMA; ++q) {
         const int idx = (DMA * wave + q) * 64 + lane;
         const int r = idx >> 4, slot = idx & 15;  // LDS row r: region r >> 6 (this wave's, wr)
-        const int row = min(m0 + ((L == 2) ? (r & 63) : r), m_end - 1);
+        const int row = min(m0 + ((NK > 1) ? (r & 63) : r), m_end - 1);
         a_off[q] = static_cast<uint32_t>(row) * static_cast<uint32_t>(p.K) + static_cast<uint32_t>((slot ^ (r & 15)) * 8);
     }
     // this wave's column tiles (clamped to the last one) and their bases
@@ -1129,7 +1133,7 @@ __global__ __launch_bounds__(256, 2) void w4_mma_kernel(W4Args p) {
     const bool live = m0 + 64 * wm < m_end;
     auto compute = [&](const uint8_t* buf, const Regs& R, int kt_in) {
         const int kt = kt_in + kofs;
-        if (!live || kt >= p.Kt) return;  // the second K half may be one tile short
+        if (!live || kt >= p.Kt) return;  // the last K part may be short
         u32x4_t a[4][4];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -1211,28 +1215,36 @@ __global__ __launch_bounds__(256, 2) void w4_mma_kernel(W4Args p) {
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-    if constexpr (L == 2) {
-        // K half 1 hands its accumulators to half 0 through LDS: after the
-        // barrier every wave's loads have landed and no wave reads the
-        // activation buffers again
+    if constexpr (NK > 1) {
+        // K parts 1.. hand their accumulators to part 0 through LDS, which
+        // adds them in part order (deterministic): after the barrier every
+        // wave's loads have landed and no wave reads the activation buffers
+        // again.  (NK-1) * WN * 16 KiB fits the 2 * A_BYTES of LDS.
+        static_assert((NK - 1) * WN * 4 * MM_CT * 64 * 16 <= 2 * A_BYTES, "reduction area");
         __syncthreads();
-        f32x4_t* red = reinterpret_cast<f32x4_t*>(mm_lds) + wn * (4 * MM_CT * 64);
-        if (ks == 1) {
+        f32x4_t* const red = reinterpret_cast<f32x4_t*>(mm_lds);
+        constexpr int RS = 4 * MM_CT * 64;  // f32x4 entries per wave's accumulators
+        if (ks > 0) {
+            f32x4_t* const mine = red + ((ks - 1) * WN + wn) * RS;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int c = 0; c < MM_CT; ++c) red[(i * MM_CT + c) * 64 + lane] = acc[i][c];
+                for (int c = 0; c < MM_CT; ++c) mine[(i * MM_CT + c) * 64 + lane] = acc[i][c];
         }
         __syncthreads();
-        if (ks == 1) return;
+        if (ks > 0) return;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int q = 1; q < NK; ++q) {
+            const f32x4_t* const part = red + ((q - 1) * WN + wn) * RS;
 #pragma unroll
-            for (int c = 0; c < MM_CT; ++c) {
-                const f32x4_t h = red[(i * MM_CT + c) * 64 + lane];
+            for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) acc[i][c][r] += h[r];
-            }
+                for (int c = 0; c < MM_CT; ++c) {
+                    const f32x4_t h = part[(i * MM_CT + c) * 64 + lane];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[i][c][r] += h[r];
+                }
+        }
     }
 
     // D element r of block (i, c): row 64*wm + 16*i + 4*(lane >> 4) + r,
@@ -1385,10 +1397,16 @@ void launch_gemv_waves(const W4Args& a, dim3 grid, int W, int bps, hipStream_t s
 // need four times the activation-sum registers and spill.
 template <bool GR, bool SWI, int L>
 void launch_mma_l(const W4Args& a, unsigned row_tiles, unsigned batch, hipStream_t s) {
-    constexpr size_t lds = 2 * ((L == 1) ? 64 : 128) * kW4TileK * 2;
+    constexpr size_t lds = 2 * ((L == 1) ? 64 : (L == 3) ? 256 : 128) * kW4TileK * 2;
+    constexpr int threads = (L == 3) ? 512 : 256;
     const dim3 grid(ceil_div(a.Nt, ((L == 1) ? 4 : 2) * MM_CT), row_tiles, batch);
-    if (a.gmul) w4_mma_kernel<4, true, GR, SWI, L><<<grid, 256, lds, s>>>(a);
-    else w4_mma_kernel<4, false, GR, SWI, L><<<grid, 256, lds, s>>>(a);
+    if (a.gmul) {
+        if constexpr (lds > 64 * 1024) allow_cu_lds<&w4_mma_kernel<4, true, GR, SWI, L>>();
+        w4_mma_kernel<4, true, GR, SWI, L><<<grid, threads, lds, s>>>(a);
+    } else {
+        if constexpr (lds > 64 * 1024) allow_cu_lds<&w4_mma_kernel<4, false, GR, SWI, L>>();
+        w4_mma_kernel<4, false, GR, SWI, L><<<grid, threads, lds, s>>>(a);
+    }
 }
 
 int device_cus() {
@@ -1406,9 +1424,11 @@ int device_cus() {
 // table of `groups` groups holding `rows` rows in all: each group adds at
 // most one partial row tile.  Layout 1 (64 x 256) unless its grid holds
 // fewer than two workgroups per CU (two fit, by LDS and registers) and K is
-// long: then layout 2 splits K for twice the workgroups.  Measured on MI355X:
+// long: then layout 2 splits K for twice the workgroups, and where even its
+// grid holds at most one workgroup per CU, layout 3 (eight waves, K in four
+// parts, 128 KiB of LDS) doubles the waves again.  Measured on MI355X:
 // 64 x 256 beat 128 x 128 on every shape tried (M=4096 K=8192 N=28672 2104
-// vs 2215 us; config 4's grouped GEMM 196 vs 229 us).  LHQ_W4_MMA_L (0|1|2)
+// vs 2215 us; config 4's grouped GEMM 196 vs 229 us).  LHQ_W4_MMA_L (0..3)
 // forces a layout.
 template <bool GR, bool SWI = false>
 int launch_mma(const W4Args& a, int64_t rows, int groups, int batch, hipStream_t s, const char* who) {
@@ -1419,13 +1439,15 @@ int launch_mma(const W4Args& a, int64_t rows, int groups, int batch, hipStream_t
     int l = 1;
     const int64_t wgs1 = static_cast<int64_t>(ceil_div(a.Nt, 4 * MM_CT)) * (ceil_div64(rows, 64) + groups) * batch;
     if (wgs1 < 2 * static_cast<int64_t>(device_cus()) && a.Kt >= 16) l = 2;
-    if (env_l >= 0 && env_l <= 2) l = env_l;
+    if (2 * wgs1 <= static_cast<int64_t>(device_cus()) && a.Kt >= 32) l = 3;
+    if (env_l >= 0 && env_l <= 3) l = env_l;
     const int64_t tiles = ceil_div64(rows, l == 0 ? 128 : 64) + groups;
     LHQ_SUPPORTED(tiles <= 65535, "%s: %lld row tiles exceed the grid limit", who, static_cast<long long>(tiles));
     const unsigned t = static_cast<unsigned>(tiles), b = static_cast<unsigned>(batch);
     if (l == 0) launch_mma_l<GR, SWI, 0>(a, t, b, s);
     else if (l == 1) launch_mma_l<GR, SWI, 1>(a, t, b, s);
-    else launch_mma_l<GR, SWI, 2>(a, t, b, s);
+    else if (l == 2) launch_mma_l<GR, SWI, 2>(a, t, b, s);
+    else launch_mma_l<GR, SWI, 3>(a, t, b, s);
     return check_launch(who);
 }
 
