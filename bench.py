@@ -331,7 +331,9 @@ def bench_moe_layer(ops, steps, warmup, seed=0, T=512, E=8, topk=2, H=4096, I=14
     dispatch(0)
     torch.cuda.synchronize()
     rows = (off[1:] - off[:-1]).cpu().numpy().tolist()
-    wbytes = lambda K, N: E * (K * N // 2 + (K // G) * N * 2 + (K // G) * N // 2)  # noqa: E731
+    # weights of the experts that hold rows (the kernels read no others)
+    active = sum(1 for r in rows if r > 0)
+    wbytes = lambda K, N: active * (K * N // 2 + (K // G) * N * 2 + (K // G) * N // 2)  # noqa: E731
     stages = {
         "dispatch": (dispatch, 0, T * H * 2 + S * H * 2 + T * topk * 4 * 4),
         "gate_up_swiglu": (gate_up, 2 * S * H * 2 * I, wbytes(H, 2 * I) + S * H * 2 + S * I * 2),
@@ -567,9 +569,9 @@ CONFIG2 = ((1, 4, 16), ((4096, 4096), (4096, 11008), (11008, 4096)))
 CONFIG5 = ((1, 8, 64, 4096), ((8192, 10240), (8192, 8192), (8192, 57344), (28672, 8192)))
 
 
-def moe_layer_leg(ops):
-    log("moe layer (config 4, Mixtral shapes): dispatch, gate/up + SwiGLU, down, combine")
-    r = bench_moe_layer(ops, 100, 10)
+def moe_layer_leg(ops, tokens=512):
+    log(f"moe layer (config 4, Mixtral shapes, {tokens} tokens): dispatch, gate/up + SwiGLU, down, combine")
+    r = bench_moe_layer(ops, 100, 10, T=tokens)
     for name, st in r["stages"].items():
         extra = f"  {st['tflops']:.0f} TFLOPS ({100 * st['mfma_frac']:.1f}%)" if "tflops" in st else ""
         log(f"  {name}: {st['us']:.1f} us  {st['gbs']:.0f} GB/s{extra}")
@@ -591,6 +593,8 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true", help="skip the W4A16 prefill and MoE legs")
     ap.add_argument("--only", choices=["w4a16", "w8a8", "prefill", "moe", "fp8", "configs"], default=None,
                     help="run one leg only (profiling); prints that leg's summary, not the bench line")
+    ap.add_argument("--moe-tokens", type=int, default=512,
+                    help="tokens of the --only moe leg (512 = config 4; 1-4 run the grouped decode kernel)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -629,7 +633,7 @@ def main() -> int:
         print(json.dumps({"leg": "w4a16_config5", "shapes": config_sweep(ops, "config 5", *CONFIG5)}), flush=True)
         return 0
     if args.only == "moe":
-        print(json.dumps(moe_layer_leg(ops)), flush=True)
+        print(json.dumps(moe_layer_leg(ops, args.moe_tokens)), flush=True)
         return 0
     if args.only == "prefill":
         for r in prefill_legs(ops):
