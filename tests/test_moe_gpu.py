@@ -244,6 +244,8 @@ def _swiglu_case(oracle, ops, T, E, K, H, I, G, seed, kind="uniform"):
     (5, 8, 1, 512, 72, 64, "uniform"),      # G = 64, I % 16 != 0
     (10, 16, 1, 384, 48, 32, "skewed"),     # 7 rows of one expert: two row blocks; G = 32
     (6, 12, 2, 1024, 40, 256, "dropped"),   # G = 256, ids outside [0, E) dropped
+    (4, 16, 2, 512, 72, 128, "skewed"),     # a block of 3 rows
+    (8, 16, 1, 256, 48, 64, "skewed"),      # 6 rows of one expert: blocks of 4 and 2; G = 64
 ])
 def test_grouped_swiglu(oracle, ops, T, E, K, H, I, G, kind):
     got, want = _swiglu_case(oracle, ops, T, E, K, H, I, G, 3000 + T, kind)

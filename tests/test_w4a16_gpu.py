@@ -291,6 +291,8 @@ def test_w4a16_grouped_many_groups(oracle, ops, T, E, topk, K, N):
     (8, 8, 1, 512, 200, 64),      # G = 64
     (3, 4, 1, 1024, 96, 256),     # G = 256
     (6, 12, 2, 384, 48, 32),      # G = 32, 3 K tiles
+    (2, 16, 2, 512, 200, 64),     # G = 64
+    (3, 16, 2, 1024, 96, 256),    # G = 256
 ])
 def test_w4a16_grouped_decode(oracle, ops, T, E, topk, K, N, G):
     """At most one row per group on average: the grouped decode kernel, each
