@@ -1301,11 +1301,15 @@ void allow_cu_lds() {
 }
 
 // Tuning knobs (read once; unset = heuristic):
-//   LHQ_W4_I8=-1 disables the integer decode kernel (M <= 4);
-//   LHQ_W4_DECODE=-1 disables the bf16 decode kernel;
+//   LHQ_W4_I8=-1 disables the integer decode kernel (M == 1);
+//   LHQ_W4_DECODE=-1 disables the bf16 decode kernel (plain and grouped);
 //   LHQ_W4_DEC_T (1|2), LHQ_W4_DEC_NPW (4|8 tiles per wave per pass) and
 //   LHQ_W4_DEC_S (waves per workgroup, 1..16) shape it;
-//   LHQ_W4_TILES (1|2), LHQ_W4_WAVES (1|2|4|8) shape the generic kernel.
+//   LHQ_W4_GRB (rows per block, 1..16) forces the grouped decode kernel
+//   with that row block on every grouped launch it can stage;
+//   LHQ_W4_TILES (1|2), LHQ_W4_WAVES (1|2|4|8) shape the generic kernel;
+//   LHQ_W4_MMA (0|1) and LHQ_W4_MMA_L (0..3) force the tile kernel off / on
+//   and its layout.
 int env_int(const char* name) {
     const char* v = std::getenv(name);
     return v ? std::atoi(v) : 0;
