@@ -188,7 +188,7 @@ __device__ __forceinline__ float swiglu(float g, float u) { return g / (1.0f + e
 // ---------------------------------------------------------------------------
 template <bool F32A, bool ASYM, bool F32C, int T, int WAVES, int BPS, bool GROUPED, bool SWI = false>
 __global__ __launch_bounds__(64 * WAVES) void w4_gemv_kernel(W4Args p) {
-    static_assert(!SWI || (T == 2 && !F32C), "SwiGLU pairs the two column tiles of a workgroup");
+    static_assert(!SWI || ((T == 2 || T == 4) && !F32C), "SwiGLU pairs the column tiles of a workgroup");
     constexpr int SEGS = 4 / BPS;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -280,33 +280,36 @@ __global__ __launch_bounds__(64 * WAVES) void w4_gemv_kernel(W4Args p) {
         if (r >= m_end || c >= p.N || nt0 + t >= p.Nt) return;
         w4_store<F32C>(p, z * p.c_bs + static_cast<int64_t>(r) * p.N + c, v);
     };
-    // SWI: tiles nt0 (gate) and nt0 + 1 (up) -> act column tile nt0 / 2
-    auto store_act = [&](int i, int ln, float g, float u) {
+    // SWI: tiles nt0 + 2h (gate) and nt0 + 2h + 1 (up) -> act column tile
+    // nt0 / 2 + h
+    auto store_act = [&](int h, int i, int ln, float g, float u) {
         const int r = m0 + 4 * (ln >> 4) + i;
-        const int c = static_cast<int>(blockIdx.x) * kW4TileN + (ln & 15);
+        const int c = (nt0 / 2 + h) * kW4TileN + (ln & 15);
         if (r >= m_end || c >= p.N) return;
         static_cast<uint16_t*>(p.C)[z * p.c_bs + static_cast<int64_t>(r) * p.N + c] = f32_to_bf16(swiglu(g, u));
     };
 
     if constexpr (SWI && WAVES == 1) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) store_act(i, lane, acc[0][i], acc[1][i]);
-    } else if constexpr (SWI) {
-        __shared__ float red[WAVES][2][4][64];
+        for (int h = 0; h < T / 2; ++h)
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+            for (int i = 0; i < 4; ++i) store_act(h, i, lane, acc[2 * h][i], acc[2 * h + 1][i]);
+    } else if constexpr (SWI) {
+        __shared__ float red[WAVES][T][4][64];
+#pragma unroll
+        for (int t = 0; t < T; ++t)
 #pragma unroll
             for (int i = 0; i < 4; ++i) red[wave][t][i][lane] = acc[t][i];
         __syncthreads();
-        for (int idx = threadIdx.x; idx < 4 * 64; idx += 64 * WAVES) {
-            const int i = idx >> 6, ln = idx & 63;
+        for (int idx = threadIdx.x; idx < (T / 2) * 4 * 64; idx += 64 * WAVES) {
+            const int h = idx >> 8, i = (idx >> 6) & 3, ln = idx & 63;
             float g = 0.0f, u = 0.0f;
 #pragma unroll
             for (int w = 0; w < WAVES; ++w) {
-                g += red[w][0][i][ln];
-                u += red[w][1][i][ln];
+                g += red[w][2 * h][i][ln];
+                u += red[w][2 * h + 1][i][ln];
             }
-            store_act(i, ln, g, u);
+            store_act(h, i, ln, g, u);
         }
     } else if constexpr (WAVES == 1) {
 #pragma unroll
@@ -1589,18 +1592,33 @@ int launch_w4(W4Args a, int batch, hipStream_t s, int mblocks = -1) {
         }
     }
 
-    int T = (a.Nt >= 1024) ? 2 : 1;
-    if (env_t == 1 || env_t == 2) T = env_t;
-    if constexpr (SWI) T = 2;
-    // Enough waves to cover 256 CUs several times over, but at least four
-    // K tiles per wave so each wave keeps loads in flight.  A grouped launch
-    // sizes this by the row blocks that can hold rows, ceil(rows / 16) plus
-    // one partial block per group that has rows, not by its grid bound (with
-    // a few tokens over many experts most of the grid exits at once, and
-    // measured at 2 rows over 8 experts, K=14336, N=4096: 2 waves walking 56
-    // K tiles each took 46.6 us).
+    // Column tiles per workgroup.  The 16-row kernel is bound by the vector
+    // memory path (each activation load touches 16 rows' cache lines), so a
+    // workgroup shares its activation loads across 4 column tiles (bf16)
+    // where that still leaves 512 workgroups; measured on MI355X: MoE down
+    // projection (K=14336, N=4096, 128 rows over 8 experts) 109 -> 96 us
+    // (255 us with the one tile Nt < 1024 used to get), M=8 K=8192 N=57344
+    // 61.6 -> 58.2 us; with 64-160 workgroups it lost (M=16 K=11008 N=4096
+    // 14.1 -> 27.7 us).  The SwiGLU launch also needs 8 rows per row block:
+    // with 2-3 (8-16 tokens over 8 experts) its activation loads are few and
+    // halving the workgroups cost 5-6 us.
+    // A grouped launch counts the row blocks that can hold rows, ceil(rows
+    // / 16) plus one partial block per group that has rows, not its grid
+    // bound (with a few tokens over many experts most of the grid exits at
+    // once).
     const int64_t live_blocks = GR ? std::min<int64_t>(mblocks, ceil_div(a.M, 16) + std::min(a.num_groups, a.M))
                                    : mblocks;
+    const bool t4 = !F32A && ASYM && !F32C && static_cast<int64_t>(ceil_div(a.Nt, 4)) * live_blocks * batch >= 512 &&
+                    (!SWI || a.M >= 8 * live_blocks);
+    int T = (a.Nt >= 1024) ? 2 : 1;
+    if (t4) T = 4;
+    if (env_t == 1 || env_t == 2) T = env_t;
+    if (env_t == 4 && !F32A && ASYM && !F32C) T = 4;
+    if constexpr (SWI) T = (T == 4) ? 4 : 2;
+    // Enough waves to cover 256 CUs several times over, but at least four
+    // K tiles per wave so each wave keeps loads in flight, sized by the live
+    // row blocks (measured at 2 rows over 8 experts, K=14336, N=4096: sized
+    // by the grid bound, 2 waves walking 56 K tiles each took 46.6 us).
     const int64_t wgs = static_cast<int64_t>(ceil_div(a.Nt, T)) * live_blocks * batch;
     // Also split K further while a wave would walk more than 16 K tiles:
     // the kernel does not prefetch across its K loop, so a long walk by a
@@ -1609,9 +1627,17 @@ int launch_w4(W4Args a, int batch, hipStream_t s, int mblocks = -1) {
     while (W < 8 && (wgs * W < 4096 || a.Kt > 16 * W) && a.Kt / (2 * W) >= 4) W *= 2;
     if (env_w == 1 || env_w == 2 || env_w == 4 || env_w == 8) W = env_w;
     dim3 grid(ceil_div(a.Nt, T), mblocks, batch);
-    if constexpr (SWI) launch_gemv_waves<F32A, ASYM, F32C, 2, GR, true>(a, grid, W, bps, s);
+    if constexpr (SWI) {
+        if (T == 4) launch_gemv_waves<F32A, ASYM, F32C, 4, GR, true>(a, grid, W, bps, s);
+        else launch_gemv_waves<F32A, ASYM, F32C, 2, GR, true>(a, grid, W, bps, s);
+    }
     else if (T == 1) launch_gemv_waves<F32A, ASYM, F32C, 1, GR>(a, grid, W, bps, s);
-    else launch_gemv_waves<F32A, ASYM, F32C, 2, GR>(a, grid, W, bps, s);
+    else if constexpr (!F32A && ASYM && !F32C) {
+        if (T == 4) launch_gemv_waves<F32A, ASYM, F32C, 4, GR>(a, grid, W, bps, s);
+        else launch_gemv_waves<F32A, ASYM, F32C, 2, GR>(a, grid, W, bps, s);
+    } else {
+        launch_gemv_waves<F32A, ASYM, F32C, 2, GR>(a, grid, W, bps, s);
+    }
     return check_launch("w4a16 gemv");
 }
 

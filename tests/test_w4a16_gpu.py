@@ -302,6 +302,22 @@ def test_w4a16_grouped_decode(oracle, ops, T, E, topk, K, N, G):
     assert rel_frobenius(got, want) <= TOL_BF16
 
 
+def test_w4a16_grouped_four_tiles(oracle, ops):
+    """128 rows over 8 groups at N = 4000: the 16-row kernel with four column
+    tiles per workgroup (63 x 16 row blocks >= 512 workgroups), the last
+    workgroup's tiles past Nt clamped and not stored."""
+    got, want, off = _grouped(oracle, ops, T=64, E=8, topk=2, K=256, N=4000, G=128, seed=21)
+    assert off[-1] == 128
+    assert rel_frobenius(got, want) <= TOL_BF16
+
+
+def test_w4a16_dense_four_tiles(oracle, ops):
+    """M = 16 whose rows exceed the decode kernel's LDS at N = 32776: the
+    16-row kernel with four column tiles per workgroup (513 workgroups)."""
+    got, want = _asym_case(oracle, ops, 16, 2304, 32776, 128, 23)
+    assert rel_frobenius(got, want) <= TOL_BF16
+
+
 def test_w4a16_grouped_empty_expert(oracle, ops):
     got, want, off = _grouped(oracle, ops, T=20, E=4, topk=1, K=128, N=48, G=64, seed=3, empty_expert=2)
     assert off[3] == off[2]
