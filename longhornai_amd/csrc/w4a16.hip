@@ -1592,28 +1592,30 @@ int launch_w4(W4Args a, int batch, hipStream_t s, int mblocks = -1) {
         }
     }
 
-    // Column tiles per workgroup.  The 16-row kernel is bound by the vector
-    // memory path (each activation load touches 16 rows' cache lines), so a
-    // workgroup shares its activation loads across 4 column tiles (bf16)
-    // where that still leaves 512 workgroups; measured on MI355X: MoE down
-    // projection (K=14336, N=4096, 128 rows over 8 experts) 109 -> 96 us
-    // (255 us with the one tile Nt < 1024 used to get), M=8 K=8192 N=57344
-    // 61.6 -> 58.2 us; with 64-160 workgroups it lost (M=16 K=11008 N=4096
-    // 14.1 -> 27.7 us).  The SwiGLU launch also needs 8 rows per row block:
-    // with 2-3 (8-16 tokens over 8 experts) its activation loads are few and
-    // halving the workgroups cost 5-6 us.
     // A grouped launch counts the row blocks that can hold rows, ceil(rows
     // / 16) plus one partial block per group that has rows, not its grid
     // bound (with a few tokens over many experts most of the grid exits at
     // once).
     const int64_t live_blocks = GR ? std::min<int64_t>(mblocks, ceil_div(a.M, 16) + std::min(a.num_groups, a.M))
                                    : mblocks;
-    const bool t4 = !F32A && ASYM && !F32C && static_cast<int64_t>(ceil_div(a.Nt, 4)) * live_blocks * batch >= 512 &&
-                    (!SWI || a.M >= 8 * live_blocks);
-    int T = (a.Nt >= 1024) ? 2 : 1;
-    if (t4) T = 4;
+    // Column tiles per workgroup: the most (4, 2 or 1) that leave 256
+    // workgroups.  The 16-row kernel is bound by the CU's vector memory path
+    // (each activation load touches its 16 rows' cache lines), and a
+    // workgroup shares those loads across its column tiles; below 256
+    // workgroups the lost parallelism costs more.  Four tiles are bf16
+    // only, and the SwiGLU form takes them only at 8 rows per row block (with
+    // 2-3, 8-16 tokens over 8 experts, its activation loads are few).
+    // Measured on MI355X (us, T = 1 / 2 / 4): M=8 K=28672 N=8192 46.4 / 42.8 /
+    // 61.3; M=32 K=8192 N=8192 35.9 / 23.5 / 21.3; M=16 K=11008 N=4096 13.9 /
+    // 19.7 / 27.5; M=8 K=8192 N=57344 80.5 / 61.4 / 58.5; MoE down projection
+    // at 64 tokens (K=14336, N=4096) 144 / 108 / 95.
+    const bool bf16a = !F32A && ASYM && !F32C;
+    auto wgs_t = [&](int t) { return static_cast<int64_t>(ceil_div(a.Nt, t)) * live_blocks * batch; };
+    int T = 1;
+    if (bf16a && wgs_t(4) >= 256 && (!SWI || a.M >= 8 * live_blocks)) T = 4;
+    else if (wgs_t(2) >= 256) T = 2;
     if (env_t == 1 || env_t == 2) T = env_t;
-    if (env_t == 4 && !F32A && ASYM && !F32C) T = 4;
+    if (env_t == 4 && bf16a) T = 4;
     if constexpr (SWI) T = (T == 4) ? 4 : 2;
     // Enough waves to cover 256 CUs several times over, but at least four
     // K tiles per wave so each wave keeps loads in flight, sized by the live
