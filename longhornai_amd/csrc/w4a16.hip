@@ -188,7 +188,7 @@ __device__ __forceinline__ float swiglu(float g, float u) { return g / (1.0f + e
 // ---------------------------------------------------------------------------
 template <bool F32A, bool ASYM, bool F32C, int T, int WAVES, int BPS, bool GROUPED, bool SWI = false>
 __global__ __launch_bounds__(64 * WAVES) void w4_gemv_kernel(W4Args p) {
-    static_assert(!SWI || ((T == 2 || T == 4) && !F32C), "SwiGLU pairs the column tiles of a workgroup");
+    static_assert(!SWI || ((T == 2 || T == 4 || T == 8) && !F32C), "SwiGLU pairs the column tiles of a workgroup");
     constexpr int SEGS = 4 / BPS;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1599,7 +1599,9 @@ int launch_w4(W4Args a, int batch, hipStream_t s, int mblocks = -1) {
     const int64_t live_blocks = GR ? std::min<int64_t>(mblocks, ceil_div(a.M, 16) + std::min(a.num_groups, a.M))
                                    : mblocks;
     // Column tiles per workgroup: the most (4, 2 or 1) that leave 256
-    // workgroups.  The 16-row kernel is bound by the CU's vector memory path
+    // workgroups, or 8 where 384 remain (MoE down projection at 128 tokens
+    // 146.9 -> 136.6 us, M=8 K=8192 N=57344 58.5 -> 51.9 us; at 320, 16
+    // tokens' down projection, it lost: 52.3 -> 59.1 us).  The 16-row kernel is bound by the CU's vector memory path
     // (each activation load touches its 16 rows' cache lines), and a
     // workgroup shares those loads across its column tiles; below 256
     // workgroups the lost parallelism costs more.  Four tiles are bf16
@@ -1611,12 +1613,14 @@ int launch_w4(W4Args a, int batch, hipStream_t s, int mblocks = -1) {
     // at 64 tokens (K=14336, N=4096) 144 / 108 / 95.
     const bool bf16a = !F32A && ASYM && !F32C;
     auto wgs_t = [&](int t) { return static_cast<int64_t>(ceil_div(a.Nt, t)) * live_blocks * batch; };
+    const bool rows8 = !SWI || a.M >= 8 * live_blocks;
     int T = 1;
-    if (bf16a && wgs_t(4) >= 256 && (!SWI || a.M >= 8 * live_blocks)) T = 4;
+    if (bf16a && wgs_t(8) >= 384 && rows8) T = 8;
+    else if (bf16a && wgs_t(4) >= 256 && rows8) T = 4;
     else if (wgs_t(2) >= 256) T = 2;
     if (env_t == 1 || env_t == 2) T = env_t;
-    if (env_t == 4 && bf16a) T = 4;
-    if constexpr (SWI) T = (T == 4) ? 4 : 2;
+    if ((env_t == 4 || env_t == 8) && bf16a) T = env_t;
+    if constexpr (SWI) T = (T >= 4) ? T : 2;
     // Enough waves to cover 256 CUs several times over, but at least four
     // K tiles per wave so each wave keeps loads in flight, sized by the live
     // row blocks (measured at 2 rows over 8 experts, K=14336, N=4096: sized
@@ -1630,12 +1634,14 @@ int launch_w4(W4Args a, int batch, hipStream_t s, int mblocks = -1) {
     if (env_w == 1 || env_w == 2 || env_w == 4 || env_w == 8) W = env_w;
     dim3 grid(ceil_div(a.Nt, T), mblocks, batch);
     if constexpr (SWI) {
-        if (T == 4) launch_gemv_waves<F32A, ASYM, F32C, 4, GR, true>(a, grid, W, bps, s);
+        if (T == 8) launch_gemv_waves<F32A, ASYM, F32C, 8, GR, true>(a, grid, W, bps, s);
+        else if (T == 4) launch_gemv_waves<F32A, ASYM, F32C, 4, GR, true>(a, grid, W, bps, s);
         else launch_gemv_waves<F32A, ASYM, F32C, 2, GR, true>(a, grid, W, bps, s);
     }
     else if (T == 1) launch_gemv_waves<F32A, ASYM, F32C, 1, GR>(a, grid, W, bps, s);
     else if constexpr (!F32A && ASYM && !F32C) {
-        if (T == 4) launch_gemv_waves<F32A, ASYM, F32C, 4, GR>(a, grid, W, bps, s);
+        if (T == 8) launch_gemv_waves<F32A, ASYM, F32C, 8, GR>(a, grid, W, bps, s);
+        else if (T == 4) launch_gemv_waves<F32A, ASYM, F32C, 4, GR>(a, grid, W, bps, s);
         else launch_gemv_waves<F32A, ASYM, F32C, 2, GR>(a, grid, W, bps, s);
     } else {
         launch_gemv_waves<F32A, ASYM, F32C, 2, GR>(a, grid, W, bps, s);

@@ -246,9 +246,9 @@ def _swiglu_case(oracle, ops, T, E, K, H, I, G, seed, kind="uniform"):
     (6, 12, 2, 1024, 40, 256, "dropped"),   # G = 256, ids outside [0, E) dropped
     (4, 16, 2, 512, 72, 128, "skewed"),     # a block of 3 rows
     (8, 16, 1, 256, 48, 64, "skewed"),      # 6 rows of one expert: blocks of 4 and 2; G = 64
-    # 16-row kernel with two gate / up pairs per workgroup (>= 512 workgroups);
-    # 2 x 127 tiles: the last workgroup's second pair lies past the end
-    (64, 8, 2, 256, 2024, 128, "uniform"),
+    # 16-row kernel with several gate / up pairs per workgroup
+    (64, 8, 2, 256, 2024, 128, "uniform"),  # 2 x 127 tiles, four pairs: the last workgroup's 4th lies past the end
+    (64, 8, 2, 256, 1000, 128, "uniform"),  # 2 x 63 tiles, two pairs: the last workgroup's 2nd lies past the end
 ])
 def test_grouped_swiglu(oracle, ops, T, E, K, H, I, G, kind):
     got, want = _swiglu_case(oracle, ops, T, E, K, H, I, G, 3000 + T, kind)

@@ -302,11 +302,14 @@ def test_w4a16_grouped_decode(oracle, ops, T, E, topk, K, N, G):
     assert rel_frobenius(got, want) <= TOL_BF16
 
 
-def test_w4a16_grouped_four_tiles(oracle, ops):
-    """128 rows over 8 groups at N = 4000: the 16-row kernel with four column
-    tiles per workgroup (63 x 16 row blocks >= 512 workgroups), the last
-    workgroup's tiles past Nt clamped and not stored."""
-    got, want, off = _grouped(oracle, ops, T=64, E=8, topk=2, K=256, N=4000, G=128, seed=21)
+@pytest.mark.parametrize("N", [
+    4000,   # 250 column tiles: eight per workgroup (32 x 16 row blocks >= 384)
+    1000,   # 63 column tiles: four per workgroup (16 x 16 >= 256)
+])
+def test_w4a16_grouped_wide_workgroups(oracle, ops, N):
+    """128 rows over 8 groups: the 16-row kernel with several column tiles
+    per workgroup, the last workgroup's tiles past Nt clamped and not stored."""
+    got, want, off = _grouped(oracle, ops, T=64, E=8, topk=2, K=256, N=N, G=128, seed=21)
     assert off[-1] == 128
     assert rel_frobenius(got, want) <= TOL_BF16
 
