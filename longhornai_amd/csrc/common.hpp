@@ -11,6 +11,7 @@
 #include <cstdint>
 
 #include "longhorn_hip.h"
+#include "w4layout.hpp"
 
 namespace lhq {
 
@@ -152,10 +153,6 @@ __device__ __forceinline__ int sat_rint(float v, int lim) {
 // Codes are unsigned: symmetric int4 q in [-7,7] is stored as q + 8 with an
 // implied zero point of 8.
 // ---------------------------------------------------------------------------
-constexpr int kW4TileN = 16;
-constexpr int kW4TileK = 128;
-constexpr int kW4TileBytes = 1024;
-
 __host__ __device__ inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 __host__ __device__ inline int64_t ceil_div64(int64_t a, int64_t b) { return (a + b - 1) / b; }
 

@@ -120,10 +120,6 @@ int launch_interleave(const void* a, const void* b, void* out, int64_t blk_bytes
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-bool w4_dims_ok(int K, int N, int G) {
-    return K > 0 && N > 0 && G > 0 && (K % G) == 0 && (K % 2) == 0;
-}
-
 }  // namespace
 
 }  // namespace lhq
@@ -131,21 +127,6 @@ bool w4_dims_ok(int K, int N, int G) {
 using namespace lhq;
 
 extern "C" {
-
-int64_t lhq_w4_qweight_bytes(int K, int N) {
-    if (K <= 0 || N <= 0) return 0;
-    return static_cast<int64_t>(ceil_div(N, kW4TileN)) * ceil_div(K, kW4TileK) * kW4TileBytes;
-}
-
-int64_t lhq_w4_scales_bytes(int K, int N, int G, int fp16_scales) {
-    if (!w4_dims_ok(K, N, G)) return 0;
-    return static_cast<int64_t>(ceil_div(N, kW4TileN)) * (K / G) * kW4TileN * (fp16_scales ? 2 : 4);
-}
-
-int64_t lhq_w4_zeros_bytes(int K, int N, int G) {
-    if (!w4_dims_ok(K, N, G)) return 0;
-    return static_cast<int64_t>(ceil_div(N, kW4TileN)) * ceil_div(K / G, 8) * kW4TileN * 4;
-}
 
 int lhq_w4_prepack_sym(const uint8_t* packed, const float* scales, int K, int N, int G,
                        uint8_t* qweight, float* scales_out, void* stream) {

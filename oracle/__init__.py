@@ -21,7 +21,9 @@ import os
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-ORACLE_SO = os.path.join(_HERE, "liboracle.so")
+# LHO_ORACLE_SO selects another build of the same restatement (the
+# sanitizer build, oracle/_asan/liboracle.so).
+ORACLE_SO = os.environ.get("LHO_ORACLE_SO") or os.path.join(_HERE, "liboracle.so")
 REF_SO = os.path.join(_HERE, "_ref", "libref.so")
 
 _f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
@@ -65,6 +67,7 @@ _COMMON = {
     "gemm_ref": (None, [_f32p, _f32p, _f32p, _i, _i, _i, _f, _f]),
     "gemm": (None, [_f32p, _f32p, _f32p, _i, _i, _i, _f, _f]),
     "gemm_batched": (None, [_f32p, _f32p, _f32p, _i, _i, _i, _i, _f, _f]),
+    "gemm_grouped": (None, [C.c_void_p, C.c_void_p, C.c_void_p, _i32p, _i32p, _i32p, _i, _f, _f]),
 }
 _COMMON.update({
     "f32_to_f16_n": (None, [_f32p, _u16p, _i64]),
@@ -288,6 +291,20 @@ class _Checker:
         self.fn["gemm_batched"](_c(A, np.float32), _c(B, np.float32), Cout, b, M, N, K,
                                 alpha, beta)
         return Cout
+
+    def gemm_grouped(self, As, Bs, C0s=None, alpha=1.0, beta=0.0):
+        """Ragged pointer-array groups (gemm.cpp:69-75): one fp32 GEMM per
+        (As[g], Bs[g]) pair; returns the list of outputs."""
+        As = [_c(a, np.float32) for a in As]
+        Bs = [_c(b, np.float32) for b in Bs]
+        Cs = [np.zeros((a.shape[0], b.shape[1]), np.float32) if C0s is None else _c(c, np.float32).copy()
+              for a, b, c in zip(As, Bs, C0s if C0s is not None else [None] * len(As))]
+        ptrs = lambda xs: (C.c_void_p * len(xs))(*[x.ctypes.data for x in xs])  # noqa: E731
+        M = np.array([a.shape[0] for a in As], np.int32)
+        K = np.array([a.shape[1] for a in As], np.int32)
+        N = np.array([b.shape[1] for b in Bs], np.int32)
+        self.fn["gemm_grouped"](ptrs(As), ptrs(Bs), ptrs(Cs), M, N, K, len(As), alpha, beta)
+        return Cs
 
 
 class Oracle(_Checker):

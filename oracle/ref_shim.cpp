@@ -90,6 +90,10 @@ void ref_gemm_batched(const float* A, const float* B, float* C, int batch, int M
                       float alpha, float beta) {
     lh::gemm_batched(A, B, C, batch, M, N, K, alpha, beta);
 }
+void ref_gemm_grouped(const float* const* A, const float* const* B, float* const* C, const int* M,
+                      const int* N, const int* K, int groups, float alpha, float beta) {
+    lh::gemm_grouped(A, B, C, M, N, K, groups, alpha, beta);
+}
 
 static lh::MoEConfig moe_cfg(int T, int H, int I, int E, int K) {
     lh::MoEConfig c;

@@ -32,6 +32,9 @@ void lho_gemm_w4a16_groupwise(const float*, const uint8_t*, const float*, float*
 void lho_gemm_fp8_e4m3(const uint8_t*, const uint8_t*, float, float, float*, int, int, int, float, float);
 void lho_gemm_ref(const float*, const float*, float*, int, int, int, float, float);
 void lho_gemm(const float*, const float*, float*, int, int, int, float, float);
+void lho_gemm_batched(const float*, const float*, float*, int, int, int, int, float, float);
+void lho_gemm_grouped(const float* const*, const float* const*, float* const*, const int*, const int*, const int*, int,
+                      float, float);
 void lho_moe_dispatch(const void*, int64_t, const int32_t*, int, int, int, int32_t*, int32_t*, int32_t*, int32_t*,
                       void*);
 void lho_moe_combine_f32(const float*, const int32_t*, const int32_t*, const float*, float*, int, int, int);

@@ -1,8 +1,7 @@
-// lh:: storage types (host-side conversions of the drop-in dtypes.hpp): the
-// reference suite's checks (tests/test_dtypes.cpp:11-88) and bit-exact
-// agreement with the oracle -- exhaustive for every 16- and 8-bit decode,
-// and for encodes over every fp32 bit pattern with a stride, plus all fp32
-// values near each format's rounding boundaries.
+// lh:: storage types (host-side conversions of the drop-in dtypes.hpp):
+// bit-exact agreement with the oracle -- exhaustive for every 16- and 8-bit
+// decode, and for encodes over every fp32 bit pattern with a stride, plus all
+// fp32 values near each format's rounding boundaries.
 #include <gtest/gtest.h>
 
 #include <cmath>
@@ -19,66 +18,6 @@ using lh::bfloat16;
 using lh::fp8_e4m3;
 using lh::fp8_e5m2;
 using lh::half;
-
-TEST(Dtypes, HalfRoundTrip) {
-    for (float v : lh_test::random_vector(4096, 1, -100.0f, 100.0f))
-        EXPECT_LE(std::fabs(static_cast<float>(half(v)) - v), 1e-3f * std::fabs(v) + 1e-4f) << "v=" << v;
-}
-
-TEST(Dtypes, Bf16RoundTrip) {
-    for (float v : lh_test::random_vector(4096, 2, -100.0f, 100.0f))
-        EXPECT_LE(std::fabs(static_cast<float>(bfloat16(v)) - v), 8e-3f * std::fabs(v) + 1e-4f) << "v=" << v;
-}
-
-TEST(Dtypes, HalfSpecialValues) {
-    EXPECT_EQ(static_cast<float>(half(0.0f)), 0.0f);
-    EXPECT_EQ(static_cast<float>(half(1.0f)), 1.0f);
-    EXPECT_EQ(static_cast<float>(half(-2.0f)), -2.0f);
-    EXPECT_TRUE(std::isinf(static_cast<float>(half(70000.0f))));
-}
-
-TEST(Dtypes, Bf16ExactForFloatPrefix) {
-    EXPECT_EQ(static_cast<float>(bfloat16(0.5f)), 0.5f);
-    EXPECT_EQ(static_cast<float>(bfloat16(256.0f)), 256.0f);
-    EXPECT_EQ(static_cast<float>(bfloat16(-1.0f)), -1.0f);
-}
-
-TEST(Dtypes, Fp8E4m3RoundTrip) {
-    int saturated = 0;
-    for (float v : lh_test::random_vector(2048, 30, -100.0f, 100.0f)) {
-        const float r = static_cast<float>(fp8_e4m3(v));
-        if (std::fabs(r) >= 448.0f) {
-            ++saturated;
-            continue;
-        }
-        EXPECT_LE(std::fabs(r - v), 0.13f * std::fabs(v) + 1e-3f) << "v=" << v;
-    }
-    EXPECT_LT(saturated, 100);
-}
-
-TEST(Dtypes, Fp8E4m3ExactForRepresentablePowers) {
-    EXPECT_EQ(static_cast<float>(fp8_e4m3(0.0f)), 0.0f);
-    EXPECT_EQ(static_cast<float>(fp8_e4m3(1.0f)), 1.0f);
-    EXPECT_EQ(static_cast<float>(fp8_e4m3(2.0f)), 2.0f);
-    EXPECT_EQ(static_cast<float>(fp8_e4m3(-4.0f)), -4.0f);
-    EXPECT_EQ(static_cast<float>(fp8_e4m3(0.5f)), 0.5f);
-    EXPECT_EQ(static_cast<float>(fp8_e4m3(1000.0f)), 448.0f);
-    EXPECT_EQ(static_cast<float>(fp8_e4m3(-1000.0f)), -448.0f);
-}
-
-TEST(Dtypes, Fp8E5m2RoundTrip) {
-    for (float v : lh_test::random_vector(2048, 31, -100.0f, 100.0f))
-        EXPECT_LE(std::fabs(static_cast<float>(fp8_e5m2(v)) - v), 0.27f * std::fabs(v) + 1e-3f) << "v=" << v;
-}
-
-TEST(Dtypes, Fp8E5m2ExactForPowers) {
-    EXPECT_EQ(static_cast<float>(fp8_e5m2(1.0f)), 1.0f);
-    EXPECT_EQ(static_cast<float>(fp8_e5m2(8.0f)), 8.0f);
-    EXPECT_EQ(static_cast<float>(fp8_e5m2(-32.0f)), -32.0f);
-    EXPECT_TRUE(std::isinf(static_cast<float>(fp8_e5m2(1.0e6f))));
-}
-
-// ---- bit-exact agreement with the oracle ----------------------------------
 
 namespace {
 uint32_t fbits(float f) {

@@ -1,5 +1,4 @@
 // test_moe.cpp -- lh::moe_dispatch / lh::moe_combine (the drop-in, on the GPU)
-// against the reference's own expectations (tests/test_moe.cpp:131-170) and
 // bit for bit against the oracle's restatement of moe.cpp:102-221.
 #include <gtest/gtest.h>
 
@@ -38,29 +37,11 @@ std::vector<int32_t> routing(int T, int E, int K, uint32_t seed) {
 
 }  // namespace
 
-// The reference's dispatch test (test_moe.cpp:131-170), unchanged in intent.
-TEST(MoE, DispatchProducesValidLayoutAndPreservesContent) {
-    constexpr int T = 6, H = 4, E = 3, K = 2;
-    auto hidden = lh_test::random_vector(T * H, 6100);
-    std::vector<int32_t> ids = {0, 1, 2, 0, 1, 2, 0, 1, 2, 1, 0, 2};
-    const auto cfg = config(T, H, E, K);
-    std::vector<int32_t> offsets(E + 1, 0), tok(T * K), slot(T * K);
-    std::vector<float> dispatched(T * K * H);
-    lh::moe_dispatch(hidden.data(), ids.data(), offsets.data(), tok.data(), slot.data(), dispatched.data(), cfg);
-    EXPECT_EQ(offsets[E], T * K);
-    std::vector<int> expected_counts(E, 0);
-    for (int s : ids) ++expected_counts[s];
-    for (int e = 0; e < E; ++e) EXPECT_EQ(offsets[e + 1] - offsets[e], expected_counts[e]);
-    // each dispatched row is a copy of its source token's hidden state
-    for (int s = 0; s < T * K; ++s)
-        for (int i = 0; i < H; ++i) EXPECT_EQ(dispatched[s * H + i], hidden[tok[s] * H + i]);
-}
-
 TEST(MoEParity, DispatchBitExactVsOracle) {
     const int shapes[][4] = {{100, 64, 8, 2}, {37, 5, 16, 4}, {1, 8, 4, 1}, {513, 128, 64, 6}};
     for (const auto& sh : shapes) {
         const int T = sh[0], H = sh[1], E = sh[2], K = sh[3];
-        auto hidden = lh_test::random_vector(T * H, 7000 + T);
+        auto hidden = lh_test::uniform(T * H, 7000 + T);
         auto ids = routing(T, E, K, 7100 + T);
         std::vector<int32_t> off(E + 1), tok(T * K), slot(T * K), woff(E + 1), wtok(T * K), wslot(T * K), wpos(T * K);
         std::vector<float> out(static_cast<size_t>(T) * K * H), want(out.size());
@@ -82,8 +63,8 @@ TEST(MoEParity, CombineBitExactVsOracle) {
         auto ids = routing(T, E, K, 8000 + T);
         std::vector<int32_t> off(E + 1), tok(T * K), slot(T * K), pos(T * K);
         lho_moe_dispatch(nullptr, 0, ids.data(), T, K, E, off.data(), tok.data(), slot.data(), pos.data(), nullptr);
-        auto y = lh_test::random_vector(T * K * H, 8100 + T);
-        auto gates = lh_test::random_vector(T * K, 8200 + T);
+        auto y = lh_test::uniform(T * K * H, 8100 + T);
+        auto gates = lh_test::uniform(T * K, 8200 + T);
         std::vector<float> got(static_cast<size_t>(T) * H), want(got.size());
         lh::moe_combine(y.data(), off.data(), tok.data(), slot.data(), gates.data(), got.data(), config(T, H, E, K));
         lho_moe_combine_f32(y.data(), tok.data(), slot.data(), gates.data(), want.data(), T, H, K);
@@ -94,7 +75,7 @@ TEST(MoEParity, CombineBitExactVsOracle) {
 // dispatch -> identity experts -> combine: each token gets sum_k gate_k * x
 TEST(MoE, DispatchThenCombineRestoresWeightedTokens) {
     constexpr int T = 64, H = 32, E = 8, K = 2;
-    auto hidden = lh_test::random_vector(T * H, 9000);
+    auto hidden = lh_test::uniform(T * H, 9000);
     auto ids = routing(T, E, K, 9001);
     std::vector<float> gates(T * K, 0.5f);  // 0.5 x + 0.5 x == x exactly
     const auto cfg = config(T, H, E, K);

@@ -1,6 +1,5 @@
-// Quantizers through the lh:: drop-in (GPU): the reference suite's checks
-// (tests/test_quant.cpp:10-130, same names, seeds and bounds) and bit-exact
-// parity with the CPU oracle's restatement of quant.cpp.
+// Quantizers through the lh:: drop-in (GPU): bit-exact parity with the CPU
+// oracle's restatement of quant.cpp (quant.cpp:34-249) at every scope.
 #include <gtest/gtest.h>
 
 #include <cmath>
@@ -13,108 +12,10 @@
 
 using lh_test::BitEqual;
 
-TEST(Quant, Q8PerTensorRoundTrip) {
-    auto x = lh_test::random_vector(1024, 4000, -3.0f, 3.0f);
-    std::vector<int8_t> q(x.size());
-    float scale = 0.0f;
-    lh::q8_quantize_per_tensor(x.data(), q.data(), &scale, x.size());
-    std::vector<float> d(x.size());
-    lh::q8_dequantize_per_tensor(q.data(), scale, d.data(), x.size());
-    for (size_t i = 0; i < x.size(); ++i) EXPECT_LT(std::fabs(d[i] - x[i]), scale + 1e-6f) << "i=" << i;
-}
-
-TEST(Quant, Q8PerRowFollowsRowScale) {
-    constexpr int rows = 8, dim = 64;
-    std::vector<float> x(rows * dim);
-    for (int r = 0; r < rows; ++r) {
-        const float mag = (r == 0) ? 0.01f : (r == rows - 1 ? 100.0f : 1.0f);
-        auto row = lh_test::random_vector(dim, static_cast<uint32_t>(4100 + r), -mag, mag);
-        for (int i = 0; i < dim; ++i) x[r * dim + i] = row[i];
-    }
-    std::vector<int8_t> q(x.size());
-    std::vector<float> scales(rows), d(x.size());
-    lh::q8_quantize_per_row(x.data(), q.data(), scales.data(), rows, dim);
-    lh::q8_dequantize_per_row(q.data(), scales.data(), d.data(), rows, dim);
-    for (int r = 0; r < rows; ++r)
-        for (int i = 0; i < dim; ++i)
-            EXPECT_LT(std::fabs(d[r * dim + i] - x[r * dim + i]), scales[r] + 1e-6f);
-}
-
-TEST(Quant, Q8PerColRoundTrip) {
-    constexpr int rows = 16, cols = 32;
-    auto x = lh_test::random_vector(rows * cols, 4200, -1.0f, 1.0f);
-    std::vector<int8_t> q(x.size());
-    std::vector<float> scales(cols), d(x.size());
-    lh::q8_quantize_per_col(x.data(), q.data(), scales.data(), rows, cols);
-    lh::q8_dequantize_per_col(q.data(), scales.data(), d.data(), rows, cols);
-    for (int c = 0; c < cols; ++c) {
-        EXPECT_GT(scales[c], 0.0f);
-        for (int r = 0; r < rows; ++r) EXPECT_LT(std::fabs(d[r * cols + c] - x[r * cols + c]), scales[c] + 1e-6f);
-    }
-}
-
-TEST(Quant, Q4GroupwiseRoundTripBoundedByScale) {
-    constexpr int K = 64, N = 16, G = 32;
-    auto x = lh_test::random_vector(K * N, 4300, -1.0f, 1.0f);
-    std::vector<uint8_t> packed(K * N / 2);
-    std::vector<float> scales((K / G) * N), d(K * N);
-    lh::q4_quantize_groupwise(x.data(), packed.data(), scales.data(), K, N, G);
-    lh::q4_dequantize_groupwise(packed.data(), scales.data(), d.data(), K, N, G);
-    for (int k = 0; k < K; ++k)
-        for (int n = 0; n < N; ++n)
-            EXPECT_LT(std::fabs(d[k * N + n] - x[k * N + n]), scales[(k / G) * N + n] + 1e-6f);
-}
-
-TEST(Quant, Q4GetMatchesDequantize) {
-    constexpr int K = 8, N = 4, G = 4;
-    auto x = lh_test::random_vector(K * N, 4400, -1.0f, 1.0f);
-    std::vector<uint8_t> packed(K * N / 2);
-    std::vector<float> scales((K / G) * N), d(K * N);
-    lh::q4_quantize_groupwise(x.data(), packed.data(), scales.data(), K, N, G);
-    lh::q4_dequantize_groupwise(packed.data(), scales.data(), d.data(), K, N, G);
-    for (int k = 0; k < K; ++k)
-        for (int n = 0; n < N; ++n) {
-            const int8_t got = lh::q4_get(packed.data(), k, n, N);
-            EXPECT_GE(got, -7);
-            EXPECT_LE(got, 7);
-            // and the dequantized value is exactly that code times its scale
-            EXPECT_EQ(d[k * N + n], static_cast<float>(got) * scales[(k / G) * N + n]);
-        }
-}
-
-TEST(Quant, Fp8PerTensorRoundTrip) {
-    auto x = lh_test::random_vector(1024, 4500, -2.0f, 2.0f);
-    std::vector<lh::fp8_e4m3> q(x.size());
-    float scale = 0.0f;
-    lh::fp8_quantize_per_tensor(x.data(), q.data(), &scale, x.size());
-    std::vector<float> d(x.size());
-    lh::fp8_dequantize_per_tensor(q.data(), scale, d.data(), x.size());
-    for (size_t i = 0; i < x.size(); ++i) EXPECT_LT(std::fabs(d[i] - x[i]), 0.13f * std::fabs(x[i]) + scale);
-}
-
-TEST(Quant, Fp8PerRowFollowsRowScale) {
-    constexpr int rows = 4, dim = 32;
-    std::vector<float> x(rows * dim);
-    for (int r = 0; r < rows; ++r) {
-        const float mag = (r == 0) ? 0.001f : 50.0f;
-        auto row = lh_test::random_vector(dim, static_cast<uint32_t>(4600 + r), -mag, mag);
-        for (int i = 0; i < dim; ++i) x[r * dim + i] = row[i];
-    }
-    std::vector<lh::fp8_e4m3> q(x.size());
-    std::vector<float> scales(rows), d(x.size());
-    lh::fp8_quantize_per_row(x.data(), q.data(), scales.data(), rows, dim);
-    lh::fp8_dequantize_per_row(q.data(), scales.data(), d.data(), rows, dim);
-    for (int r = 0; r < rows; ++r)
-        for (int i = 0; i < dim; ++i)
-            EXPECT_LT(std::fabs(d[r * dim + i] - x[r * dim + i]), 0.13f * std::fabs(x[r * dim + i]) + scales[r]);
-}
-
-// ---- bit-exact parity with the oracle (quant.cpp semantics) ---------------
-
 namespace {
 std::vector<float> spiky(int rows, int cols, uint32_t seed) {
     // wide magnitudes, exact zeros, a zero row and +-127 ties (x*inv = k+0.5)
-    auto x = lh_test::random_vector(static_cast<int64_t>(rows) * cols, seed, -4.0f, 4.0f);
+    auto x = lh_test::uniform(static_cast<int64_t>(rows) * cols, seed, -4.0f, 4.0f);
     for (int c = 0; c < cols; ++c) x[c] = 0.0f;                       // all-zero first row
     for (size_t i = 7; i < x.size(); i += 13) x[i] *= 1000.0f;        // outliers
     for (size_t i = 5; i < x.size(); i += 17) x[i] = 0.0f;

@@ -1,7 +1,5 @@
-// test_util.hpp -- seeded inputs and comparators for the C++ suites; the
-// same helpers the reference suites use (lh_test::random_vector, random_ids,
-// AllClose; tests/test_util.hpp:17-57), plus the relative Frobenius error
-// the parity bounds are stated in.
+// test_util.hpp -- seeded inputs and comparators for the project's C++
+// parity suites over the lh:: drop-in.
 #ifndef LONGHORN_TESTS_TEST_UTIL_HPP
 #define LONGHORN_TESTS_TEST_UTIL_HPP
 
@@ -10,44 +8,37 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
-#include <random>
 #include <vector>
 
 namespace lh_test {
 
-constexpr float kAtolF32 = 1e-4f;
-constexpr float kRtolF32 = 1e-4f;
+// splitmix64 (Steele, Lea and Flood, "Fast splittable pseudorandom number
+// generators", 2014): a 64-bit counter-based stream, identical on every
+// platform, so a seed names the same inputs everywhere.
+inline uint64_t splitmix64(uint64_t& state) {
+    uint64_t z = (state += 0x9e3779b97f4a7c15ull);
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
 
-// Uniform floats in [lo, hi) from a 32-bit Mersenne twister with `seed`.
-inline std::vector<float> random_vector(int64_t n, uint32_t seed, float lo = -1.0f, float hi = 1.0f) {
-    std::mt19937 gen(seed);
-    std::uniform_real_distribution<float> u(lo, hi);
+// n floats uniform in [lo, hi): the top 24 bits of each draw scaled to [0, 1).
+inline std::vector<float> uniform(int64_t n, uint64_t seed, float lo = -1.0f, float hi = 1.0f) {
+    uint64_t st = seed * 0x2545f4914f6cdd1dull + 1;
     std::vector<float> out(static_cast<size_t>(n));
-    for (float& v : out) v = u(gen);
-    return out;
-}
-
-inline std::vector<int32_t> random_ids(int64_t n, int32_t vocab, uint32_t seed) {
-    std::mt19937 gen(seed);
-    std::uniform_int_distribution<int32_t> u(0, vocab - 1);
-    std::vector<int32_t> out(static_cast<size_t>(n));
-    for (int32_t& v : out) v = u(gen);
-    return out;
-}
-
-// |a - b| <= atol + rtol*|b| everywhere (NaN fails).
-inline ::testing::AssertionResult AllClose(const std::vector<float>& a, const std::vector<float>& b,
-                                           float atol = kAtolF32, float rtol = kRtolF32) {
-    if (a.size() != b.size())
-        return ::testing::AssertionFailure() << "size mismatch: " << a.size() << " vs " << b.size();
-    for (size_t i = 0; i < a.size(); ++i) {
-        const float d = std::fabs(a[i] - b[i]);
-        const float tol = atol + rtol * std::fabs(b[i]);
-        if (!(d <= tol))
-            return ::testing::AssertionFailure() << "mismatch at index " << i << ": " << a[i] << " vs " << b[i]
-                                                 << " (|diff|=" << d << ", tol=" << tol << ")";
+    for (float& v : out) {
+        const float u = static_cast<float>(splitmix64(st) >> 40) * (1.0f / 16777216.0f);
+        v = lo + (hi - lo) * u;
     }
-    return ::testing::AssertionSuccess();
+    return out;
+}
+
+// n ints uniform in [0, bound).
+inline std::vector<int32_t> uniform_ids(int64_t n, int32_t bound, uint64_t seed) {
+    uint64_t st = seed ^ 0x5851f42d4c957f2dull;
+    std::vector<int32_t> out(static_cast<size_t>(n));
+    for (int32_t& v : out) v = static_cast<int32_t>(splitmix64(st) % static_cast<uint64_t>(bound));
+    return out;
 }
 
 // Relative Frobenius error ||got - want|| / ||want||, in double.

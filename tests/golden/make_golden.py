@@ -126,6 +126,49 @@ def main() -> None:
     d["gb_A"], d["gb_B"] = Ab, Bb
     d["gemm_batched"] = r.gemm_batched(Ab, Bb, None, 1.0, 0.0)
 
+    # -- dequantizers (quant.cpp:47-50,65-73,98-105 and the fp8 forms) --------
+    for kind in ("q8", "fp8"):
+        d[f"{kind}_row_deq"] = getattr(r, f"{kind}_dequantize_per_row")(d[f"{kind}_row_q"], d[f"{kind}_row_s"])
+        d[f"{kind}_col_deq"] = getattr(r, f"{kind}_dequantize_per_col")(d[f"{kind}_col_q"], d[f"{kind}_col_s"])
+        d[f"{kind}_tensor_deq"] = getattr(r, f"{kind}_dequantize_per_tensor")(
+            d[f"{kind}_tensor_q"], float(d[f"{kind}_tensor_s"]))
+
+    # -- per-token int8 of bf16 rows (config 3's activations): the reference's
+    # q8_quantize_per_row (quant.cpp:52-63) on the exact fp32 widening ---------
+    g2 = np.random.default_rng(8)
+    xb = g2.standard_normal((9, 256)).astype(np.float32)
+    xb[0] = 0.0                                             # all-zero row: scale 1
+    xb[1] = g2.uniform(-100, 100, 256).astype(np.float32)   # max 127: scale 1, exact ties
+    xb[1, :9] = [127.0, 0.5, 1.5, 2.5, -2.5, 63.5, -63.5, -0.5, 126.5]
+    xb[2, [7, 100, 201]] = [20.0, -20.0, 20.0]              # +-20 outliers
+    xb[3, 5] = np.nan                                       # NaN never wins the max
+    xb[4, 17] = -20.0                                       # negative peak
+    xb[5] *= 1e-3
+    xb[6] *= 1e4
+    for row in (7, 8):
+        xb[row, g2.integers(0, 256)] = 20.0 if row == 7 else -20.0
+    bits = r.f32_to_bf16_n(xb)
+    d["q8bf_x"] = bits
+    d["q8bf_q"], d["q8bf_s"] = r.q8_quantize_per_row((bits.astype(np.uint32) << 16).view(np.float32))
+
+    # -- the W8A8 epilogue with alpha = 1, beta = 0, rounded to bf16 by the
+    # reference's own rule (gemm_quant.cpp:29-49, dtypes.hpp:87-98) -----------
+    Aq3, As3 = r.q8_quantize_per_row(g2.standard_normal((16, 96)).astype(np.float32))
+    Bq3, Bs3 = r.q8_quantize_per_col((g2.standard_normal((96, 40)) * 0.02).astype(np.float32))
+    d["w8bf_Aq"], d["w8bf_As"], d["w8bf_Bq"], d["w8bf_Bs"] = Aq3, As3, Bq3, Bs3
+    d["w8bf_C"] = r.f32_to_bf16_n(r.gemm_w8a8(Aq3, Bq3, As3, Bs3, None, 1.0, 0.0))
+
+    # -- ragged pointer-array groups (gemm.cpp:69-75), alpha/beta applied -----
+    dims = [(8, 6, 7), (5, 9, 4), (1, 13, 3)]
+    for i, (m, k, n) in enumerate(dims):
+        d[f"gg_A{i}"] = g2.uniform(-1, 1, (m, k)).astype(np.float32)
+        d[f"gg_B{i}"] = g2.uniform(-1, 1, (k, n)).astype(np.float32)
+        d[f"gg_C0{i}"] = g2.uniform(-1, 1, (m, n)).astype(np.float32)
+    outs = r.gemm_grouped([d[f"gg_A{i}"] for i in range(3)], [d[f"gg_B{i}"] for i in range(3)],
+                          [d[f"gg_C0{i}"] for i in range(3)], 0.75, -1.25)
+    for i, c in enumerate(outs):
+        d[f"gg_C{i}"] = c
+
     np.savez_compressed(OUT, **d)
     print(f"wrote {OUT} ({os.path.getsize(OUT)} bytes, {len(d)} arrays)")
 

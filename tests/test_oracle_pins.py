@@ -391,3 +391,288 @@ def test_grouped_equals_per_group_calls(o):
     for e in range(E):
         sub = o.gemm_w4a16_asym(A[off[e]:off[e + 1]], Ps[e], Ss[e], Zs[e], N, G)
         assert same(got[off[e]:off[e + 1]], sub)
+
+
+# ---------------------------------------------------------------------------
+# 4. the bf16 per-token quantizer, the bf16 W8A8 epilogue, the dequantizers
+#    and the ragged group driver: golden vectors, the compiled reference and
+#    closed forms
+# ---------------------------------------------------------------------------
+
+def test_golden_dequantizers(o, g):
+    for kind in ("q8", "fp8"):
+        assert same(getattr(o, f"{kind}_dequantize_per_row")(g[f"{kind}_row_q"], g[f"{kind}_row_s"]),
+                    g[f"{kind}_row_deq"])
+        assert same(getattr(o, f"{kind}_dequantize_per_col")(g[f"{kind}_col_q"], g[f"{kind}_col_s"]),
+                    g[f"{kind}_col_deq"])
+        assert same(getattr(o, f"{kind}_dequantize_per_tensor")(g[f"{kind}_tensor_q"], float(g[f"{kind}_tensor_s"])),
+                    g[f"{kind}_tensor_deq"])
+
+
+def test_golden_q8_per_row_bf16(o, g):
+    """quant.cpp:52-63 on the fp32 widening of bf16 rows: zero row, exact ties
+    at scale 1, +-20 outliers, a NaN, a negative peak, tiny and huge rows."""
+    q, s = o.q8_quantize_per_row_bf16(g["q8bf_x"])
+    assert same(q, g["q8bf_q"]) and same(s, g["q8bf_s"])
+    assert g["q8bf_s"][0] == 1.0 and g["q8bf_s"][1] == 1.0
+    assert g["q8bf_q"][1, :9].tolist() == [127, 0, 2, 2, -2, 64, -64, 0, 126]
+
+
+def test_golden_w8a8_bf16out(o, g):
+    got = o.gemm_w8a8_bf16out(g["w8bf_Aq"], g["w8bf_Bq"], g["w8bf_As"], g["w8bf_Bs"])
+    assert np.array_equal(got, g["w8bf_C"])
+
+
+def test_golden_gemm_grouped(o, g):
+    outs = o.gemm_grouped([g[f"gg_A{i}"] for i in range(3)], [g[f"gg_B{i}"] for i in range(3)],
+                          [g[f"gg_C0{i}"] for i in range(3)], 0.75, -1.25)
+    for i, c in enumerate(outs):
+        assert same(c, g[f"gg_C{i}"])
+
+
+def _bf16_rows(gen, rows, dim):
+    """bf16 bit patterns of per-token rows in the shape of config 3's
+    activations: N(0,1) with 0.1% of entries at +-20, plus one row of exact
+    ties at scale 1, one all-zero row and one holding a NaN."""
+    x = gen.standard_normal((rows, dim)).astype(np.float32)
+    n_out = max(1, int(0.001 * x.size))
+    pos = gen.choice(x.size, n_out, replace=False)
+    x.ravel()[pos] = np.where(gen.random(n_out) < 0.5, -20.0, 20.0)
+    x[0] = 0.0
+    x[1] = np.round(gen.uniform(-126, 126, dim) * 2) / 2      # halves: ties at scale 1
+    x[1, 0] = 127.0
+    x[2, dim // 2] = np.nan
+    return (x.view(np.uint32) >> 16).astype(np.uint16)
+
+
+@need_ref
+@pytest.mark.parametrize("seed", range(3))
+def test_ref_q8_per_row_bf16_and_bf16_epilogue(o, seed):
+    r = Ref()
+    gen = np.random.default_rng(300 + seed)
+    xb = _bf16_rows(gen, 24, int(gen.integers(64, 700)))
+    q, s = o.q8_quantize_per_row_bf16(xb)
+    qr, sr = r.q8_quantize_per_row(D.bf16_bits_to_f32(xb))
+    assert same(q, qr) and same(s, sr)
+    K, N = xb.shape[1], int(gen.integers(1, 90))
+    Bq, Bs = r.q8_quantize_per_col((gen.standard_normal((K, N)) * 0.02).astype(np.float32))
+    want = r.f32_to_bf16_n(r.gemm_w8a8(qr, Bq, sr, Bs, None, 1.0, 0.0))
+    assert np.array_equal(o.gemm_w8a8_bf16out(q, Bq, s, Bs), want)
+
+
+@need_ref
+@pytest.mark.parametrize("seed", range(3))
+def test_ref_dequantizers_and_grouped(o, seed):
+    r = Ref()
+    gen = np.random.default_rng(400 + seed)
+    x = (gen.standard_normal((int(gen.integers(1, 30)), int(gen.integers(1, 50)))) * 10).astype(np.float32)
+    for kind in ("q8", "fp8"):
+        q, s = getattr(r, f"{kind}_quantize_per_row")(x)
+        assert same(getattr(o, f"{kind}_dequantize_per_row")(q, s), getattr(r, f"{kind}_dequantize_per_row")(q, s))
+        q, s = getattr(r, f"{kind}_quantize_per_col")(x)
+        assert same(getattr(o, f"{kind}_dequantize_per_col")(q, s), getattr(r, f"{kind}_dequantize_per_col")(q, s))
+        q, s = getattr(r, f"{kind}_quantize_per_tensor")(x)
+        assert same(getattr(o, f"{kind}_dequantize_per_tensor")(q, s),
+                    getattr(r, f"{kind}_dequantize_per_tensor")(q, s))
+    dims = [tuple(int(v) for v in gen.integers(0, 20, 3)) for _ in range(4)]
+    As = [gen.uniform(-1, 1, (m, k)).astype(np.float32) for m, k, _ in dims]
+    Bs = [gen.uniform(-1, 1, (k, n)).astype(np.float32) for _, k, n in dims]
+    Cs = [gen.uniform(-1, 1, (m, n)).astype(np.float32) for m, _, n in dims]
+    al, be = float(gen.uniform(-2, 2)), float(gen.choice([0.0, 1.0, 0.5]))
+    for u, v in zip(o.gemm_grouped(As, Bs, Cs, al, be), r.gemm_grouped(As, Bs, Cs, al, be)):
+        assert same(u, v)
+
+
+def _bf16_recip_vs_div_case():
+    """bf16 x, m with rint(x * (1/(m/127))) != rint(x / (m/127)) in fp32."""
+    for mb in range(0x3f00, 0x4000):                    # m in [0.5, 2)
+        m = np.uint32(mb << 16).view(np.float32)
+        s = np.float32(m / np.float32(127))
+        inv = np.float32(np.float32(1) / s)
+        for xb in range(0x3c00, mb):                    # 0 < x < m
+            x = np.uint32(xb << 16).view(np.float32)
+            if np.rint(np.float32(x * inv)) != np.rint(np.float32(x / s)):
+                return x, m
+    raise AssertionError("no distinguishing case found")
+
+
+def test_q8_per_row_bf16_closed_forms(o):
+    """The bf16 per-token quantizer: scale = max|x|/127 (1 for an all-zero
+    row), q = rint(x * (1/scale)) -- the reciprocal multiply of
+    quant.cpp:57-58, not a division, on a case where the two differ -- ties
+    to even, NaN never the max, and equal to the fp32 per-row quantizer on
+    the exact widening."""
+    x, m = _bf16_recip_vs_div_case()
+    row = np.array([[m, x, -x]], np.float32)
+    xb = (row.view(np.uint32) >> 16).astype(np.uint16)
+    q, s = o.q8_quantize_per_row_bf16(xb)
+    scale = np.float32(m / np.float32(127))
+    inv = np.float32(np.float32(1) / scale)
+    assert s[0] == scale and q[0, 0] == 127
+    assert q[0, 1] == np.rint(np.float32(x * inv)) != np.rint(np.float32(x / scale))
+    assert q[0, 2] == -q[0, 1]
+    ties = np.array([[127.0, 0.5, 1.5, 2.5, -0.5, -1.5, 126.5, np.nan, 0.0]], np.float32)
+    q, s = o.q8_quantize_per_row_bf16((ties.view(np.uint32) >> 16).astype(np.uint16))
+    assert s[0] == 1.0 and q[0, :7].tolist() == [127, 0, 2, 2, 0, -2, 126] and q[0, 8] == 0
+    q, s = o.q8_quantize_per_row_bf16(np.zeros((3, 7), np.uint16))
+    assert (s == 1.0).all() and not q.any()
+    xb = _bf16_rows(np.random.default_rng(9), 16, 300)
+    for a, b in zip(o.q8_quantize_per_row_bf16(xb), o.q8_quantize_per_row(D.bf16_bits_to_f32(xb))):
+        assert same(a, b)
+
+
+def test_w8a8_bf16out_closed_form(o):
+    """bf16(((1*a_s)*b_s)*float(acc)), acc from an int64 matmul, the fp32
+    products rounded one at a time in that order, then torch's
+    round-to-nearest-even bf16 cast."""
+    torch = pytest.importorskip("torch")
+    gen = np.random.default_rng(10)
+    Aq = gen.integers(-127, 128, (7, 333)).astype(np.int8)
+    Bq = gen.integers(-127, 128, (333, 29)).astype(np.int8)
+    As = gen.uniform(1e-3, 1, 7).astype(np.float32)
+    Bs = gen.uniform(1e-4, 1e-2, 29).astype(np.float32)
+    acc = (Aq.astype(np.int64) @ Bq.astype(np.int64)).astype(np.float32)
+    f = ((np.float32(1) * As)[:, None] * Bs[None, :]).astype(np.float32) * acc
+    want = torch.from_numpy(f.astype(np.float32)).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(o.gemm_w8a8_bf16out(Aq, Bq, As, Bs), want)
+
+
+def test_dequantizers_closed_form(o):
+    """dequant = float(q) * scale, one fp32 rounding (quant.cpp:47-50,65-73,98-105)."""
+    gen = np.random.default_rng(11)
+    q = gen.integers(-127, 128, (5, 9)).astype(np.int8)
+    s_row = gen.uniform(0.01, 3, 5).astype(np.float32)
+    s_col = gen.uniform(0.01, 3, 9).astype(np.float32)
+    assert same(o.q8_dequantize_per_row(q, s_row), q.astype(np.float32) * s_row[:, None])
+    assert same(o.q8_dequantize_per_col(q, s_col), q.astype(np.float32) * s_col[None, :])
+    assert same(o.q8_dequantize_per_tensor(q.ravel(), 0.37), q.ravel().astype(np.float32) * np.float32(0.37))
+    e = gen.integers(0, 256, (5, 9)).astype(np.uint8)
+    e[e == 0x7f] = 0; e[e == 0xff] = 0
+    ef = o.e4m3_to_f32_n(e)
+    assert same(o.fp8_dequantize_per_row(e, s_row), ef * s_row[:, None])
+    assert same(o.fp8_dequantize_per_col(e, s_col), ef * s_col[None, :])
+    assert same(o.fp8_dequantize_per_tensor(e.ravel(), 0.37), ef.ravel() * np.float32(0.37))
+
+
+def test_gemm_grouped_is_per_group_gemm(o):
+    """gemm.cpp:69-75: group g is gemm(A[g], B[g], C[g], M[g], N[g], K[g]),
+    empty groups included, against a float64 product."""
+    gen = np.random.default_rng(12)
+    dims = [(9, 17, 5), (0, 4, 3), (4, 0, 6), (1, 31, 2)]
+    As = [gen.uniform(-1, 1, (m, k)).astype(np.float32) for m, k, _ in dims]
+    Bs = [gen.uniform(-1, 1, (k, n)).astype(np.float32) for _, k, n in dims]
+    Cs = [gen.uniform(-1, 1, (m, n)).astype(np.float32) for m, _, n in dims]
+    outs = o.gemm_grouped(As, Bs, Cs, 1.5, 0.5)
+    for a, b, c, out in zip(As, Bs, Cs, outs):
+        assert same(out, o.gemm(a, b, c, 1.5, 0.5))
+        want = 0.5 * c.astype(np.float64) + 1.5 * (a.astype(np.float64) @ b.astype(np.float64))
+        assert np.allclose(out, want, rtol=1e-5, atol=1e-5)
+
+
+def test_bf16_decode_closed_form(o):
+    """bf16 -> fp32 is the 16-bit left shift of the pattern, for all 2^16."""
+    h = np.arange(65536, dtype=np.uint16)
+    dec = np.array([o.bf16_to_f32(int(b)) for b in h[::257]], np.float32)
+    assert same(dec, (h[::257].astype(np.uint32) << 16).view(np.float32))
+
+
+# ---------------------------------------------------------------------------
+# 5. every exported oracle function has a pin
+# ---------------------------------------------------------------------------
+
+# lho_* symbol -> the tests that pin it (module-qualified when not in this
+# file).  Scalar conversions are pinned through their array forms, which
+# call them element by element.
+PINS = {
+    "lho_f32_to_f16": ["test_golden_encoders", "test_ref_conversions_exhaustive", "test_f16_matches_numpy_ieee"],
+    "lho_f16_to_f32": ["test_golden_decode_tables", "test_ref_conversions_exhaustive", "test_f16_matches_numpy_ieee"],
+    "lho_f32_to_bf16": ["test_golden_encoders", "test_ref_conversions_exhaustive", "test_bf16_matches_torch"],
+    "lho_bf16_to_f32": ["test_bf16_decode_closed_form"],
+    "lho_f32_to_e4m3": ["test_golden_encoders", "test_ref_conversions_exhaustive",
+                        "test_e4m3_encode_vs_torch_and_quirks"],
+    "lho_e4m3_to_f32": ["test_golden_decode_tables", "test_ref_conversions_exhaustive",
+                        "test_e4m3_decode_closed_form"],
+    "lho_f32_to_e5m2": ["test_golden_encoders", "test_ref_conversions_exhaustive", "test_e5m2_closed_form"],
+    "lho_e5m2_to_f32": ["test_golden_decode_tables", "test_ref_conversions_exhaustive", "test_e5m2_closed_form"],
+    "lho_f32_to_f16_n": ["test_golden_encoders", "test_f16_matches_numpy_ieee"],
+    "lho_f16_to_f32_n": ["test_golden_decode_tables", "test_f16_matches_numpy_ieee"],
+    "lho_f32_to_bf16_n": ["test_golden_encoders", "test_bf16_matches_torch"],
+    "lho_f32_to_e4m3_n": ["test_golden_encoders", "test_e4m3_encode_vs_torch_and_quirks"],
+    "lho_e4m3_to_f32_n": ["test_golden_decode_tables", "test_ref_conversions_exhaustive"],
+    "lho_f32_to_e5m2_n": ["test_golden_encoders", "test_ref_conversions_exhaustive"],
+    "lho_e5m2_to_f32_n": ["test_golden_decode_tables", "test_ref_conversions_exhaustive"],
+    "lho_q8_quantize_per_tensor": ["test_golden_quantizers", "test_ref_dequantizers_and_grouped"],
+    "lho_q8_dequantize_per_tensor": ["test_golden_dequantizers", "test_ref_dequantizers_and_grouped",
+                                     "test_dequantizers_closed_form"],
+    "lho_q8_quantize_per_row": ["test_golden_quantizers", "test_ref_random_quantizers_and_gemms",
+                                "test_q8_known_answers", "test_q8_row_multiplies_col_divides", "test_q8_invariants"],
+    "lho_q8_dequantize_per_row": ["test_golden_dequantizers", "test_ref_dequantizers_and_grouped",
+                                  "test_dequantizers_closed_form"],
+    "lho_q8_quantize_per_col": ["test_golden_quantizers", "test_ref_random_quantizers_and_gemms",
+                                "test_q8_known_answers", "test_q8_row_multiplies_col_divides", "test_q8_invariants"],
+    "lho_q8_dequantize_per_col": ["test_golden_dequantizers", "test_ref_dequantizers_and_grouped",
+                                  "test_dequantizers_closed_form"],
+    "lho_q4_get": ["test_q4_get_exhaustive"],
+    "lho_q4_quantize_groupwise": ["test_golden_quantizers", "test_ref_random_quantizers_and_gemms",
+                                  "test_q4_known_answer_and_packing"],
+    "lho_q4_dequantize_groupwise": ["test_golden_quantizers", "test_w4a16_vs_float64"],
+    "lho_fp8_quantize_per_tensor": ["test_golden_quantizers", "test_ref_random_quantizers_and_gemms"],
+    "lho_fp8_dequantize_per_tensor": ["test_golden_dequantizers", "test_ref_dequantizers_and_grouped",
+                                      "test_dequantizers_closed_form"],
+    "lho_fp8_quantize_per_row": ["test_golden_quantizers", "test_ref_random_quantizers_and_gemms"],
+    "lho_fp8_dequantize_per_row": ["test_golden_dequantizers", "test_ref_dequantizers_and_grouped",
+                                   "test_dequantizers_closed_form"],
+    "lho_fp8_quantize_per_col": ["test_golden_quantizers", "test_ref_random_quantizers_and_gemms"],
+    "lho_fp8_dequantize_per_col": ["test_golden_dequantizers", "test_ref_dequantizers_and_grouped",
+                                   "test_dequantizers_closed_form"],
+    "lho_gemm_w8a8": ["test_golden_gemms", "test_ref_random_quantizers_and_gemms", "test_w8a8_epilogue_order"],
+    "lho_gemm_w8a8_i32acc": ["test_golden_gemms", "test_w8a8_acc_vs_int64_matmul"],
+    "lho_gemm_w8a8_bf16out": ["test_golden_w8a8_bf16out", "test_ref_q8_per_row_bf16_and_bf16_epilogue",
+                              "test_w8a8_bf16out_closed_form"],
+    "lho_gemm_w4a16_groupwise": ["test_golden_gemms", "test_ref_random_quantizers_and_gemms",
+                                 "test_w4a16_vs_float64"],
+    "lho_gemm_fp8_e4m3": ["test_golden_gemms", "test_ref_random_quantizers_and_gemms"],
+    "lho_gemm_ref": ["test_golden_gemms"],
+    "lho_gemm": ["test_golden_gemms", "test_ref_random_quantizers_and_gemms"],
+    "lho_gemm_batched": ["test_golden_gemms"],
+    "lho_gemm_grouped": ["test_golden_gemm_grouped", "test_ref_dequantizers_and_grouped",
+                         "test_gemm_grouped_is_per_group_gemm"],
+    "lho_q8_quantize_per_row_bf16": ["test_golden_q8_per_row_bf16", "test_ref_q8_per_row_bf16_and_bf16_epilogue",
+                                     "test_q8_per_row_bf16_closed_forms"],
+    # asymmetric int4 / bf16 I/O: no reference counterpart (closed forms and
+    # reduction to the reference on the symmetric subset)
+    "lho_q4a_quantize_groupwise": ["test_q4a_closed_forms"],
+    "lho_q4a_dequantize_groupwise": ["test_q4a_closed_forms", "test_w4a16_asym_reduces_to_reference"],
+    "lho_gemm_w4a16_asym": ["test_w4a16_asym_reduces_to_reference"],
+    "lho_gemm_w4a16_asym_grouped": ["test_grouped_equals_per_group_calls"],
+    # MoE routing (moe.cpp): bit-exact against the compiled reference
+    "lho_moe_dispatch": ["test_moe_oracle.py::test_dispatch_reference_known_answer",
+                         "test_moe_oracle.py::test_dispatch_bitexact_vs_reference"],
+    "lho_moe_dispatch_table": ["test_moe_dispatch_table_invariants",
+                               "test_moe_oracle.py::test_dispatch_equals_stable_sort"],
+    "lho_swiglu_bf16": ["test_moe_oracle.py::test_swiglu_special_values", "test_moe_oracle.py::test_swiglu_vs_float64",
+                        "test_moe_oracle.py::test_expert_mlp_vs_reference"],
+    "lho_moe_combine_f32": ["test_moe_oracle.py::test_combine_bitexact_vs_reference",
+                            "test_moe_oracle.py::test_combine_order_is_slot_order"],
+    "lho_moe_combine_bf16": ["test_moe_oracle.py::test_combine_bf16_is_f32_combine_rounded"],
+}
+
+
+def _oracle_exports():
+    import re
+    src = open(os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "oracle", "lhq_oracle.c")).read()
+    return set(re.findall(r"^EXPORT\b[^(]*?\b(lho_\w+)\s*\(", src, re.M))
+
+
+def test_every_oracle_export_is_pinned():
+    import importlib
+    exports = _oracle_exports()
+    assert len(exports) > 40
+    assert exports - set(PINS) == set(), f"oracle exports without a pin: {sorted(exports - set(PINS))}"
+    assert set(PINS) - exports == set(), f"pin table names unknown exports: {sorted(set(PINS) - exports)}"
+    this = importlib.import_module(__name__)
+    for sym, tests in PINS.items():
+        for t in tests:
+            mod, name = (t.split("::") if "::" in t else (None, t))
+            m = this if mod is None else importlib.import_module("tests." + mod[:-3])
+            assert callable(getattr(m, name, None)), f"{sym}: pin {t} does not exist"

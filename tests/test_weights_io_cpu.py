@@ -130,3 +130,52 @@ def test_rejects_damaged_bytes(lib, tmp_path):
         assert st == capi.LHQ_ERR_INVALID, (name, st, lib.last_error())
     st, _ = info(lib, tmp_path / "does_not_exist.safetensors")
     assert st == capi.LHQ_ERR_INVALID
+
+
+def _rewrite_header(raw: bytes, edit) -> bytes:
+    """The same file with its JSON header replaced by edit(header dict)."""
+    import json
+    hlen = int.from_bytes(raw[:8], "little")
+    h = json.loads(raw[8:8 + hlen])
+    edit(h)
+    hb = json.dumps(h, separators=(",", ":")).encode()
+    hb += b" " * ((8 - (8 + len(hb)) % 8) % 8)
+    return len(hb).to_bytes(8, "little") + hb + raw[8 + hlen:]
+
+
+def test_rejects_hostile_headers(lib, tmp_path):
+    """Header claims that would index outside the data section or size a
+    buffer from a length the file does not hold are rejected before any
+    allocation: wrapped 64-bit offsets, offsets past the data, swapped
+    offsets, and dims implying far more bytes than the file has."""
+    K, N, G = 256, 48, 128
+    p = tmp_path / "w.safetensors"
+    write(str(p), tensors(lib, K, N, G, True), meta_for(K, N, G))
+    raw = open(p, "rb").read()
+    q, _, _ = sizes(lib, K, N, G, True)
+    big = 2 ** 64 - 1
+
+    def set_off(name, b, e):
+        return lambda h: h[name].update(data_offsets=[b, e])
+
+    def claim(k, n):
+        def f(h):
+            h["__metadata__"].update(K=str(k), N=str(n))
+        return f
+
+    cases = {
+        "wrapped_offsets": set_off("qweight", big - q, big),
+        "offsets_past_data": set_off("qweight", 10 ** 12, 10 ** 12 + q),
+        "swapped_offsets": set_off("qweight", q, 0),
+        "huge_dims": claim(2 ** 20, 2 ** 20),
+        "max_int_dims": claim(2 ** 31 - 2, 2 ** 31 - 1),
+    }
+    for name, edit in cases.items():
+        f = tmp_path / f"{name}.safetensors"
+        open(f, "wb").write(_rewrite_header(raw, edit))
+        st, _ = info(lib, f)
+        assert st == capi.LHQ_ERR_INVALID, (name, st, lib.last_error())
+    # the untouched rewrite is still a valid file (the helper itself is sound)
+    f = tmp_path / "same.safetensors"
+    open(f, "wb").write(_rewrite_header(raw, lambda h: None))
+    assert info(lib, f)[0] == capi.LHQ_OK, lib.last_error()
