@@ -151,7 +151,11 @@ def make_w4_sets(ops, K: int, N: int, G: int, nsets: int, seed: int):
     return sets
 
 
-def bench_w4a16(ops, M, K, N, G, steps, warmup, seed=0, min_rotate_bytes=2 * INFINITY_CACHE_BYTES + (1 << 26)):
+def bench_w4a16(ops, M, K, N, G, steps, warmup, seed=0, min_rotate_bytes=2 * INFINITY_CACHE_BYTES + (1 << 26),
+                workspace=False):
+    """W4A16 bf16 timed over rotating weight sets.  workspace: through
+    lhq_gemm_w4a16_bf16_ws with the workspace the shape asks for (K split
+    across workgroups where the grid is thin), else lhq_gemm_w4a16_bf16."""
     import numpy as np
     import torch
     per = w4a16_bytes(M, K, N, G)
@@ -162,24 +166,29 @@ def bench_w4a16(ops, M, K, N, G, steps, warmup, seed=0, min_rotate_bytes=2 * INF
     A = [(torch.randn((M, K), generator=gen, device="cuda") .to(torch.bfloat16)).view(torch.int16)
          for _ in range(nsets)]
     C = [ops.empty((M, N), np.int16) for _ in range(nsets)]
-    fn = ops.lib().cdll.lhq_gemm_w4a16_bf16
     args = [(A[i].data_ptr(), sets[i].qweight.data_ptr(), sets[i].scales.data_ptr(),
              sets[i].zeros.data_ptr(), C[i].data_ptr()) for i in range(nsets)]
+    ws_bytes = ops.lib().lhq_gemm_w4a16_bf16_workspace_bytes(M, N, K, G) if workspace else 0
+    ws = ops.empty((max(ws_bytes, 1),), np.uint8)
+    name = "lhq_gemm_w4a16_bf16_ws" if workspace else "lhq_gemm_w4a16_bf16"
+    fn = getattr(ops.lib().cdll, name)
+    extra = (ws.data_ptr(), ws_bytes) if workspace else ()
 
     def launch(i):
         a = args[i % nsets]
-        st = fn(a[0], a[1], a[2], a[3], a[4], M, N, K, G, ops.stream())
+        st = fn(a[0], a[1], a[2], a[3], a[4], M, N, K, G, *extra, ops.stream())
         if st:
-            raise RuntimeError(f"lhq_gemm_w4a16_bf16: {ops.lib().last_error()}")
+            raise RuntimeError(f"{name}: {ops.lib().last_error()}")
 
     timer = GraphTimer(launch, nsets, chunk=nsets * max(1, 64 // nsets))
     ms, wall = timer.time(steps, warmup)
     us = ms * 1e3 / steps
-    res = {"M": M, "K": K, "N": N, "G": G, "bytes_per_call": per, "weight_sets": nsets,
+    res = {"M": M, "K": K, "N": N, "G": G, "entry": name, "workspace_bytes": ws_bytes,
+           "bytes_per_call": per, "weight_sets": nsets,
            "rotate_bytes": per * nsets, "us_per_call": us, "gbs": per / (us * 1e-6) / 1e9,
            "elapsed_ms": ms, "wall_ms": wall}
     res["hbm_frac"] = res["gbs"] / HBM_PEAK_GBS
-    del timer, sets, A, C
+    del timer, sets, A, C, ws
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     return res
@@ -410,8 +419,24 @@ def bench_w8a8(ops, M, K, N, steps, warmup, seed=0):
     qms, _ = GraphTimer(qlaunch, 1, chunk=16).time(steps, warmup)
     qus = qms * 1e3 / steps
     qbytes = M * K * 2 + M * K + M * 4
+    # the per-output-channel weight quantizer (quant.cpp:75-96) on this B
+    W = torch.randn((K, N), generator=gen, device="cuda") * 0.02
+    Bq = ops.empty((K, N), np.int8)
+    wfn = ops.lib().cdll.lhq_q8_quantize_per_col
+
+    def wlaunch(_i):
+        st = wfn(W.data_ptr(), Bq.data_ptr(), Bs.data_ptr(), K, N, ops.stream())
+        if st:
+            raise RuntimeError(f"lhq_q8_quantize_per_col: {ops.lib().last_error()}")
+
+    wsteps = max(5, steps // 10)
+    wms, _ = GraphTimer(wlaunch, 1, chunk=8).time(wsteps, 2)
+    wus = wms * 1e3 / wsteps
+    wbytes = K * N * 4 + K * N + N * 4
+    del W, Bq
     res = {"M": M, "K": K, "N": N, "us_per_call": us, "tops": ops_per / (us * 1e-6) / 1e12,
-           "act_quant_us": qus, "act_quant_gbs": qbytes / (qus * 1e-6) / 1e9}
+           "act_quant_us": qus, "act_quant_gbs": qbytes / (qus * 1e-6) / 1e9,
+           "weight_quant_us": wus, "weight_quant_gbs": wbytes / (wus * 1e-6) / 1e9}
     res["mfma_frac"] = res["tops"] / INT8_PEAK_TOPS
     del Bt, Xb, Aq, As, C
     torch.cuda.synchronize()
@@ -434,6 +459,24 @@ def copy_probe(nbytes: int = 1 << 30, reps: int = 5) -> None:
 # ---------------------------------------------------------------------------
 # CPU baseline (test infrastructure: the reference's path or its restatement)
 # ---------------------------------------------------------------------------
+
+def host_cpu() -> str:
+    """The host CPU's model name and the cores this process may use."""
+    model = "unknown CPU"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count()
+    return f"{model}; host nproc={os.cpu_count()}, {usable} usable by this process"
+
 
 def cpu_baseline_w8a8(K: int, N: int, budget_s: float):
     """The reference's gemm_w8a8 (gemm_quant.cpp:29-49, fp32 output) on an
@@ -467,7 +510,7 @@ def cpu_baseline_w8a8(K: int, N: int, budget_s: float):
         "kind": kind,
         "sample": (f"gemm_w8a8 (gemm_quant.cpp:29-49) on {m} rows of the K={K}, N={N} workload, "
                    f"{per_row * 1e3:.0f} ms/row, 1 thread; extrapolated linearly in M (rows are independent): "
-                   f"M=4096 {4096 * per_row:.0f} s, M=2048 {2048 * per_row:.0f} s; host nproc={os.cpu_count()}"),
+                   f"M=4096 {4096 * per_row:.0f} s, M=2048 {2048 * per_row:.0f} s; {host_cpu()}"),
         "s_per_call_m4096_extrapolated": 4096 * per_row,
     }
 
@@ -498,7 +541,7 @@ def cpu_baseline(M: int, K: int, N: int, G: int, budget_s: float):
         "kind": kind,
         "sample": (f"gemm_w4a16_groupwise (gemm_quant.cpp:54-82) M={M} K={K} N={N} G={G}, fp32 A/C, "
                    f"symmetric int4 + fp32 scales ({per} algorithmic B/call); p50 of {len(times)} calls, "
-                   f"{p50 * 1e3:.1f} ms/call, 1 thread; host nproc={os.cpu_count()}"),
+                   f"{p50 * 1e3:.1f} ms/call, 1 thread; {host_cpu()}"),
         "ms_per_call": p50 * 1e3,
         "speedup_gpu_over_cpu": None,
     }
@@ -527,11 +570,12 @@ def prefill_legs(ops):
     out = []
     for m, steps in ((64, 500), (4096, 40)):
         log(f"w4a16 prefill M={m} K=8192 N=28672: {steps} steps")
-        r = bench_w4a16(ops, m, 8192, 28672, 128, steps, max(5, steps // 10))
+        r = bench_w4a16(ops, m, 8192, 28672, 128, steps, max(5, steps // 10), workspace=True)
         tf = 2 * m * 8192 * 28672 / (r["us_per_call"] * 1e-6) / 1e12
         log(f"  {r['us_per_call']:.1f} us/call  {tf:.0f} TFLOPS ({100 * tf / BF16_PEAK_TFLOPS:.1f}% of bf16 peak), "
             f"{r['gbs']:.0f} GB/s ({100 * r['hbm_frac']:.1f}% of HBM peak)")
         out.append({"leg": "w4a16_prefill", "M": m, "K": 8192, "N": 28672, "G": 128,
+                    "entry": r["entry"], "workspace_bytes": r["workspace_bytes"],
                     "us_per_call": round(r["us_per_call"], 2), "tflops": round(tf, 1),
                     "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4), "gbs": round(r["gbs"], 1),
                     "hbm_frac": round(r["hbm_frac"], 4)})
@@ -554,10 +598,11 @@ def config_sweep(ops, name, ms, kns, G=128):
         for k, n in kns:
             flops = 2 * m * k * n
             steps = 200 if m <= 64 else max(10, int(2e14 // flops))
-            r = bench_w4a16(ops, m, k, n, G, steps, max(5, steps // 10))
+            r = bench_w4a16(ops, m, k, n, G, steps, max(5, steps // 10), workspace=True)
             tf = flops / (r["us_per_call"] * 1e-6) / 1e12
             bound = "hbm" if r["gbs"] / HBM_PEAK_GBS >= tf / BF16_PEAK_TFLOPS else "mfma"
-            out.append({"M": m, "K": k, "N": n, "us_per_call": round(r["us_per_call"], 2),
+            out.append({"M": m, "K": k, "N": n, "workspace_bytes": r["workspace_bytes"],
+                        "us_per_call": round(r["us_per_call"], 2),
                         "gbs": round(r["gbs"], 1), "hbm_frac": round(r["hbm_frac"], 4),
                         "tflops": round(tf, 1), "mfma_frac": round(tf / BF16_PEAK_TFLOPS, 4), "bound": bound})
             log(f"  {name} M={m} K={k} N={n}: {r['us_per_call']:.1f} us  {r['gbs']:.0f} GB/s "
@@ -654,7 +699,8 @@ def main() -> int:
             log(f"w8a8 prefill M={m} K=4096 N=14336: {args.w8a8_steps} steps")
             r = bench_w8a8(ops, m, 4096, 14336, args.w8a8_steps, max(10, args.w8a8_steps // 10))
             log(f"  {r['us_per_call']:.1f} us/call  {r['tops']:.0f} TOPS ({100 * r['mfma_frac']:.1f}% of int8 peak); "
-                f"act quant {r['act_quant_us']:.1f} us ({r['act_quant_gbs']:.0f} GB/s)")
+                f"act quant {r['act_quant_us']:.1f} us ({r['act_quant_gbs']:.0f} GB/s); "
+                f"weight quant (per column) {r['weight_quant_us']:.1f} us ({r['weight_quant_gbs']:.0f} GB/s)")
             w8.append(r)
 
     fp8 = []
@@ -690,7 +736,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u4xbf16->f32",
+        "dtype": "u4 x bf16 -> bf16 (fp32 accumulate)",
         "data": "synthetic (seeded N(0,0.02) weights quantized on device, N(0,1) bf16 activations)",
         "config": {"workload": "w4a16_decode_gemv", "M": M, "K": K, "N": N, "group_size": G,
                    "weights": "asymmetric int4, fp16 scale + u4 zero per group",
@@ -703,7 +749,8 @@ def main() -> int:
         "w8a8_prefill": [
             {"M": r["M"], "K": r["K"], "N": r["N"], "us_per_call": round(r["us_per_call"], 2),
              "value": round(r["tops"], 1), "unit": "TOPS", "peak": INT8_PEAK_TOPS,
-             "frac": round(r["mfma_frac"], 4), "act_quant_us": round(r["act_quant_us"], 2)}
+             "frac": round(r["mfma_frac"], 4), "act_quant_us": round(r["act_quant_us"], 2),
+             "weight_quant_us": round(r["weight_quant_us"], 2), "weight_quant_gbs": round(r["weight_quant_gbs"], 1)}
             for r in w8],
         "w8a8_cpu_baseline": cpu_w8,
         "fp8_gemm": fp8,

@@ -154,6 +154,22 @@ int lhq_gemm_w4a16(const float* A, const uint8_t* qweight, const float* scales,
 int lhq_gemm_w4a16_bf16(const uint16_t* A, const uint8_t* qweight, const uint16_t* scales,
                         const uint32_t* zeros, uint16_t* C, int M, int N, int K,
                         int group_size, void* stream);
+/* lhq_gemm_w4a16_bf16 with a caller workspace (no reference counterpart:
+ * the reference's CPU loop needs no partial sums).  Where the output grid
+ * cannot fill the GPU (17 <= M <= 64 rows, group_size a multiple of 128,
+ * and weights large enough for the tile kernel), K is split across
+ * workgroups: each split writes fp32 partial sums to `workspace` and they
+ * are added in split order into C (deterministic).  The split count is
+ * the most the workspace allows, up to what
+ * lhq_gemm_w4a16_bf16_workspace_bytes reports for the shape (0: no split);
+ * with a NULL or smaller workspace the call runs with fewer splits or none,
+ * same results to the bf16 bar.  workspace: device memory, 16-byte aligned, not
+ * shared with a call running concurrently.  Results match
+ * lhq_gemm_w4a16_bf16 within fp32 reassociation. */
+int64_t lhq_gemm_w4a16_bf16_workspace_bytes(int M, int N, int K, int group_size);
+int lhq_gemm_w4a16_bf16_ws(const uint16_t* A, const uint8_t* qweight, const uint16_t* scales,
+                           const uint32_t* zeros, uint16_t* C, int M, int N, int K, int group_size,
+                           void* workspace, int64_t workspace_bytes, void* stream);
 /* Uniform batch of independent W4A16 GEMMs (the gemm_batched contract,
  * gemm.cpp:59-67): A [batch,M,K], weights stacked with the per-matrix
  * strides lhq_w4_*_bytes, C [batch,M,N]. */

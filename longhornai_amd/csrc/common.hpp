@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <cstdlib>
 
 #include "longhorn_hip.h"
 #include "w4layout.hpp"
@@ -201,6 +202,19 @@ __device__ __forceinline__ u32x4_t w4_operand_z(uint32_t d, uint32_t zb) {
 // Host-side status plumbing (defined in capi.cpp).
 // ---------------------------------------------------------------------------
 namespace lhq {
+// Tuning knobs (kernel choice and launch shape overrides, LHQ_W4_* and
+// LHQ_GEMM8_*) are read from the environment only in a build made with
+// -DLHQ_TUNING_KNOBS (make TUNING=1), for sweeps.  The product library
+// ignores the environment and always runs the tested heuristic.
+inline int tuning_knob(const char* name, int dflt) {
+#ifdef LHQ_TUNING_KNOBS
+    const char* v = std::getenv(name);
+    return v ? std::atoi(v) : dflt;
+#else
+    (void)name;
+    return dflt;
+#endif
+}
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }

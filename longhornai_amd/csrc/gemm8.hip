@@ -950,10 +950,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm8_skinny_kernel(Gemm8Args p
     }
 }
 
-int env_int(const char* name, int dflt) {
-    const char* v = std::getenv(name);
-    return v ? std::atoi(v) : dflt;
-}
+int env_int(const char* name, int dflt) { return tuning_knob(name, dflt); }
 
 // Compute units of the current device (one persistent workgroup each).
 int device_cus() {

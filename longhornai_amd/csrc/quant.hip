@@ -172,25 +172,77 @@ __global__ __launch_bounds__(kBlock) void quant_per_row_bf16_vec_kernel(const ui
     if (threadIdx.x == 0) scales[blockIdx.x] = scale;
 }
 
-// Per-column scales: a thread per column scans the rows (coalesced across
-// threads), then scale = m / QMAX (quant.cpp:75-96, 218-238).
+// Per-column scales (quant.cpp:75-96, 218-238), in three launches that need
+// no scratch memory: the scales array first holds the running max |x| of its
+// column as float bits (non-negative floats order like their bit patterns),
+// then the scale m / QMAX (1 where m == 0).
+//   (1) zero the scales;
+//   (2) a grid of (column block) x (row chunk) workgroups: each thread reduces
+//       VEC adjacent columns over kColRows rows with 16-byte loads, then one
+//       atomic max per column and chunk -- the max is order-independent and
+//       NaN never wins, so any split gives the reference's maximum;
+//   (3) turn each max into its scale.
+constexpr int kColRows = 64;
+
+__global__ void zero_f32_kernel(float* __restrict__ p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0.0f;
+}
+
+template <int VEC>
+__global__ __launch_bounds__(kBlock) void col_max_kernel(const float* __restrict__ src,
+                                                         float* __restrict__ maxw, int rows, int cols) {
+    const int c0 = (blockIdx.x * kBlock + threadIdx.x) * VEC;
+    if (c0 >= cols) return;
+    float m[VEC];
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) m[j] = 0.0f;
+    // row chunks blockIdx.y, blockIdx.y + gridDim.y, ... (the grid's y extent
+    // is capped, so very tall inputs give a workgroup several chunks)
+    for (int r0 = blockIdx.y * kColRows; r0 < rows; r0 += gridDim.y * kColRows) {
+        const int r1 = min(rows, r0 + kColRows);
+        for (int r = r0; r < r1; ++r) {
+            const float* row = src + static_cast<int64_t>(r) * cols + c0;
+            if constexpr (VEC == 4) {
+                const f32x4_t v = *reinterpret_cast<const f32x4_t*>(row);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) m[j] = amax(m[j], fabsf(v[j]));
+            } else {
+                m[0] = amax(m[0], fabsf(row[0]));
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < VEC; ++j)
+        if (m[j] > 0.0f) atomicMax(reinterpret_cast<unsigned int*>(maxw + c0 + j), __float_as_uint(m[j]));
+}
+
 template <bool FP8>
-__global__ void col_scales_kernel(const float* __restrict__ src, float* __restrict__ scales, int rows,
-                                  int cols) {
+__global__ void col_finalize_kernel(float* __restrict__ scales, int cols) {
     const int c = blockIdx.x * blockDim.x + threadIdx.x;
     if (c >= cols) return;
-    float m = 0.0f;
-    for (int r = 0; r < rows; ++r) m = amax(m, fabsf(src[static_cast<int64_t>(r) * cols + c]));
+    const float m = scales[c];
     const float qmax = FP8 ? 448.0f : 127.0f;
     scales[c] = (m > 0.0f) ? m / qmax : 1.0f;
 }
 
-template <bool FP8>
+// q = round(x / scale[c]); VEC adjacent elements per thread (VEC divides cols).
+template <bool FP8, int VEC>
 __global__ void quant_per_col_kernel(const float* __restrict__ src, const float* __restrict__ scales,
-                                     uint8_t* __restrict__ dst, int rows, int cols, int64_t n) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+                                     uint8_t* __restrict__ dst, int cols, int64_t n) {
+    const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * VEC;
     if (i >= n) return;
-    dst[i] = quant_div<FP8>(src[i], scales[i % cols]);
+    const int c = static_cast<int>(i % cols);
+    if constexpr (VEC == 4) {
+        const f32x4_t v = *reinterpret_cast<const f32x4_t*>(src + i);
+        const f32x4_t sc = *reinterpret_cast<const f32x4_t*>(scales + c);
+        uint32_t o = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o |= static_cast<uint32_t>(quant_div<FP8>(v[j], sc[j])) << (8 * j);
+        *reinterpret_cast<uint32_t*>(dst + i) = o;
+    } else {
+        dst[i] = quant_div<FP8>(src[i], scales[c]);
+    }
 }
 
 // Per-tensor: (1) clear the max word, (2) atomic max of |x| bits (non-negative
@@ -409,9 +461,24 @@ int quantize_per_col(const float* src, uint8_t* dst, float* scales, int rows, in
     LHQ_REQUIRE(rows >= 0 && cols >= 0, "%s: negative dims", who);
     if (cols == 0) return LHQ_OK;
     hipStream_t s = as_stream(stream);
-    col_scales_kernel<FP8><<<blocks_for(cols), kBlock, 0, s>>>(src, scales, rows, cols);
+    // 16-byte loads need 4 | cols and aligned rows; scales and dst are then
+    // read / written in 16- and 4-byte units at multiples of 4 elements.
+    const bool vec = cols % 4 == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0 &&
+                     (reinterpret_cast<uintptr_t>(scales) & 15) == 0 && (reinterpret_cast<uintptr_t>(dst) & 3) == 0;
+    zero_f32_kernel<<<blocks_for(cols), kBlock, 0, s>>>(scales, cols);
+    if (rows > 0) {
+        const int vcols = vec ? cols / 4 : cols;
+        const dim3 grid(static_cast<unsigned>(ceil_div(vcols, kBlock)),
+                        static_cast<unsigned>(min(ceil_div(rows, kColRows), 65535)));
+        if (vec) col_max_kernel<4><<<grid, kBlock, 0, s>>>(src, scales, rows, cols);
+        else col_max_kernel<1><<<grid, kBlock, 0, s>>>(src, scales, rows, cols);
+    }
+    col_finalize_kernel<FP8><<<blocks_for(cols), kBlock, 0, s>>>(scales, cols);
     const int64_t n = static_cast<int64_t>(rows) * cols;
-    if (n > 0) quant_per_col_kernel<FP8><<<blocks_for(n), kBlock, 0, s>>>(src, scales, dst, rows, cols, n);
+    if (n > 0) {
+        if (vec) quant_per_col_kernel<FP8, 4><<<blocks_for(n / 4), kBlock, 0, s>>>(src, scales, dst, cols, n);
+        else quant_per_col_kernel<FP8, 1><<<blocks_for(n), kBlock, 0, s>>>(src, scales, dst, cols, n);
+    }
     return check_launch(who);
 }
 

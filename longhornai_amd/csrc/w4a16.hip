@@ -58,6 +58,10 @@ struct W4Args {
     const uint32_t* const* zss;
     int num_groups, row_capacity;
     int group_rb;  // rows per row block of a grouped decode launch
+    // split-K tile launches (grid.z = split): split s covers K tiles
+    // [s * kps, (s + 1) * kps) and writes fp32 partial sums ws[s][M][N]
+    float* ws;
+    int kps;
 };
 
 // Scale group of segment s of K tile kt; a segment is BPS 32-wide k blocks
@@ -1029,13 +1033,20 @@ constexpr int MM_CT = 4;  // column tiles per wave
 
 #define LHQ_LDS_AS __attribute__((address_space(3)))
 
-template <int BPS, bool GBIG, bool GR, bool SWI, int L>
+// SK (split-K, plain launches only): grid.z is the K split instead of the
+// batch; the workgroup's K parts share its split's K range, and it writes
+// fp32 partial sums to p.ws[split][M][N] for w4_splitk_reduce_kernel to add
+// in split order.  RB (L == 1 only): 16-row blocks per wave, 64 rows at
+// RB = 4; RB = 2 serves up to 32 rows without the MFMAs of 64.
+template <int BPS, bool GBIG, bool GR, bool SWI, int L, bool SK = false, int RB = 4>
 __global__ __launch_bounds__(L == 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_kernel(W4Args p) {
+    static_assert(RB == 4 || (RB == 2 && L == 1 && !GR), "32-row blocks in the plain 64 x 256 layout only");
+    static_assert(!SK || (!GR && !SWI), "split-K on plain launches only");
     constexpr int SEGS = 4 / BPS;
     constexpr int NW = (L == 3) ? 8 : 4;                   // waves
     constexpr int NK = (L == 2) ? 2 : (L == 3) ? 4 : 1;  // K parts
-    constexpr int BM = (L == 0) ? 128 : 64, WN = (L == 1) ? 4 : 2;
-    constexpr int A_BYTES = ((L == 1) ? 64 : (L == 3) ? 256 : 128) * kW4TileK * 2;
+    constexpr int BM = (L == 0) ? 128 : 16 * RB, WN = (L == 1) ? 4 : 2;
+    constexpr int A_BYTES = ((L == 1) ? 16 * RB : (L == 3) ? 256 : 128) * kW4TileK * 2;
     constexpr int DMA = A_BYTES / 1024 / NW;  // activation DMAs per wave per K tile
     extern __shared__ __attribute__((aligned(1024))) uint8_t mm_lds[];  // 2 x A_BYTES
     const int lane = threadIdx.x & 63;
@@ -1046,9 +1057,13 @@ __global__ __launch_bounds__(L == 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
     const int wm = (L == 0) ? wr : 0;
     const int ks = (NK > 1) ? wr : 0;
     const int wn = (L == 1) ? wave : (wave & 1);
-    const int kh = (p.Kt + NK - 1) / NK;  // K tiles per part
-    const int kofs = ks * kh;             // this wave's first K tile
-    const int z = blockIdx.z;
+    // K tiles [kb, ke) of this workgroup (its split, or all of K), in NK
+    // parts of kh tiles; this wave's part starts at kofs
+    const int kb = SK ? static_cast<int>(blockIdx.z) * p.kps : 0;
+    const int ke = SK ? min(p.Kt, kb + p.kps) : p.Kt;
+    const int kh = (ke - kb + NK - 1) / NK;
+    const int kofs = kb + ks * kh;
+    const int z = SK ? 0 : blockIdx.z;
     int m0, m_end;
     const uint8_t* qw;
     const uint16_t* sc;
@@ -1075,7 +1090,7 @@ __global__ __launch_bounds__(L == 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
     // (a fixed bound: a bound that depends on a template parameter, with the
     // array captured by the lambdas below, makes hipcc's host pass drop the
     // kernel's launch stub without a diagnostic; entries past DMA are unused)
-    static_assert(DMA <= 8, "activation DMAs per wave");
+    static_assert(DMA >= 1 && DMA <= 8, "activation DMAs per wave");
     uint32_t a_off[8];
 #pragma unroll
     for (int q = 0; q < DMA; ++q) {
@@ -1119,9 +1134,9 @@ __global__ __launch_bounds__(L == 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
         }
     };
 
-    f32x4_t acc[4][MM_CT];
+    f32x4_t acc[RB][MM_CT];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < RB; ++i)
 #pragma unroll
         for (int c = 0; c < MM_CT; ++c) acc[i][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     const u32x4_t m144 = {kM144Bf16x2, kM144Bf16x2, kM144Bf16x2, kM144Bf16x2};
@@ -1136,10 +1151,10 @@ __global__ __launch_bounds__(L == 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
     const bool live = m0 + 64 * wm < m_end;
     auto compute = [&](const uint8_t* buf, const Regs& R, int kt_in) {
         const int kt = kt_in + kofs;
-        if (!live || kt >= p.Kt) return;  // the last K part may be short
-        u32x4_t a[4][4];
+        if (!live || kt >= ke) return;  // the last K part may be short
+        u32x4_t a[RB][4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < RB; ++i)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 a[i][j] = *reinterpret_cast<const u32x4_t*>(buf + a_frag + i * 16 * 256 +
@@ -1147,9 +1162,9 @@ __global__ __launch_bounds__(L == 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
         // xs = -144 * sum_k x (the MFMA against a -144 operand), per row
         // block; it seeds every t chain of the K tile (below)
         static_assert(SEGS == 1, "one scale segment per K tile");
-        f32x4_t xs[4];
+        f32x4_t xs[RB];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < RB; ++i) {
             xs[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < 4; ++j) xs[i] = mfma_bf16_16x16x32(a[i][j], m144, xs[i]);
@@ -1177,16 +1192,16 @@ __global__ __launch_bounds__(L == 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
             for (int j = 0; j < 4; ++j) b[j] = w4_operand_z(R.w[c][j], zb);
             const float sc = f16_to_f32(static_cast<uint16_t>(R.sw[c][0] >> s_half));
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+            for (int i = 0; i < RB; ++i) {
                 f32x4_t t = xs[i];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) t = mfma_bf16_16x16x32(a[i][j], b[j], t);
-                if (c > 0 || i > 0) correct(i == 0 ? c - 1 : c, i == 0 ? 3 : i - 1, tp, sp);
+                if (c > 0 || i > 0) correct(i == 0 ? c - 1 : c, i == 0 ? RB - 1 : i - 1, tp, sp);
                 tp = t;
                 sp = sc;
             }
         }
-        correct(MM_CT - 1, 3, tp, sp);
+        correct(MM_CT - 1, RB - 1, tp, sp);
     };
     // all of this wave's loads have landed and every wave is done with the
     // buffer the next DMA overwrites.  Builtins, not inline asm: the
@@ -1252,6 +1267,23 @@ __global__ __launch_bounds__(L == 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
 
     // D element r of block (i, c): row 64*wm + 16*i + 4*(lane >> 4) + r,
     // column of tile (blockIdx.x*8 + 4*wn + c), lane & 15
+    if constexpr (SK) {
+        float* const W = p.ws + static_cast<int64_t>(blockIdx.z) * p.M * p.N;
+#pragma unroll
+        for (int c = 0; c < MM_CT; ++c) {
+            const int nt = static_cast<int>(blockIdx.x) * WN * MM_CT + wn * MM_CT + c;
+            const int cn = nt * kW4TileN + col;
+            if (nt >= p.Nt || cn >= p.N) continue;
+#pragma unroll
+            for (int i = 0; i < RB; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = m0 + wm * 64 + i * 16 + 4 * (lane >> 4) + r;
+                    if (row < m_end) W[static_cast<int64_t>(row) * p.N + cn] = acc[i][c][r];
+                }
+        }
+        return;
+    }
     uint16_t* C = static_cast<uint16_t*>(p.C) + (GR ? 0 : z * p.c_bs);
     if constexpr (SWI) {
         // blocks (c, c + 1) hold a gate tile and its up tile (nt even)
@@ -1277,12 +1309,33 @@ __global__ __launch_bounds__(L == 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
         const int cn = nt * kW4TileN + col;
         if (nt >= p.Nt || cn >= p.N) continue;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < RB; ++i)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = m0 + wm * 64 + i * 16 + 4 * (lane >> 4) + r;
                 if (row < m_end) C[static_cast<int64_t>(row) * p.N + cn] = f32_to_bf16(acc[i][c][r]);
             }
+    }
+}
+
+// C[m][n] = bf16(sum over s < S of ws[s][m][n]), the splits added in order
+// (deterministic); four consecutive elements per thread where 4 | MN.
+template <bool VEC>
+__global__ void w4_splitk_reduce_kernel(const float* __restrict__ ws, uint16_t* __restrict__ C, int64_t mn, int S) {
+    const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * (VEC ? 4 : 1);
+    if (i >= mn) return;
+    if constexpr (VEC) {
+        f32x4_t v = *reinterpret_cast<const f32x4_t*>(ws + i);
+        for (int s = 1; s < S; ++s) {
+            const f32x4_t w = *reinterpret_cast<const f32x4_t*>(ws + static_cast<int64_t>(s) * mn + i);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] += w[j];
+        }
+        *reinterpret_cast<u32x2_t*>(C + i) = u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    } else {
+        float v = ws[i];
+        for (int s = 1; s < S; ++s) v += ws[static_cast<int64_t>(s) * mn + i];
+        C[i] = f32_to_bf16(v);
     }
 }
 
@@ -1303,7 +1356,8 @@ void allow_cu_lds() {
     (void)e;
 }
 
-// Tuning knobs (read once; unset = heuristic):
+// Tuning knobs (tuning_knob: read only in a -DLHQ_TUNING_KNOBS build; unset
+// or product build = heuristic):
 //   LHQ_W4_I8=-1 disables the integer decode kernel (M == 1);
 //   LHQ_W4_DECODE=-1 disables the bf16 decode kernel (plain and grouped);
 //   LHQ_W4_DEC_T (1|2), LHQ_W4_DEC_NPW (4|8 tiles per wave per pass) and
@@ -1313,10 +1367,7 @@ void allow_cu_lds() {
 //   LHQ_W4_TILES (1|2), LHQ_W4_WAVES (1|2|4|8) shape the generic kernel;
 //   LHQ_W4_MMA (0|1) and LHQ_W4_MMA_L (0..3) force the tile kernel off / on
 //   and its layout.
-int env_int(const char* name) {
-    const char* v = std::getenv(name);
-    return v ? std::atoi(v) : 0;
-}
+int env_int(const char* name) { return tuning_knob(name, 0); }
 
 template <bool F32A, bool ASYM, bool F32C, int T, int NPW, int MR>
 void launch_decode_mr(const W4Args& a, dim3 grid, int S, int bps, size_t lds, hipStream_t s) {
@@ -1439,10 +1490,7 @@ int device_cus() {
 // forces a layout.
 template <bool GR, bool SWI = false>
 int launch_mma(const W4Args& a, int64_t rows, int groups, int batch, hipStream_t s, const char* who) {
-    static const int env_l = [] {
-        const char* v = std::getenv("LHQ_W4_MMA_L");
-        return v ? std::atoi(v) : -1;
-    }();
+    static const int env_l = tuning_knob("LHQ_W4_MMA_L", -1);
     int l = 1;
     const int64_t wgs1 = static_cast<int64_t>(ceil_div(a.Nt, 4 * MM_CT)) * (ceil_div64(rows, 64) + groups) * batch;
     if (wgs1 < 2 * static_cast<int64_t>(device_cus()) && a.Kt >= 16) l = 2;
@@ -1463,10 +1511,7 @@ int launch_mma(const W4Args& a, int64_t rows, int groups, int batch, hipStream_t
 // on where it applies): G >= 128, K % 128 == 0 (no activation padding in
 // LDS) and 32-bit element offsets for the activations.
 bool mma_applies(const W4Args& a, int64_t rows, double rows_per_block) {
-    static const int env = [] {
-        const char* v = std::getenv("LHQ_W4_MMA");
-        return v ? std::atoi(v) : -1;
-    }();
+    static const int env = tuning_knob("LHQ_W4_MMA", -1);
     if (env == 0) return false;
     if (a.G < kW4TileK || a.K % kW4TileK != 0 || rows * a.K >= (int64_t{1} << 31)) return false;
     // The 16-row kernel re-reads the activation rows for every column tile
@@ -1702,6 +1747,115 @@ int grouped_w4(const char* who, const uint16_t* A, const int32_t* offsets, const
     return launch_w4<false, true, false, true, SWI>(a, 1, as_stream(stream), static_cast<int>(mblocks));
 }
 
+// ---------------------------------------------------------------------------
+// Thin grids: the tile kernel with K split across workgroups.
+//
+// At 17..64 rows the tile kernel's grid has ceil(N / 256) column groups --
+// 32 for N = 8192, far short of 256 CUs -- and each workgroup walks all of
+// K.  A plan here spreads K over S workgroups per output tile: each writes
+// fp32 partial sums of its K range to a workspace [S][M][N], and
+// w4_splitk_reduce_kernel adds them in split order into the bf16 output
+// (deterministic, whatever the schedule).  Up to 32 rows use 32-row blocks
+// (RB = 2), so they do not pay for the MFMAs of 64.
+// ---------------------------------------------------------------------------
+struct TilePlan {
+    bool split = false;  // false: the entry point's ordinary launch
+    int L = 1;           // tile kernel layout
+    int RB = 4;          // 16-row blocks per wave
+    int S = 1;           // K splits
+    int kps = 0;         // K tiles per split
+    int64_t ws_bytes = 0;
+};
+
+constexpr int kSplitMinKt = 4;  // K tiles per split at least
+
+// ws_cap: the workspace bytes available (-1: as much as the plan wants).
+// A split applies to 17..64 rows where the tile kernel runs (G >= 128), and
+// where the ordinary launch would be the tile kernel or the weights are
+// large enough (K * N >= 32 Mi) that the 16-row kernel loses to it: measured
+// at M = 32, (K, N) = (4096, 4096) 9.2 us on the 16-row kernel against 12.5
+// split, but (4096, 11008) 19.9 against 15.6 and (8192, 8192) 22.0 against
+// 17.0.  S brings the grid to about one workgroup per CU, with at least 4 K
+// tiles per split (M = 64, K = N = 8192: 48.5 us unsplit, 24.5 with 8
+// splits, 27.3 with 16).
+TilePlan plan_thin(const W4Args& a, int64_t ws_cap) {
+    TilePlan t;
+    // (read on every call in a tuning build, so one process can sweep them)
+    const int env_thin = tuning_knob("LHQ_W4_THIN", -1);   // 0: never split
+    const int env_s = tuning_knob("LHQ_W4_THIN_S", 0);     // force the split count
+    const int env_l = tuning_knob("LHQ_W4_THIN_L", 0);     // force the layout (1..3)
+    if (env_thin == 0 || a.M <= 16 || a.M > 64) return t;
+    if (a.G < kW4TileK || a.K % kW4TileK != 0 || static_cast<int64_t>(a.M) * a.K >= (int64_t{1} << 31)) return t;
+    if (!mma_applies(a, a.M, a.M) && static_cast<int64_t>(a.K) * a.N < (int64_t{32} << 20)) return t;
+    t.RB = a.M <= 32 ? 2 : 4;
+    if (env_l >= 1 && env_l <= 3) t.L = env_l;
+    if (t.L != 1) t.RB = 4;
+    const int64_t wgs = static_cast<int64_t>(ceil_div(a.Nt, (t.L == 1 ? 4 : 2) * MM_CT)) * ceil_div(a.M, 16 * t.RB);
+    const int cus = std::max(device_cus(), 1);
+    int S = static_cast<int>(std::min<int64_t>(ceil_div64(cus, wgs), std::max(1, a.Kt / kSplitMinKt)));
+    if (env_s >= 1) S = std::min(env_s, a.Kt);
+    const int64_t per_split = static_cast<int64_t>(a.M) * a.N * 4;
+    if (ws_cap >= 0) S = static_cast<int>(std::min<int64_t>(S, std::max<int64_t>(1, ws_cap / per_split)));
+    // splits of equal length: no split ends up empty
+    const int kps = ceil_div(a.Kt, std::max(S, 1));
+    S = ceil_div(a.Kt, kps);
+    if (S <= 1) return t;
+    t.split = true;
+    t.S = S;
+    t.kps = kps;
+    t.ws_bytes = S * per_split;
+    return t;
+}
+
+template <int L, int RB>
+void launch_split_rb(const W4Args& a, unsigned splits, hipStream_t s) {
+    constexpr size_t lds = 2 * ((L == 1) ? 16 * RB : (L == 3) ? 256 : 128) * kW4TileK * 2;
+    constexpr int threads = (L == 3) ? 512 : 256;
+    const dim3 grid(ceil_div(a.Nt, ((L == 1) ? 4 : 2) * MM_CT), ceil_div(a.M, 16 * RB), splits);
+    if (a.gmul) {
+        if constexpr (lds > 64 * 1024) allow_cu_lds<&w4_mma_kernel<4, true, false, false, L, true, RB>>();
+        w4_mma_kernel<4, true, false, false, L, true, RB><<<grid, threads, lds, s>>>(a);
+    } else {
+        if constexpr (lds > 64 * 1024) allow_cu_lds<&w4_mma_kernel<4, false, false, false, L, true, RB>>();
+        w4_mma_kernel<4, false, false, false, L, true, RB><<<grid, threads, lds, s>>>(a);
+    }
+}
+
+int launch_split(W4Args a, const TilePlan& t, void* ws, hipStream_t s, const char* who) {
+    a.ws = static_cast<float*>(ws);
+    a.kps = t.kps;
+    if (t.L == 3) launch_split_rb<3, 4>(a, t.S, s);
+    else if (t.L == 2) launch_split_rb<2, 4>(a, t.S, s);
+    else if (t.RB == 2) launch_split_rb<1, 2>(a, t.S, s);
+    else launch_split_rb<1, 4>(a, t.S, s);
+    if (int st = check_launch(who)) return st;
+    const int64_t mn = static_cast<int64_t>(a.M) * a.N;
+    const bool vec = mn % 4 == 0 && (reinterpret_cast<uintptr_t>(a.C) & 7) == 0;
+    const unsigned blocks = static_cast<unsigned>(ceil_div64(vec ? mn / 4 : mn, 256));
+    if (vec) w4_splitk_reduce_kernel<true><<<blocks, 256, 0, s>>>(a.ws, static_cast<uint16_t*>(a.C), mn, t.S);
+    else w4_splitk_reduce_kernel<false><<<blocks, 256, 0, s>>>(a.ws, static_cast<uint16_t*>(a.C), mn, t.S);
+    return check_launch(who);
+}
+
+// lhq_gemm_w4a16_bf16 with a workspace of ws_bytes at ws (ws_cap < 0: the
+// plan may use as much as it wants, the caller has checked that it fits).
+int gemm_w4a16_bf16_plan(const char* who, const uint16_t* A, const uint8_t* qweight, const uint16_t* scales,
+                         const uint32_t* zeros, uint16_t* C, int M, int N, int K, int G, void* ws,
+                         int64_t ws_cap, void* stream) {
+    if (int st = check_w4_shape(who, M, N, K, G)) return st;
+    LHQ_REQUIRE(qweight && scales && zeros && C && (A || M == 0), "%s: null pointer", who);
+    LHQ_REQUIRE(ws || ws_cap <= 0, "%s: null workspace with %lld bytes", who, static_cast<long long>(ws_cap));
+    if (M == 0) return LHQ_OK;
+    W4Args a = make_args(A, qweight, scales, zeros, C, M, N, K, G, 1.0f, 0.0f);
+    const TilePlan t = plan_thin(a, ws ? ws_cap : 0);
+    if (t.split) {
+        LHQ_REQUIRE((reinterpret_cast<uintptr_t>(ws) & 15) == 0, "%s: workspace not 16-byte aligned", who);
+        return launch_split(a, t, ws, as_stream(stream), who);
+    }
+    if (mma_applies(a, M, M)) return launch_mma<false>(a, M, 0, 1, as_stream(stream), who);
+    return launch_w4<false, true, false>(a, 1, as_stream(stream));
+}
+
 }  // namespace
 }  // namespace lhq
 
@@ -1727,6 +1881,20 @@ int lhq_gemm_w4a16_bf16(const uint16_t* A, const uint8_t* qweight, const uint16_
     W4Args a = make_args(A, qweight, scales, zeros, C, M, N, K, G, 1.0f, 0.0f);
     if (mma_applies(a, M, M)) return launch_mma<false>(a, M, 0, 1, as_stream(stream), "w4a16 prefill");
     return launch_w4<false, true, false>(a, 1, as_stream(stream));
+}
+
+int64_t lhq_gemm_w4a16_bf16_workspace_bytes(int M, int N, int K, int G) {
+    if (check_w4_shape("gemm_w4a16_bf16_workspace_bytes", M, N, K, G) || M == 0) return 0;
+    const W4Args a = make_args(nullptr, nullptr, nullptr, nullptr, nullptr, M, N, K, G, 1.0f, 0.0f);
+    return plan_thin(a, -1).ws_bytes;
+}
+
+int lhq_gemm_w4a16_bf16_ws(const uint16_t* A, const uint8_t* qweight, const uint16_t* scales,
+                           const uint32_t* zeros, uint16_t* C, int M, int N, int K, int G, void* workspace,
+                           int64_t workspace_bytes, void* stream) {
+    LHQ_REQUIRE(workspace_bytes >= 0, "gemm_w4a16_bf16_ws: negative workspace_bytes");
+    return gemm_w4a16_bf16_plan("gemm_w4a16_bf16_ws", A, qweight, scales, zeros, C, M, N, K, G, workspace,
+                                workspace ? workspace_bytes : 0, stream);
 }
 
 int lhq_gemm_w4a16_bf16_batched(const uint16_t* A, const uint8_t* qweight, const uint16_t* scales,

@@ -180,6 +180,26 @@ def gemm_w4a16(A: torch.Tensor, w: W4Weights, C: torch.Tensor | None = None,
     return C
 
 
+def w4a16_bf16_workspace(M: int, w: W4Weights) -> torch.Tensor | None:
+    """A device workspace of the size lhq_gemm_w4a16_bf16_ws asks for (None
+    when the shape runs without one)."""
+    n = lib().lhq_gemm_w4a16_bf16_workspace_bytes(M, w.N, w.K, w.G)
+    return empty((n,), np.uint8) if n > 0 else None
+
+
+def gemm_w4a16_bf16_ws(A: torch.Tensor, w: W4Weights, ws: torch.Tensor | None,
+                       C: torch.Tensor | None = None) -> torch.Tensor:
+    """gemm_w4a16_bf16 with a workspace (K split across workgroups where the
+    output grid is thin)."""
+    M = A.shape[0]
+    if C is None:
+        C = empty((M, w.N), np.int16)
+    nbytes = 0 if ws is None else ws.numel() * ws.element_size()
+    lib().call("lhq_gemm_w4a16_bf16_ws", P(A), P(w.qweight), P(w.scales), P(w.zeros), P(C),
+               M, w.N, w.K, w.G, P(ws), nbytes, stream())
+    return C
+
+
 def gemm_w4a16_bf16(A: torch.Tensor, w: W4Weights, C: torch.Tensor | None = None) -> torch.Tensor:
     """bf16 A [M,K] (int16 bits), asymmetric weights, bf16 C [M,N] (int16 bits)."""
     M = A.shape[0]

@@ -69,11 +69,16 @@ def test_per_row_bf16(oracle, ops, rows, dim):
     _eq(ops.host(s), s_w)
 
 
-@pytest.mark.parametrize("rows,cols", [(16, 32), (4096, 1000), (7, 3)])
+# 4 | cols: 16-byte loads; otherwise one column per thread.  Row counts span
+# one and many 64-row chunks of the max pass.
+@pytest.mark.parametrize("rows,cols", [(16, 32), (4096, 1000), (7, 3), (130, 14336), (65, 6), (200, 1001)])
 @pytest.mark.parametrize("kind", ["q8", "fp8"])
 def test_per_col(oracle, ops, rows, cols, kind):
     x = D.uniform((rows, cols), -1, 1, rows + cols)
-    x[:, 0] = 0.0
+    x[:, 0] = 0.0                                 # all-zero column -> scale 1
+    if cols > 2 and rows > 4:
+        x[:4, 1] = [np.nan, 0.25, -1.5, 1.0]      # NaN never wins; its code is 0
+        x[rows - 1, 2] = 40.0                     # the max in the last row chunk
     q_w, s_w = getattr(oracle, f"{kind}_quantize_per_col")(x)
     q = ops.empty((rows, cols), np.int8 if kind == "q8" else np.uint8)
     s = ops.empty((cols,), np.float32)
@@ -142,3 +147,41 @@ def test_q4a_groupwise(oracle, ops, K, N, G):
     d = ops.empty((K, N), np.float32)
     ops.run("lhq_q4a_dequantize_groupwise", p, s, z, d, K, N, G)
     _eq(ops.host(d), oracle.q4a_dequantize_groupwise(p_w, s_w, z_w, K, N, G))
+
+
+def test_per_col_config3_weights(oracle, ops):
+    """Config 3's weight quantization at full size (K=4096, N=14336, per
+    output channel), with a spike per column at a random row."""
+    K, N = 4096, 14336
+    w = D.normal((K, N), 0.02, 31)
+    w[D.rng(32).integers(0, K, N), np.arange(N)] = 0.5
+    q_w, s_w = oracle.q8_quantize_per_col(w)
+    q = ops.empty((K, N), np.int8)
+    s = ops.empty((N,), np.float32)
+    ops.run("lhq_q8_quantize_per_col", w, q, s, K, N)
+    _eq(ops.host(q), q_w)
+    _eq(ops.host(s), s_w)
+
+
+def test_per_col_unaligned_rows(oracle, ops):
+    """4 | cols but a source 4 bytes past a 16-byte boundary: the scalar
+    kernels, same bits."""
+    rows, cols = 70, 64
+    x = D.uniform((rows, cols), -2, 2, 33)
+    buf = ops.dev(np.concatenate([np.zeros(1, np.float32), x.ravel()]))
+    src = buf[1:]
+    assert src.data_ptr() % 16 == 4
+    q = ops.empty((rows, cols), np.int8)
+    s = ops.empty((cols,), np.float32)
+    ops.run("lhq_q8_quantize_per_col", src, q, s, rows, cols)
+    q_w, s_w = oracle.q8_quantize_per_col(x)
+    _eq(ops.host(q), q_w)
+    _eq(ops.host(s), s_w)
+
+
+def test_per_col_zero_rows(oracle, ops):
+    """rows = 0: every scale is 1 (the reference's max of nothing is 0)."""
+    s = ops.dev(np.full(9, 7.0, np.float32))
+    q = ops.empty((1,), np.int8)
+    ops.run("lhq_q8_quantize_per_col", ops.empty((1,), np.float32), q, s, 0, 9)
+    assert (ops.host(s) == 1.0).all()
