@@ -1777,7 +1777,10 @@ constexpr int kSplitMinKt = 4;  // K tiles per split at least
 // split, but (4096, 11008) 19.9 against 15.6 and (8192, 8192) 22.0 against
 // 17.0.  S brings the grid to about one workgroup per CU, with at least 4 K
 // tiles per split (M = 64, K = N = 8192: 48.5 us unsplit, 24.5 with 8
-// splits, 27.3 with 16).
+// splits, 27.3 with 16).  The plain 64 x 256 layout with a K split beat the
+// in-workgroup split layouts with a K split as well (M = 64, K = N = 8192:
+// 24.3 us against 24.3 and 25.1; K = 28672: 58.0 against 56.2 and 58.8;
+// M = 32, K = 8192, N = 57344: 69.5 against 97.2 and 112.2).
 TilePlan plan_thin(const W4Args& a, int64_t ws_cap) {
     TilePlan t;
     // (read on every call in a tuning build, so one process can sweep them)
@@ -1786,12 +1789,18 @@ TilePlan plan_thin(const W4Args& a, int64_t ws_cap) {
     const int env_l = tuning_knob("LHQ_W4_THIN_L", 0);     // force the layout (1..3)
     if (env_thin == 0 || a.M <= 16 || a.M > 64) return t;
     if (a.G < kW4TileK || a.K % kW4TileK != 0 || static_cast<int64_t>(a.M) * a.K >= (int64_t{1} << 31)) return t;
-    if (!mma_applies(a, a.M, a.M) && static_cast<int64_t>(a.K) * a.N < (int64_t{32} << 20)) return t;
+    const bool tile = mma_applies(a, a.M, a.M);
+    if (!tile && static_cast<int64_t>(a.K) * a.N < (int64_t{32} << 20)) return t;
     t.RB = a.M <= 32 ? 2 : 4;
     if (env_l >= 1 && env_l <= 3) t.L = env_l;
     if (t.L != 1) t.RB = 4;
     const int64_t wgs = static_cast<int64_t>(ceil_div(a.Nt, (t.L == 1 ? 4 : 2) * MM_CT)) * ceil_div(a.M, 16 * t.RB);
     const int cus = std::max(device_cus(), 1);
+    // 64-row blocks with a quarter of the CUs' worth of column groups or
+    // more: the ordinary launch's split-K layouts (K in two or four parts
+    // inside a workgroup) do as well or better (M = 64, K = 8192: N = 28672
+    // 57.2 us against 61.2 split, N = 57344 100.6 against 100.5)
+    if (env_s == 0 && env_l == 0 && tile && t.RB == 4 && 4 * wgs >= cus) return t;
     int S = static_cast<int>(std::min<int64_t>(ceil_div64(cus, wgs), std::max(1, a.Kt / kSplitMinKt)));
     if (env_s >= 1) S = std::min(env_s, a.Kt);
     const int64_t per_split = static_cast<int64_t>(a.M) * a.N * 4;
