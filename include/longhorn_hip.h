@@ -170,6 +170,19 @@ int64_t lhq_gemm_w4a16_bf16_workspace_bytes(int M, int N, int K, int group_size)
 int lhq_gemm_w4a16_bf16_ws(const uint16_t* A, const uint8_t* qweight, const uint16_t* scales,
                            const uint32_t* zeros, uint16_t* C, int M, int N, int K, int group_size,
                            void* workspace, int64_t workspace_bytes, void* stream);
+/* lhq_gemm_w4a16_bf16_ws for callers that cannot allocate (code under HIP
+ * graph capture, serving loops, harnesses that forbid hipMalloc); no
+ * counterpart in the reference.  It allocates nothing: the split-K partial
+ * sums go to a static 32 MiB device array of the library, one per GPU, held
+ * until the process ends, whose address is looked up once per device.  The
+ * split plan is lhq_gemm_w4a16_bf16_ws's with the workspace it asks for, so
+ * the results are bit-identical to that entry point's; a shape whose plan
+ * needs more than 32 MiB is rejected with LHQ_ERR_UNSUPPORTED (no shape up to
+ * 64 rows does today).  Calls that overlap on one GPU share the array and
+ * race: serialize them (one stream, or events). */
+int lhq_gemm_w4a16_bf16_noalloc(const uint16_t* A, const uint8_t* qweight, const uint16_t* scales,
+                                const uint32_t* zeros, uint16_t* C, int M, int N, int K,
+                                int group_size, void* stream);
 /* Uniform batch of independent W4A16 GEMMs (the gemm_batched contract,
  * gemm.cpp:59-67): A [batch,M,K], weights stacked with the per-matrix
  * strides lhq_w4_*_bytes, C [batch,M,N]. */

@@ -56,6 +56,7 @@ SIGNATURES = {
     "lhq_gemm_w4a16_bf16": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
     "lhq_gemm_w4a16_bf16_workspace_bytes": [_i, _i, _i, _i],
     "lhq_gemm_w4a16_bf16_ws": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p, _i64, _p],
+    "lhq_gemm_w4a16_bf16_noalloc": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
     "lhq_gemm_w4a16_bf16_batched": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p],
     "lhq_gemm_w4a16_bf16_grouped": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p],
     "lhq_gemm_w4a16_bf16_grouped_swiglu": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p],

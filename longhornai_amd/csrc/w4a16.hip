@@ -26,6 +26,7 @@
 // LDS in wave order, so results are deterministic.
 #include <algorithm>
 #include <cstdlib>
+#include <mutex>
 #include <type_traits>
 
 #include "common.hpp"
@@ -1866,6 +1867,44 @@ int gemm_w4a16_bf16_plan(const char* who, const uint16_t* A, const uint8_t* qwei
 }
 
 }  // namespace
+
+// The no-allocation entry point's split-K scratch: one array per device, in
+// the code object's zero-initialised device data (every GPU the library runs
+// on holds it until the process ends).  Host code never uses the array's
+// name as an address: it reaches each device's copy only through the
+// pointer hipGetSymbolAddress returns with that device current.  The plan
+// writes every partial sum it later reads, so nothing in it needs clearing
+// between calls; calls that overlap on one GPU share it and race.
+constexpr int64_t kNoAllocScratchBytes = int64_t{32} << 20;
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / 4];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's scratch address, looked up on the first call made on
+// that device and kept.
+int scratch_for_current_device(const char* who, void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return set_error(LHQ_ERR_HIP, "%s: hipGetDevice: %s", who, hipGetErrorString(e));
+    LHQ_SUPPORTED(dev >= 0 && dev < kMaxDevices, "%s: device %d beyond the %d this library tracks", who, dev,
+                  kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return set_error(LHQ_ERR_HIP, "%s: scratch address on device %d: %s", who, dev, hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return LHQ_OK;
+}
+
+}  // namespace
 }  // namespace lhq
 
 using namespace lhq;
@@ -1904,6 +1943,21 @@ int lhq_gemm_w4a16_bf16_ws(const uint16_t* A, const uint8_t* qweight, const uint
     LHQ_REQUIRE(workspace_bytes >= 0, "gemm_w4a16_bf16_ws: negative workspace_bytes");
     return gemm_w4a16_bf16_plan("gemm_w4a16_bf16_ws", A, qweight, scales, zeros, C, M, N, K, G, workspace,
                                 workspace ? workspace_bytes : 0, stream);
+}
+
+int lhq_gemm_w4a16_bf16_noalloc(const uint16_t* A, const uint8_t* qweight, const uint16_t* scales,
+                                const uint32_t* zeros, uint16_t* C, int M, int N, int K, int G, void* stream) {
+    const char* who = "gemm_w4a16_bf16_noalloc";
+    if (int st = check_w4_shape(who, M, N, K, G)) return st;
+    const int64_t need = lhq_gemm_w4a16_bf16_workspace_bytes(M, N, K, G);
+    LHQ_SUPPORTED(need <= kNoAllocScratchBytes,
+                  "%s: M=%d N=%d K=%d needs %lld bytes of split-K scratch, the static scratch holds %lld "
+                  "(use lhq_gemm_w4a16_bf16_ws with a larger workspace)",
+                  who, M, N, K, static_cast<long long>(need), static_cast<long long>(kNoAllocScratchBytes));
+    void* ws = nullptr;
+    if (need > 0)
+        if (int st = scratch_for_current_device(who, &ws)) return st;
+    return gemm_w4a16_bf16_plan(who, A, qweight, scales, zeros, C, M, N, K, G, ws, need, stream);
 }
 
 int lhq_gemm_w4a16_bf16_batched(const uint16_t* A, const uint8_t* qweight, const uint16_t* scales,

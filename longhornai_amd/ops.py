@@ -200,6 +200,14 @@ def gemm_w4a16_bf16_ws(A: torch.Tensor, w: W4Weights, ws: torch.Tensor | None,
     return C
 
 
+def gemm_w4a16_bf16_noalloc(A: torch.Tensor, w: W4Weights, C: torch.Tensor) -> torch.Tensor:
+    """gemm_w4a16_bf16_ws on the library's static scratch: allocates nothing."""
+    M = A.shape[0]
+    lib().call("lhq_gemm_w4a16_bf16_noalloc", P(A), P(w.qweight), P(w.scales), P(w.zeros), P(C),
+               M, w.N, w.K, w.G, stream())
+    return C
+
+
 def gemm_w4a16_bf16(A: torch.Tensor, w: W4Weights, C: torch.Tensor | None = None) -> torch.Tensor:
     """bf16 A [M,K] (int16 bits), asymmetric weights, bf16 C [M,N] (int16 bits)."""
     M = A.shape[0]
