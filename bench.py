@@ -25,7 +25,8 @@ prefill TOPS (% MFMA peak), 1 GPU".
 Timing: launches are captured into HIP graphs (torch.cuda.CUDAGraph drives
 hipStreamBeginCapture on the stream the kernels are launched on) so the
 timed region measures the GPU, not Python; HIP events bracket the region on
-that same stream.
+that same stream, opened behind a short spin kernel so that the host's
+submission of the graphs is not inside it.
 """
 from __future__ import annotations
 
@@ -121,6 +122,10 @@ class GraphTimer:
         ev0 = torch.cuda.Event(enable_timing=True)
         ev1 = torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
+        # A spin kernel (~0.5 ms) ahead of the opening event: the host
+        # submits the graphs while it runs, so the events bracket the GPU's
+        # execution of the steps and not the host's launch latency.
+        torch.cuda._sleep(1_000_000)
         ev0.record()
         self.run(steps)
         ev1.record()

@@ -156,7 +156,7 @@ int lhq_gemm_w4a16_bf16(const uint16_t* A, const uint8_t* qweight, const uint16_
                         int group_size, void* stream);
 /* lhq_gemm_w4a16_bf16 with a caller workspace (no reference counterpart:
  * the reference's CPU loop needs no partial sums).  Where the output grid
- * cannot fill the GPU (17 <= M <= 64 rows, group_size a multiple of 128,
+ * cannot fill the GPU (2 <= M <= 64 rows, group_size a multiple of 128,
  * and weights large enough for the tile kernel), K is split across
  * workgroups: each split writes fp32 partial sums to `workspace` and they
  * are added in split order into C (deterministic).  The split count is

@@ -1004,7 +1004,10 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512) void w4_decode_i8_kernel(W4Arg
 //   L = 2:  64 x 128 with K split in two, waves (ks, wn) in 2 x 2: half ks
 //           walks K tiles ks*ceil(Kt/2) .. and half 1 hands its accumulators
 //           to half 0 through LDS at the end (a fixed order: deterministic);
-//           twice the workgroups of L = 1 where those cannot fill the chip.
+//           twice the workgroups of L = 1 where those cannot fill the chip;
+//   L = 3:  64 x 128 with K split in four, eight waves (ks, wn) in 4 x 2;
+//   L = 4:  64 x 256 with K split in two, eight waves (ks, wn) in 2 x 4
+//           (split-K launches: two waves per SIMD on L = 1's grid).
 // A wave owns 64 rows x 64 columns (4 column tiles) as 4 x 4 blocks of
 // 16x16x32 MFMA accumulators in every layout.  Per 128-deep K tile:
 //   - the workgroup's activations (64 rows x 128 k per row group or K half)
@@ -1027,37 +1030,39 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512) void w4_decode_i8_kernel(W4Arg
 // (the activations are not zero-padded in LDS).
 // ---------------------------------------------------------------------------
 constexpr int MM_CT = 4;  // column tiles per wave
-// rows per workgroup tile: L == 0 ? 128 : 64; column tiles per workgroup:
-// (L == 1 ? 4 : 2) * MM_CT; K parts: 2 (L == 2) or 4 (L == 3, eight waves);
-// one activation buffer: 64 rows (L == 1), 128 (L == 0, 2) or 256 (L == 3)
-// of 128 k x 2 bytes
+// rows per workgroup tile: L == 0 ? 128 : 16 * RB; column tiles per
+// workgroup: (L == 1 || L == 4 ? 4 : 2) * MM_CT; K parts: 2 (L == 2, 4) or
+// 4 (L == 3); one activation buffer: 128 rows (L == 0) or one region of
+// 16 * RB rows per K part, of 128 k x 2 bytes
 
 #define LHQ_LDS_AS __attribute__((address_space(3)))
 
 // SK (split-K, plain launches only): grid.z is the K split instead of the
 // batch; the workgroup's K parts share its split's K range, and it writes
 // fp32 partial sums to p.ws[split][M][N] for w4_splitk_reduce_kernel to add
-// in split order.  RB (L == 1 only): 16-row blocks per wave, 64 rows at
-// RB = 4; RB = 2 serves up to 32 rows without the MFMAs of 64.
+// in split order.  RB (L != 0): 16-row blocks per wave, 64 rows at RB = 4;
+// RB = 1 or 2 serve up to 16 or 32 rows without the MFMAs of 64.
 template <int BPS, bool GBIG, bool GR, bool SWI, int L, bool SK = false, int RB = 4>
-__global__ __launch_bounds__(L == 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_kernel(W4Args p) {
-    static_assert(RB == 4 || (RB == 2 && L == 1 && !GR), "32-row blocks in the plain 64 x 256 layout only");
+__global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_kernel(W4Args p) {
+    static_assert(RB == 4 || (RB <= 2 && L != 0 && !GR), "16- and 32-row blocks on plain launches, not 128 x 128");
     static_assert(!SK || (!GR && !SWI), "split-K on plain launches only");
+    static_assert(L != 4 || SK, "the 8-wave 64 x 256 layout on split-K launches only");
     constexpr int SEGS = 4 / BPS;
-    constexpr int NW = (L == 3) ? 8 : 4;                   // waves
-    constexpr int NK = (L == 2) ? 2 : (L == 3) ? 4 : 1;  // K parts
-    constexpr int BM = (L == 0) ? 128 : 16 * RB, WN = (L == 1) ? 4 : 2;
-    constexpr int A_BYTES = ((L == 1) ? 16 * RB : (L == 3) ? 256 : 128) * kW4TileK * 2;
+    constexpr int NW = (L >= 3) ? 8 : 4;                                  // waves
+    constexpr int NK = (L == 2 || L == 4) ? 2 : (L == 3) ? 4 : 1;        // K parts
+    constexpr int BM = (L == 0) ? 128 : 16 * RB, WN = (L == 1 || L == 4) ? 4 : 2;
+    constexpr int RR = (L == 0) ? 64 : 16 * RB;                          // rows per LDS region
+    constexpr int A_BYTES = ((L == 0) ? 128 : NK * RR) * kW4TileK * 2;
     constexpr int DMA = A_BYTES / 1024 / NW;  // activation DMAs per wave per K tile
     extern __shared__ __attribute__((aligned(1024))) uint8_t mm_lds[];  // 2 x A_BYTES
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // this wave's LDS activation region (row group or K part), row group,
     // K part and column group
-    const int wr = (L == 1) ? 0 : (wave >> 1);
+    const int wr = (L == 1) ? 0 : (L == 4) ? (wave >> 2) : (wave >> 1);
     const int wm = (L == 0) ? wr : 0;
     const int ks = (NK > 1) ? wr : 0;
-    const int wn = (L == 1) ? wave : (wave & 1);
+    const int wn = (L == 1) ? wave : (L == 4) ? (wave & 3) : (wave & 1);
     // K tiles [kb, ke) of this workgroup (its split, or all of K), in NK
     // parts of kh tiles; this wave's part starts at kofs
     const int kb = SK ? static_cast<int>(blockIdx.z) * p.kps : 0;
@@ -1085,19 +1090,23 @@ __global__ __launch_bounds__(L == 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
     const uint16_t* A = static_cast<const uint16_t*>(p.A) + (GR ? 0 : z * p.a_bs);
     const int col = lane & 15;
 
-    // activation DMA q of this wave: chunk idx = (8*wave + q)*64 + lane is
-    // row idx >> 4, LDS slot idx & 15, global chunk slot ^ (row & 15);
-    // element offsets are 32-bit (the launcher bounds rows * K)
+    // activation DMA q of this wave: chunk idx = (DMA*wave + q)*64 + lane is
+    // LDS row idx >> 4, LDS slot idx & 15, global chunk slot ^ (row & 15);
+    // LDS row r lies in region r / RR, the region of the K part whose waves
+    // issue it (DMA*4 rows per wave); element offsets are 32-bit (the
+    // launcher bounds rows * K)
     // (a fixed bound: a bound that depends on a template parameter, with the
     // array captured by the lambdas below, makes hipcc's host pass drop the
     // kernel's launch stub without a diagnostic; entries past DMA are unused)
     static_assert(DMA >= 1 && DMA <= 8, "activation DMAs per wave");
+    static_assert(NK == 1 || (RR % (DMA * 4) == 0 && RR / (DMA * 4) == NW / NK),
+                  "each wave's DMA rows lie in its own K part's region");
     uint32_t a_off[8];
 #pragma unroll
     for (int q = 0; q < DMA; ++q) {
         const int idx = (DMA * wave + q) * 64 + lane;
-        const int r = idx >> 4, slot = idx & 15;  // LDS row r: region r >> 6 (this wave's, wr)
-        const int row = min(m0 + ((NK > 1) ? (r & 63) : r), m_end - 1);
+        const int r = idx >> 4, slot = idx & 15;  // LDS row r: region r / RR (this wave's, wr)
+        const int row = min(m0 + ((NK > 1) ? (r % RR) : r), m_end - 1);
         a_off[q] = static_cast<uint32_t>(row) * static_cast<uint32_t>(p.K) + static_cast<uint32_t>((slot ^ (r & 15)) * 8);
     }
     // this wave's column tiles (clamped to the last one) and their bases
@@ -1143,7 +1152,7 @@ __global__ __launch_bounds__(L == 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
     const u32x4_t m144 = {kM144Bf16x2, kM144Bf16x2, kM144Bf16x2, kM144Bf16x2};
     // fragment (row block i, k block j): LDS row 64*wr + 16*i + (lane & 15), k
     // chunk 4j + (lane >> 4), stored in slot chunk ^ (lane & 15)
-    const uint32_t a_frag = static_cast<uint32_t>((wr * 64 + col) * 256);
+    const uint32_t a_frag = static_cast<uint32_t>((wr * RR + col) * 256);
 
     // a wave whose 64 rows all lie past the block's last row (a ragged
     // group's tail block, or M <= 64) has nothing to compute; it still
@@ -1238,15 +1247,15 @@ __global__ __launch_bounds__(L == 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
         // K parts 1.. hand their accumulators to part 0 through LDS, which
         // adds them in part order (deterministic): after the barrier every
         // wave's loads have landed and no wave reads the activation buffers
-        // again.  (NK-1) * WN * 16 KiB fits the 2 * A_BYTES of LDS.
-        static_assert((NK - 1) * WN * 4 * MM_CT * 64 * 16 <= 2 * A_BYTES, "reduction area");
+        // again.  (NK-1) * WN * RB * 4 KiB fits the 2 * A_BYTES of LDS.
+        static_assert((NK - 1) * WN * RB * MM_CT * 64 * 16 <= 2 * A_BYTES, "reduction area");
         __syncthreads();
         f32x4_t* const red = reinterpret_cast<f32x4_t*>(mm_lds);
-        constexpr int RS = 4 * MM_CT * 64;  // f32x4 entries per wave's accumulators
+        constexpr int RS = RB * MM_CT * 64;  // f32x4 entries per wave's accumulators
         if (ks > 0) {
             f32x4_t* const mine = red + ((ks - 1) * WN + wn) * RS;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < RB; ++i)
 #pragma unroll
                 for (int c = 0; c < MM_CT; ++c) mine[(i * MM_CT + c) * 64 + lane] = acc[i][c];
         }
@@ -1256,7 +1265,7 @@ __global__ __launch_bounds__(L == 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
         for (int q = 1; q < NK; ++q) {
             const f32x4_t* const part = red + ((q - 1) * WN + wn) * RS;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < RB; ++i)
 #pragma unroll
                 for (int c = 0; c < MM_CT; ++c) {
                     const f32x4_t h = part[(i * MM_CT + c) * 64 + lane];
@@ -1320,24 +1329,31 @@ __global__ __launch_bounds__(L == 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
 }
 
 // C[m][n] = bf16(sum over s < S of ws[s][m][n]), the splits added in order
-// (deterministic); four consecutive elements per thread where 4 | MN.
+// (deterministic); four consecutive elements per thread where 4 | MN.  The
+// loads of eight splits are issued before any is added: a thread's loads
+// are independent, so it waits for the memory system once per eight splits
+// instead of once per split.
 template <bool VEC>
 __global__ void w4_splitk_reduce_kernel(const float* __restrict__ ws, uint16_t* __restrict__ C, int64_t mn, int S) {
+    constexpr int U = 8;
+    using V = std::conditional_t<VEC, f32x4_t, float>;
     const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * (VEC ? 4 : 1);
     if (i >= mn) return;
-    if constexpr (VEC) {
-        f32x4_t v = *reinterpret_cast<const f32x4_t*>(ws + i);
-        for (int s = 1; s < S; ++s) {
-            const f32x4_t w = *reinterpret_cast<const f32x4_t*>(ws + static_cast<int64_t>(s) * mn + i);
+    V v{};
+    for (int s0 = 0; s0 < S; s0 += U) {
+        V w[U];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) v[j] += w[j];
+        for (int u = 0; u < U; ++u)  // splits past S re-read the last one (not added)
+            w[u] = *reinterpret_cast<const V*>(ws + static_cast<int64_t>(min(s0 + u, S - 1)) * mn + i);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (s0 + u >= S) break;
+            if (s0 + u == 0) v = w[u];
+            else v += w[u];
         }
-        *reinterpret_cast<u32x2_t*>(C + i) = u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-    } else {
-        float v = ws[i];
-        for (int s = 1; s < S; ++s) v += ws[static_cast<int64_t>(s) * mn + i];
-        C[i] = f32_to_bf16(v);
     }
+    if constexpr (VEC) *reinterpret_cast<u32x2_t*>(C + i) = u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    else C[i] = f32_to_bf16(v);
 }
 
 // ---------------------------------------------------------------------------
@@ -1751,13 +1767,19 @@ int grouped_w4(const char* who, const uint16_t* A, const int32_t* offsets, const
 // ---------------------------------------------------------------------------
 // Thin grids: the tile kernel with K split across workgroups.
 //
-// At 17..64 rows the tile kernel's grid has ceil(N / 256) column groups --
+// At 2..64 rows the tile kernel's grid has ceil(N / 256) column groups --
 // 32 for N = 8192, far short of 256 CUs -- and each workgroup walks all of
 // K.  A plan here spreads K over S workgroups per output tile: each writes
 // fp32 partial sums of its K range to a workspace [S][M][N], and
 // w4_splitk_reduce_kernel adds them in split order into the bf16 output
-// (deterministic, whatever the schedule).  Up to 32 rows use 32-row blocks
-// (RB = 2), so they do not pay for the MFMAs of 64.
+// (deterministic, whatever the schedule).  Up to 16 or 32 rows use 16- or
+// 32-row blocks (RB = 1, 2), so they do not pay for the MFMAs of 64.
+// 2..16 rows run 16 x 128 tiles with K in two halves inside the workgroup
+// (L = 2).  Measured on MI355X (us, ordinary launch / split), (K, N) at 16
+// rows: (8192, 8192) 16.3 / 14.4, (28672, 8192) 50.2 / 30.8, (16384, 4096)
+// 18.7 / 15.5, (11008, 4096) 14.0 / 13.6, (4096, 11008) 13.2 / 12.6; at 8
+// rows (28672, 8192) 41.8 / 29.1 but (8192, 8192) 13.5 / 14.5; at 4 rows
+// (28672, 8192) 36.3 / 29.0 but (8192, 8192) 11.1 / 14.0.
 // ---------------------------------------------------------------------------
 struct TilePlan {
     bool split = false;  // false: the entry point's ordinary launch
@@ -1771,7 +1793,7 @@ struct TilePlan {
 constexpr int kSplitMinKt = 4;  // K tiles per split at least
 
 // ws_cap: the workspace bytes available (-1: as much as the plan wants).
-// A split applies to 17..64 rows where the tile kernel runs (G >= 128), and
+// A split applies to 2..64 rows where the tile kernel runs (G >= 128), and
 // where the ordinary launch would be the tile kernel or the weights are
 // large enough (K * N >= 32 Mi) that the 16-row kernel loses to it: measured
 // at M = 32, (K, N) = (4096, 4096) 9.2 us on the 16-row kernel against 12.5
@@ -1787,22 +1809,35 @@ TilePlan plan_thin(const W4Args& a, int64_t ws_cap) {
     // (read on every call in a tuning build, so one process can sweep them)
     const int env_thin = tuning_knob("LHQ_W4_THIN", -1);   // 0: never split
     const int env_s = tuning_knob("LHQ_W4_THIN_S", 0);     // force the split count
-    const int env_l = tuning_knob("LHQ_W4_THIN_L", 0);     // force the layout (1..3)
-    if (env_thin == 0 || a.M <= 16 || a.M > 64) return t;
+    const int env_l = tuning_knob("LHQ_W4_THIN_L", 0);     // force the layout (1..4)
+    if (env_thin == 0 || a.M < 2 || a.M > 64) return t;
     if (a.G < kW4TileK || a.K % kW4TileK != 0 || static_cast<int64_t>(a.M) * a.K >= (int64_t{1} << 31)) return t;
     const bool tile = mma_applies(a, a.M, a.M);
     if (!tile && static_cast<int64_t>(a.K) * a.N < (int64_t{32} << 20)) return t;
-    t.RB = a.M <= 32 ? 2 : 4;
-    if (env_l >= 1 && env_l <= 3) t.L = env_l;
-    if (t.L != 1) t.RB = 4;
-    const int64_t wgs = static_cast<int64_t>(ceil_div(a.Nt, (t.L == 1 ? 4 : 2) * MM_CT)) * ceil_div(a.M, 16 * t.RB);
+    t.RB = a.M <= 16 ? 1 : a.M <= 32 ? 2 : 4;
+    // 2..16 rows: 16 x 128 tiles with K in two halves inside the workgroup
+    // (L = 2), which reach the same grid as 16 x 256 tiles with half the
+    // splits, so half the partial-sum traffic
+    if (t.RB == 1) t.L = 2;
+    if (env_l >= 1 && env_l <= 4) t.L = env_l;
+    const int64_t wgs =
+        static_cast<int64_t>(ceil_div(a.Nt, (t.L == 1 || t.L == 4 ? 4 : 2) * MM_CT)) * ceil_div(a.M, 16 * t.RB);
     const int cus = std::max(device_cus(), 1);
     // 64-row blocks with a quarter of the CUs' worth of column groups or
     // more: the ordinary launch's split-K layouts (K in two or four parts
     // inside a workgroup) do as well or better (M = 64, K = 8192: N = 28672
     // 57.2 us against 61.2 split, N = 57344 100.6 against 100.5)
     if (env_s == 0 && env_l == 0 && tile && t.RB == 4 && 4 * wgs >= cus) return t;
-    int S = static_cast<int>(std::min<int64_t>(ceil_div64(cus, wgs), std::max(1, a.Kt / kSplitMinKt)));
+    // about one workgroup per CU, and for 16-row blocks at most 28 K tiles
+    // per split (16 rows, K = 28672: 8 splits 30.8 us, 6 34.3, 4 37.4)
+    const int64_t fill = ceil_div64(cus, wgs);
+    const int64_t want = (t.RB == 1) ? std::max<int64_t>(fill, ceil_div(a.Kt, 28)) : fill;
+    int S = static_cast<int>(std::min<int64_t>(want, std::max(1, a.Kt / kSplitMinKt)));
+    // 2..16 rows: the split costs about the same at any row count, the
+    // ordinary launch (decode or 16-row kernel) grows with the rows, so it
+    // takes a grid at most half full unsplit, three splits or more, and up
+    // to 8 rows K >= 16384 and N >= 8192
+    if (env_s == 0 && t.RB == 1 && (fill < 2 || S < 3 || (a.M <= 8 && (a.K < 16384 || a.N < 8192)))) return t;
     if (env_s >= 1) S = std::min(env_s, a.Kt);
     const int64_t per_split = static_cast<int64_t>(a.M) * a.N * 4;
     if (ws_cap >= 0) S = static_cast<int>(std::min<int64_t>(S, std::max<int64_t>(1, ws_cap / per_split)));
@@ -1819,9 +1854,10 @@ TilePlan plan_thin(const W4Args& a, int64_t ws_cap) {
 
 template <int L, int RB>
 void launch_split_rb(const W4Args& a, unsigned splits, hipStream_t s) {
-    constexpr size_t lds = 2 * ((L == 1) ? 16 * RB : (L == 3) ? 256 : 128) * kW4TileK * 2;
-    constexpr int threads = (L == 3) ? 512 : 256;
-    const dim3 grid(ceil_div(a.Nt, ((L == 1) ? 4 : 2) * MM_CT), ceil_div(a.M, 16 * RB), splits);
+    constexpr int NK = (L == 2 || L == 4) ? 2 : (L == 3) ? 4 : 1;
+    constexpr size_t lds = 2 * NK * 16 * RB * kW4TileK * 2;
+    constexpr int threads = (L >= 3) ? 512 : 256;
+    const dim3 grid(ceil_div(a.Nt, ((L == 1 || L == 4) ? 4 : 2) * MM_CT), ceil_div(a.M, 16 * RB), splits);
     if (a.gmul) {
         if constexpr (lds > 64 * 1024) allow_cu_lds<&w4_mma_kernel<4, true, false, false, L, true, RB>>();
         w4_mma_kernel<4, true, false, false, L, true, RB><<<grid, threads, lds, s>>>(a);
@@ -1831,13 +1867,34 @@ void launch_split_rb(const W4Args& a, unsigned splits, hipStream_t s) {
     }
 }
 
-int launch_split(W4Args a, const TilePlan& t, void* ws, hipStream_t s, const char* who) {
-    a.ws = static_cast<float*>(ws);
-    a.kps = t.kps;
+// the split launch's tile kernel (every layout with every row block in a
+// tuning build, where LHQ_W4_THIN_L forces them; the plan's forms otherwise)
+void launch_split_tiles(const W4Args& a, const TilePlan& t, hipStream_t s) {
+#ifdef LHQ_TUNING_KNOBS
+    if (t.L != 1) {
+        auto by_rb = [&](auto lc) {
+            constexpr int LL = decltype(lc)::value;
+            if (t.RB == 1) launch_split_rb<LL, 1>(a, t.S, s);
+            else if (t.RB == 2) launch_split_rb<LL, 2>(a, t.S, s);
+            else launch_split_rb<LL, 4>(a, t.S, s);
+        };
+        if (t.L == 2) by_rb(std::integral_constant<int, 2>{});
+        else if (t.L == 3) by_rb(std::integral_constant<int, 3>{});
+        else by_rb(std::integral_constant<int, 4>{});
+        return;
+    }
+#endif
     if (t.L == 3) launch_split_rb<3, 4>(a, t.S, s);
+    else if (t.L == 2 && t.RB == 1) launch_split_rb<2, 1>(a, t.S, s);
     else if (t.L == 2) launch_split_rb<2, 4>(a, t.S, s);
     else if (t.RB == 2) launch_split_rb<1, 2>(a, t.S, s);
     else launch_split_rb<1, 4>(a, t.S, s);
+}
+
+int launch_split(W4Args a, const TilePlan& t, void* ws, hipStream_t s, const char* who) {
+    a.ws = static_cast<float*>(ws);
+    a.kps = t.kps;
+    launch_split_tiles(a, t, s);
     if (int st = check_launch(who)) return st;
     const int64_t mn = static_cast<int64_t>(a.M) * a.N;
     const bool vec = mn % 4 == 0 && (reinterpret_cast<uintptr_t>(a.C) & 7) == 0;

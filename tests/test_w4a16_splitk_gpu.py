@@ -1,9 +1,10 @@
 """W4A16 with a caller workspace (lhq_gemm_w4a16_bf16_ws) vs the CPU oracle.
 
-At 17..64 rows the tile kernel's output grid cannot fill the GPU, so K is
+At 2..64 rows the tile kernel's output grid cannot fill the GPU, so K is
 split across workgroups: each split writes fp32 partial sums to the
-workspace and a second kernel adds them in split order.  Checked here: both
-row-block forms (32 and 64 rows per wave), ragged M and N, split boundaries
+workspace and a second kernel adds them in split order.  Checked here: the
+three row-block forms (16, 32 and 64 rows per wave; 16-row blocks with K in
+two halves inside the workgroup), ragged M and N, split boundaries
 inside scale groups, G = 128, 256 and 384, the workspace-size rules (none,
 smaller than asked, exactly asked) and bit-for-bit determinism across calls.  Bars as the
 other bf16 tests: relative Frobenius <= 1e-2, and > 99.9% of elements within
@@ -38,9 +39,13 @@ def _case(oracle, ops, M, K, N, G, seed):
     return ops.dev(A), w, want
 
 
-# 17..64 rows on the tile kernel, where the ordinary launch is the tile
-# kernel or the weights hold K * N >= 32 Mi values
+# 2..64 rows on the tile kernel, where the ordinary launch is the tile
+# kernel or the weights hold K * N >= 32 Mi values (2..16 rows: at least
+# three splits and larger weights the fewer the rows)
 @pytest.mark.parametrize("M,K,N,G", [
+    (16, 8192, 8192, 128),    # 16-row blocks, 4 splits
+    (11, 8192, 10248, 256),   # 16-row blocks, 11 live rows, N % 16 != 0, G = 256
+    (3, 16384, 8192, 128),    # 3 rows, K >= 16384
     (17, 4096, 8200, 128),    # 32-row blocks, N % 16 != 0
     (32, 2048, 16400, 256),   # G = 256: two K tiles per scale group
     (48, 2048, 1024, 128),    # 64-row blocks, 48 live rows
@@ -89,7 +94,12 @@ def test_splitk_workspace_bytes_rules(ops):
     assert f(64, 4096, 8192, 64) == 0        # the tile kernel needs G >= 128
     assert f(64, 4160, 8192, 64) == 0        # (and so K % 128 == 0)
     assert f(0, 8192, 8192, 128) == 0
-    assert f(16, 8192, 8192, 128) == 0       # up to 16 rows: the 16-row and decode kernels
+    assert f(16, 8192, 8192, 128) == 4 * 16 * 8192 * 4   # 16-row blocks, 4 splits
+    assert f(16, 8192, 57344, 128) == 0      # 2 splits would not pay at 16 rows
+    assert f(8, 8192, 8192, 128) == 0        # nor K < 16384 at 8 rows or fewer
+    assert f(8, 28672, 8192, 128) > 0
+    assert f(12, 4096, 4096, 128) == 0       # small weights
+    assert f(4, 16384, 4096, 128) == 0       # (up to 8 rows, N < 8192)
     assert f(32, 4096, 4096, 128) == 0       # small weights: the 16-row kernel
     assert f(32, 4096, 8192, 128) > 0
     assert f(64, 8192, 8192, 128) == 8 * 64 * 8192 * 4   # 8 splits of 8 K tiles
