@@ -449,6 +449,36 @@ def bench_w8a8(ops, M, K, N, steps, warmup, seed=0):
     return res
 
 
+def mfma_ceiling(ops, steps: int = 5, warmup: int = 2):
+    """The matrix cores' sustained rate with every CU loaded: a probe kernel
+    of back-to-back independent MFMAs on register operands (no memory
+    traffic), timed like the legs.  The GEMM legs' MFMA fractions are read
+    against this as well as against the published peaks."""
+    import numpy as np
+    import torch
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    blocks = 8 * cus
+    sink = ops.empty((blocks,), np.int32)
+    out = {}
+    for kind, name, per_op, iters, peak in ((0, "int8_32x32x32", 65536, 2800, INT8_PEAK_TOPS),
+                                            (3, "int8_16x16x64", 32768, 5600, INT8_PEAK_TOPS),
+                                            (1, "bf16_16x16x32", 16384, 5600, BF16_PEAK_TFLOPS),
+                                            (2, "bf16_32x32x16", 32768, 2800, BF16_PEAK_TFLOPS),
+                                            (4, "bf16_16x16x32_valu2", 16384, 5600, BF16_PEAK_TFLOPS),
+                                            (5, "bf16_16x16x32_valu4", 16384, 5600, BF16_PEAK_TFLOPS)):
+        def launch(i, kind=kind, iters=iters):
+            st = ops.lib().cdll.lhq_probe_mfma_rate(kind, blocks, iters, sink.data_ptr(), ops.stream())
+            if st:
+                raise RuntimeError(f"lhq_probe_mfma_rate: {ops.lib().last_error()}")
+        ms, _ = GraphTimer(launch, 1, chunk=steps).time(steps, warmup)
+        per_launch = blocks * 4 * iters * 4 * per_op
+        rate = per_launch * steps / (ms * 1e-3) / 1e12
+        out[name] = {"value": round(rate, 1), "unit": "TOPS" if kind in (0, 3) else "TFLOPS", "peak": peak,
+                     "frac": round(rate / peak, 4), "us_per_launch": round(ms * 1e3 / steps, 1)}
+    del sink
+    return out
+
+
 def copy_probe(nbytes: int = 1 << 30, reps: int = 5) -> None:
     """A plain device copy of known size: the calibration kernel for the
     FETCH_SIZE / WRITE_SIZE counters (each launch reads and writes nbytes)."""
@@ -641,7 +671,7 @@ def main() -> int:
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a 1 GiB device copy (PMC calibration kernel)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the W4A16 prefill and MoE legs")
-    ap.add_argument("--only", choices=["w4a16", "w8a8", "prefill", "moe", "fp8", "configs"], default=None,
+    ap.add_argument("--only", choices=["w4a16", "w8a8", "prefill", "moe", "fp8", "configs", "mfma"], default=None,
                     help="run one leg only (profiling); prints that leg's summary, not the bench line")
     ap.add_argument("--moe-tokens", type=int, default=512,
                     help="tokens of the --only moe leg (512 = config 4; 1-4 run the grouped decode kernel)")
@@ -678,6 +708,9 @@ def main() -> int:
                 f"({100 * r['mfma_frac']:.1f}% of fp8 peak)")
             print(json.dumps(r), flush=True)
         return 0
+    if args.only == "mfma":
+        print(json.dumps({"leg": "mfma_ceiling", **mfma_ceiling(ops)}), flush=True)
+        return 0
     if args.only == "configs":
         print(json.dumps({"leg": "w4a16_config2", "shapes": config_sweep(ops, "config 2", *CONFIG2)}), flush=True)
         print(json.dumps({"leg": "w4a16_config5", "shapes": config_sweep(ops, "config 5", *CONFIG5)}), flush=True)
@@ -707,6 +740,16 @@ def main() -> int:
                 f"act quant {r['act_quant_us']:.1f} us ({r['act_quant_gbs']:.0f} GB/s); "
                 f"weight quant (per column) {r['weight_quant_us']:.1f} us ({r['weight_quant_gbs']:.0f} GB/s)")
             w8.append(r)
+
+    ceiling = None
+    if not args.no_w8a8:
+        ceiling = mfma_ceiling(ops)
+        c8 = ceiling["int8_32x32x32"]
+        log(f"matrix-core ceiling (register-only MFMA probe, all CUs): int8 {c8['value']:.0f} TOPS "
+            f"({100 * c8['frac']:.1f}% of peak); bf16 {ceiling['bf16_16x16x32']['value']:.0f} TFLOPS "
+            f"({100 * ceiling['bf16_16x16x32']['frac']:.1f}%)")
+        for r in w8:
+            log(f"  w8a8 M={r['M']}: {100 * r['tops'] / c8['value']:.1f}% of the sustained int8 rate")
 
     fp8 = []
     if not args.no_w8a8:
@@ -755,8 +798,10 @@ def main() -> int:
             {"M": r["M"], "K": r["K"], "N": r["N"], "us_per_call": round(r["us_per_call"], 2),
              "value": round(r["tops"], 1), "unit": "TOPS", "peak": INT8_PEAK_TOPS,
              "frac": round(r["mfma_frac"], 4), "act_quant_us": round(r["act_quant_us"], 2),
-             "weight_quant_us": round(r["weight_quant_us"], 2), "weight_quant_gbs": round(r["weight_quant_gbs"], 1)}
+             "weight_quant_us": round(r["weight_quant_us"], 2), "weight_quant_gbs": round(r["weight_quant_gbs"], 1),
+             "frac_of_sustained": (round(r["tops"] / ceiling["int8_32x32x32"]["value"], 4) if ceiling else None)}
             for r in w8],
+        "mfma_ceiling": ceiling,
         "w8a8_cpu_baseline": cpu_w8,
         "fp8_gemm": fp8,
         "w4a16_prefill": pre,

@@ -18,10 +18,116 @@ __global__ __launch_bounds__(256) void bf16_selftest_kernel(uint32_t base, unsig
     if (bad1) atomicAdd(&counts[(x1 & 0x7fffffffu) > 0x7f800000u ? 1 : 0], 1ull);
 }
 
+// Matrix-core rate probe: each wave runs `iters` rounds of four
+// independent MFMA chains on register operands, with no memory traffic in
+// the loop, so the launch's duration gives the matrix cores' sustained rate
+// with every CU loaded (the clock and power limits included).  One result
+// per workgroup goes to sink (keeps the chains live).
+// KIND 0: v_mfma_i32_32x32x32_i8 (the W8A8 kernel's instruction),
+// KIND 1: v_mfma_f32_16x16x32_bf16 (the W4A16 kernels' instruction),
+// KIND 2: v_mfma_f32_32x32x16_bf16, KIND 3: v_mfma_i32_16x16x64_i8;
+// KIND 4, 5: KIND 1's loop with 2 or 4 independent integer VALU operations
+// per MFMA (does the VALU work hide under the matrix core's?).
+template <int KIND>
+__global__ __launch_bounds__(256) void mfma_rate_kernel(int iters, int* sink) {
+    const uint32_t t = threadIdx.x;
+    // bf16 operands are small normal numbers (1 + t/2^7 and 1 - t/2^8 in
+    // the high half): no Inf, NaN or subnormal on any path
+    constexpr bool I8 = KIND == 0 || KIND == 3;
+    const uint32_t ea = I8 ? (t * 0x01010101u) ^ 0x5a3c96e1u : 0x3f803f80u + (t & 0x7fu) * 0x00010001u;
+    const uint32_t eb = I8 ? (t * 0x00ff00ffu) ^ 0x1e2d3c4bu : 0x3f7f3f7fu - (t & 0x7fu) * 0x00010000u;
+    const u32x4_t a = {ea, ea + 1u, ea ^ 3u, ea + 7u}, b = {eb, eb ^ 5u, eb + 2u, eb ^ 9u};
+    if constexpr (KIND == 0) {
+        i32x16_t c0 = {}, c1 = {}, c2 = {}, c3 = {};
+        for (int i = 0; i < iters; ++i) {
+            c0 = mfma_i8_32x32x32(a, b, c0);
+            c1 = mfma_i8_32x32x32(b, a, c1);
+            c2 = mfma_i8_32x32x32(a, a, c2);
+            c3 = mfma_i8_32x32x32(b, b, c3);
+        }
+        int r = 0;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) r += c0[j] ^ c1[j] ^ c2[j] ^ c3[j];
+        if (t == 0) sink[blockIdx.x] = r;
+    } else if constexpr (KIND == 2) {
+        f32x16_t c0 = {}, c1 = {}, c2 = {}, c3 = {};
+        for (int i = 0; i < iters; ++i) {
+            c0 = mfma_bf16_32x32x16(a, b, c0);
+            c1 = mfma_bf16_32x32x16(b, a, c1);
+            c2 = mfma_bf16_32x32x16(a, a, c2);
+            c3 = mfma_bf16_32x32x16(b, b, c3);
+        }
+        float r = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) r += c0[j] + c1[j] + c2[j] + c3[j];
+        if (t == 0) sink[blockIdx.x] = __float_as_int(r);
+    } else if constexpr (KIND == 3) {
+        i32x4_t c0 = {}, c1 = {}, c2 = {}, c3 = {};
+        for (int i = 0; i < iters; ++i) {
+            c0 = mfma_i8_16x16x64(a, b, c0);
+            c1 = mfma_i8_16x16x64(b, a, c1);
+            c2 = mfma_i8_16x16x64(a, a, c2);
+            c3 = mfma_i8_16x16x64(b, b, c3);
+        }
+        int r = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r += c0[j] ^ c1[j] ^ c2[j] ^ c3[j];
+        if (t == 0) sink[blockIdx.x] = r;
+    } else if constexpr (KIND == 4 || KIND == 5) {
+        constexpr int NV = KIND == 4 ? 2 : 4;  // VALU operations per MFMA
+        f32x4_t c0 = {}, c1 = {}, c2 = {}, c3 = {};
+        uint32_t v[4] = {ea, eb, ea ^ eb, ea + eb};
+        for (int i = 0; i < iters; ++i) {
+            c0 = mfma_bf16_16x16x32(a, b, c0);
+#pragma unroll
+            for (int q = 0; q < NV; ++q) v[q] = __builtin_amdgcn_perm(v[q], v[(q + 1) & 3], 0x05010400u) + 0x01010101u;
+            c1 = mfma_bf16_16x16x32(b, a, c1);
+#pragma unroll
+            for (int q = 0; q < NV; ++q) v[q] = __builtin_amdgcn_perm(v[q], v[(q + 2) & 3], 0x07030602u) ^ 0x80808080u;
+            c2 = mfma_bf16_16x16x32(a, a, c2);
+#pragma unroll
+            for (int q = 0; q < NV; ++q) v[q] = __builtin_amdgcn_perm(v[q], v[(q + 3) & 3], 0x05040100u) + 0x00ff00ffu;
+            c3 = mfma_bf16_16x16x32(b, b, c3);
+#pragma unroll
+            for (int q = 0; q < NV; ++q) v[q] = __builtin_amdgcn_perm(v[q], v[(q + 1) & 3], 0x07060302u) ^ 0x0f0f0f0fu;
+        }
+        float r = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r += c0[j] + c1[j] + c2[j] + c3[j];
+        if (t == 0) sink[blockIdx.x] = __float_as_int(r) ^ static_cast<int>(v[0] ^ v[1] ^ v[2] ^ v[3]);
+    } else {
+        f32x4_t c0 = {}, c1 = {}, c2 = {}, c3 = {};
+        for (int i = 0; i < iters; ++i) {
+            c0 = mfma_bf16_16x16x32(a, b, c0);
+            c1 = mfma_bf16_16x16x32(b, a, c1);
+            c2 = mfma_bf16_16x16x32(a, a, c2);
+            c3 = mfma_bf16_16x16x32(b, b, c3);
+        }
+        float r = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) r += c0[j] + c1[j] + c2[j] + c3[j];
+        if (t == 0) sink[blockIdx.x] = __float_as_int(r);
+    }
+}
+
 }  // namespace
 }  // namespace lhq
 
 using namespace lhq;
+
+extern "C" int lhq_probe_mfma_rate(int kind, int blocks, int iters, int* sink, void* stream) {
+    LHQ_REQUIRE(sink, "probe_mfma_rate: null sink");
+    LHQ_REQUIRE(kind >= 0 && kind <= 5, "probe_mfma_rate: kind %d (0..5)", kind);
+    LHQ_REQUIRE(blocks >= 1 && iters >= 1, "probe_mfma_rate: blocks %d, iters %d", blocks, iters);
+    hipStream_t s = as_stream(stream);
+    if (kind == 0) mfma_rate_kernel<0><<<blocks, 256, 0, s>>>(iters, sink);
+    else if (kind == 1) mfma_rate_kernel<1><<<blocks, 256, 0, s>>>(iters, sink);
+    else if (kind == 2) mfma_rate_kernel<2><<<blocks, 256, 0, s>>>(iters, sink);
+    else if (kind == 3) mfma_rate_kernel<3><<<blocks, 256, 0, s>>>(iters, sink);
+    else if (kind == 4) mfma_rate_kernel<4><<<blocks, 256, 0, s>>>(iters, sink);
+    else mfma_rate_kernel<5><<<blocks, 256, 0, s>>>(iters, sink);
+    return check_launch("probe_mfma_rate");
+}
 
 extern "C" int lhq_selftest_bf16(unsigned long long* counts, void* stream) {
     LHQ_REQUIRE(counts, "selftest_bf16: null pointer");

@@ -19,3 +19,16 @@ def test_bf16_convert_matches_reference_rule_exhaustively(lib):
     torch.cuda.synchronize()
     non_nan, nan = counts.cpu().tolist()
     assert non_nan == 0 and nan == 0, f"mismatches: {non_nan} non-NaN, {nan} NaN"
+
+
+def test_mfma_rate_probe_runs_and_rejects_bad_arguments(lib):
+    """The matrix-core rate probe (bench.py's ceiling leg): a small launch of
+    each kind completes and writes one value per workgroup; an unknown kind
+    is refused before any launch."""
+    import torch
+    from longhornai_amd import ops
+    sink = torch.full((16,), -1, dtype=torch.int32, device="cuda")
+    for kind in range(6):
+        lib.call("lhq_probe_mfma_rate", kind, 16, 8, sink.data_ptr(), ops.stream())
+    torch.cuda.synchronize()
+    assert lib.status("lhq_probe_mfma_rate", 6, 16, 8, sink.data_ptr(), ops.stream()) != 0
