@@ -1172,6 +1172,12 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
         // xs = -144 * sum_k x (the MFMA against a -144 operand), per row
         // block; it seeds every t chain of the K tile (below)
         static_assert(SEGS == 1, "one scale segment per K tile");
+        const int g = group_of_c<BPS, GBIG>(kt, 0, p.gmul);
+        // 16 - z of column tile c in every byte (a byte broadcast, not a
+        // multiply: v_mul_lo_u32 issues at a quarter of the VALU rate)
+        auto zero_bytes = [&](int c) {
+            return __builtin_amdgcn_perm(0u, 16u - ((R.zw[c] >> (4 * (g & 7))) & 15u), 0u);
+        };
         f32x4_t xs[RB];
 #pragma unroll
         for (int i = 0; i < RB; ++i) {
@@ -1195,8 +1201,7 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
         };
 #pragma unroll
         for (int c = 0; c < MM_CT; ++c) {
-            const int g = group_of_c<BPS, GBIG>(kt, 0, p.gmul);
-            const uint32_t zb = (16u - ((R.zw[c] >> (4 * (g & 7))) & 15u)) * 0x01010101u;
+            const uint32_t zb = zero_bytes(c);
             u32x4_t b[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) b[j] = w4_operand_z(R.w[c][j], zb);
