@@ -191,9 +191,14 @@ __device__ __forceinline__ float swiglu(float g, float u) { return g / (1.0f + e
 // WAVES waves owns T column tiles and 16 rows; wave w walks its share of the
 // K tiles.  BPS = 32-wide k blocks per scale segment (min(G,128)/32).
 // ---------------------------------------------------------------------------
-template <bool F32A, bool ASYM, bool F32C, int T, int WAVES, int BPS, bool GROUPED, bool SWI = false>
+// PIPE (bf16 activations, plain launches of one or two column tiles per
+// workgroup): the K loop keeps the next tile's loads in flight while the
+// current tile is consumed; its extra registers cost occupancy, which the
+// many-workgroup grouped and wide launches need more.
+template <bool F32A, bool ASYM, bool F32C, int T, int WAVES, int BPS, bool GROUPED, bool SWI = false, bool PIPE = false>
 __global__ __launch_bounds__(64 * WAVES) void w4_gemv_kernel(W4Args p) {
     static_assert(!SWI || ((T == 2 || T == 4 || T == 8) && !F32C), "SwiGLU pairs the column tiles of a workgroup");
+    static_assert(!PIPE || (!F32A && !GROUPED && !SWI && T <= 2), "pipelined K loop: plain bf16 launches of 1-2 tiles");
     constexpr int SEGS = 4 / BPS;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -230,51 +235,166 @@ __global__ __launch_bounds__(64 * WAVES) void w4_gemv_kernel(W4Args p) {
     for (int t = 0; t < T; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     const u32x4_t ones = {kOnesBf16x2, kOnesBf16x2, kOnesBf16x2, kOnesBf16x2};
 
-    for (int kt = kb; kt < ke; ++kt) {
-        u32x4_t w[T];
+    if constexpr (PIPE) {
+        // The K tiles run in passes of P tiles whose loads (weights,
+        // activations, scales, zero words) are all issued before any is
+        // used, and the next pass's loads are in flight while the current
+        // pass is consumed, so a wave waits for memory once per pass instead
+        // of once per tile.  Every load is unconditional: tiles past this
+        // wave's range re-read its last tile (never consumed), rows past the
+        // block's end read its last row (their outputs are not stored; an
+        // output row depends on its own activation row only), and k past K
+        // reads the row's last 8 elements, zeroed at use.  One tile per pass
+        // measured faster than two (M=8, K=N=8192: 10.6 against 11.1 us),
+        // which hold more registers.
+        constexpr int P = 1;
+        constexpr int NZ = ASYM ? 1 : 0;
+        struct Pass {
+            u32x4_t w[P][T];
+            u32x4_t a[P][4];
+            uint32_t sr[P][T][SEGS];
+            uint32_t zw[P][T][NZ > 0 ? SEGS : 1];
+        };
+        const int64_t arow = static_cast<int64_t>(min(row, m_end - 1)) * p.K;
+        auto issue = [&](Pass& Q, int kt0) {
 #pragma unroll
-        for (int t = 0; t < T; ++t)
-            w[t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(
-                qw + ((static_cast<int64_t>(ntc[t]) * p.Kt + kt) * 64 + lane) * 16));
-        u32x4_t ah[4], al[4];
+            for (int i = 0; i < P; ++i) {
+                const int kt = min(kt0 + i, ke - 1);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int k = kt * kW4TileK + 32 * j + 8 * (lane >> 4);
-            load_a8<F32A>(A, static_cast<int64_t>(row) * p.K + k, row_ok && k < p.K, ah[j], al[j]);
-        }
+                for (int t = 0; t < T; ++t)
+                    Q.w[i][t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(
+                        qw + ((static_cast<int64_t>(ntc[t]) * p.Kt + kt) * 64 + lane) * 16));
 #pragma unroll
-        for (int s = 0; s < SEGS; ++s) {
-            f32x4_t xs = {0.f, 0.f, 0.f, 0.f};
+                for (int j = 0; j < 4; ++j) {
+                    const int k = min(kt * kW4TileK + 32 * j + 8 * (lane >> 4), p.K - 8);
+                    Q.a[i][j] = *reinterpret_cast<const u32x4_t*>(static_cast<const uint16_t*>(static_cast<const void*>(A)) +
+                                                                  (arow + k));
+                }
 #pragma unroll
-            for (int jj = 0; jj < BPS; ++jj) {
-                const int j = s * BPS + jj;
-                xs = mfma_bf16_16x16x32(ah[j], ones, xs);
-                if constexpr (F32A) xs = mfma_bf16_16x16x32(al[j], ones, xs);
+                for (int s2 = 0; s2 < SEGS; ++s2) {
+                    const int g = (BPS < 4) ? min(group_of<BPS>(kt, s2, p.gmul), p.NG - 1) : group_of<BPS>(kt, s2, p.gmul);
+#pragma unroll
+                    for (int t = 0; t < T; ++t) {
+                        const int64_t si = (static_cast<int64_t>(ntc[t]) * p.NG + g) * 16 + col;
+                        if constexpr (ASYM) {
+                            Q.sr[i][t][s2] = static_cast<const uint16_t*>(scales)[si];
+                            Q.zw[i][t][s2] = zeros[(static_cast<int64_t>(ntc[t]) * p.NG8 + (g >> 3)) * 16 + col];
+                        } else {
+                            Q.sr[i][t][s2] = static_cast<const uint32_t*>(scales)[si];
+                        }
+                    }
+                }
             }
-            const int g = (BPS < 4) ? min(group_of<BPS>(kt, s, p.gmul), p.NG - 1) : group_of<BPS>(kt, s, p.gmul);
+        };
+        // tile i of pass Q, K tile kt
+        auto consume1 = [&](const Pass& Q, int i, int kt) {
+            u32x4_t ah[4];
 #pragma unroll
-            for (int t = 0; t < T; ++t) {
-                f32x4_t acc_t = {0.f, 0.f, 0.f, 0.f};
+            for (int j = 0; j < 4; ++j) ah[j] = Q.a[i][j];
+            if (kt == p.Kt - 1 && (p.K & (kW4TileK - 1))) {
+                // the zero padding of the last K tile (uniform branch)
 #pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (kt * kW4TileK + 32 * j + 8 * (lane >> 4) >= p.K) ah[j] = u32x4_t{0, 0, 0, 0};
+            }
+#pragma unroll
+            for (int s2 = 0; s2 < SEGS; ++s2) {
+                f32x4_t xs = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int jj = 0; jj < BPS; ++jj) xs = mfma_bf16_16x16x32(ah[s2 * BPS + jj], ones, xs);
+                const int g = (BPS < 4) ? min(group_of<BPS>(kt, s2, p.gmul), p.NG - 1) : group_of<BPS>(kt, s2, p.gmul);
+#pragma unroll
+                for (int t = 0; t < T; ++t) {
+                    f32x4_t acc_t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int jj = 0; jj < BPS; ++jj) {
+                        const int j = s2 * BPS + jj;
+                        acc_t = mfma_bf16_16x16x32(ah[j], w4_operand(Q.w[i][t][j]), acc_t);
+                    }
+                    float sc, zc;
+                    if constexpr (ASYM) {
+                        sc = f16_to_f32(static_cast<uint16_t>(Q.sr[i][t][s2]));
+                        zc = kW4Bias + static_cast<float>((Q.zw[i][t][s2] >> (4 * (g & 7))) & 15u);
+                    } else {
+                        sc = __uint_as_float(Q.sr[i][t][s2]);
+                        zc = kW4Bias + 8.0f;  // implied zero point 8
+                    }
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        acc[t][r] = __builtin_fmaf(sc, __builtin_fmaf(-zc, xs[r], acc_t[r]), acc[t][r]);
+                }
+            }
+        };
+        auto consume = [&](const Pass& Q, int kt0) {
+#pragma unroll
+            for (int i = 0; i < P; ++i)
+                if (kt0 + i < ke) consume1(Q, i, kt0 + i);
+        };
+        if (kb < ke) {
+            Pass pa, pb;
+            issue(pa, kb);
+            int k0 = kb;
+            for (; k0 + 2 * P < ke; k0 += 2 * P) {
+                issue(pb, k0 + P);
+                consume(pa, k0);
+                issue(pa, k0 + 2 * P);
+                consume(pb, k0 + P);
+            }
+            if (k0 + P < ke) {
+                issue(pb, k0 + P);
+                consume(pa, k0);
+                consume(pb, k0 + P);
+            } else {
+                consume(pa, k0);
+            }
+        }
+    } else {
+        for (int kt = kb; kt < ke; ++kt) {
+            u32x4_t w[T];
+    #pragma unroll
+            for (int t = 0; t < T; ++t)
+                w[t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(
+                    qw + ((static_cast<int64_t>(ntc[t]) * p.Kt + kt) * 64 + lane) * 16));
+            u32x4_t ah[4], al[4];
+    #pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int k = kt * kW4TileK + 32 * j + 8 * (lane >> 4);
+                load_a8<F32A>(A, static_cast<int64_t>(row) * p.K + k, row_ok && k < p.K, ah[j], al[j]);
+            }
+    #pragma unroll
+            for (int s = 0; s < SEGS; ++s) {
+                f32x4_t xs = {0.f, 0.f, 0.f, 0.f};
+    #pragma unroll
                 for (int jj = 0; jj < BPS; ++jj) {
                     const int j = s * BPS + jj;
-                    const u32x4_t b = w4_operand(w[t][j]);
-                    acc_t = mfma_bf16_16x16x32(ah[j], b, acc_t);
-                    if constexpr (F32A) acc_t = mfma_bf16_16x16x32(al[j], b, acc_t);
+                    xs = mfma_bf16_16x16x32(ah[j], ones, xs);
+                    if constexpr (F32A) xs = mfma_bf16_16x16x32(al[j], ones, xs);
                 }
-                const int64_t si = (static_cast<int64_t>(ntc[t]) * p.NG + g) * 16 + col;
-                float sc, zc;
-                if constexpr (ASYM) {
-                    sc = f16_to_f32(static_cast<const uint16_t*>(scales)[si]);
-                    const uint32_t zw = zeros[(static_cast<int64_t>(ntc[t]) * p.NG8 + (g >> 3)) * 16 + col];
-                    zc = kW4Bias + static_cast<float>((zw >> (4 * (g & 7))) & 15u);
-                } else {
-                    sc = static_cast<const float*>(scales)[si];
-                    zc = kW4Bias + 8.0f;  // implied zero point 8
+                const int g = (BPS < 4) ? min(group_of<BPS>(kt, s, p.gmul), p.NG - 1) : group_of<BPS>(kt, s, p.gmul);
+    #pragma unroll
+                for (int t = 0; t < T; ++t) {
+                    f32x4_t acc_t = {0.f, 0.f, 0.f, 0.f};
+    #pragma unroll
+                    for (int jj = 0; jj < BPS; ++jj) {
+                        const int j = s * BPS + jj;
+                        const u32x4_t b = w4_operand(w[t][j]);
+                        acc_t = mfma_bf16_16x16x32(ah[j], b, acc_t);
+                        if constexpr (F32A) acc_t = mfma_bf16_16x16x32(al[j], b, acc_t);
+                    }
+                    const int64_t si = (static_cast<int64_t>(ntc[t]) * p.NG + g) * 16 + col;
+                    float sc, zc;
+                    if constexpr (ASYM) {
+                        sc = f16_to_f32(static_cast<const uint16_t*>(scales)[si]);
+                        const uint32_t zw = zeros[(static_cast<int64_t>(ntc[t]) * p.NG8 + (g >> 3)) * 16 + col];
+                        zc = kW4Bias + static_cast<float>((zw >> (4 * (g & 7))) & 15u);
+                    } else {
+                        sc = static_cast<const float*>(scales)[si];
+                        zc = kW4Bias + 8.0f;  // implied zero point 8
+                    }
+    #pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        acc[t][i] = __builtin_fmaf(sc, __builtin_fmaf(-zc, xs[i], acc_t[i]), acc[t][i]);
                 }
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    acc[t][i] = __builtin_fmaf(sc, __builtin_fmaf(-zc, xs[i], acc_t[i]), acc[t][i]);
             }
         }
     }
@@ -1448,10 +1568,11 @@ void launch_decode_bps(const W4Args& a, dim3 grid, int S, int bps, size_t lds, h
 
 template <bool F32A, bool ASYM, bool F32C, int T, int WAVES, bool GR, bool SWI>
 void launch_gemv_bps(const W4Args& a, dim3 grid, int bps, hipStream_t s) {
+    constexpr bool PIPE = !F32A && !GR && !SWI && T <= 2;
     switch (bps) {
-        case 1: w4_gemv_kernel<F32A, ASYM, F32C, T, WAVES, 1, GR, SWI><<<grid, 64 * WAVES, 0, s>>>(a); break;
-        case 2: w4_gemv_kernel<F32A, ASYM, F32C, T, WAVES, 2, GR, SWI><<<grid, 64 * WAVES, 0, s>>>(a); break;
-        default: w4_gemv_kernel<F32A, ASYM, F32C, T, WAVES, 4, GR, SWI><<<grid, 64 * WAVES, 0, s>>>(a); break;
+        case 1: w4_gemv_kernel<F32A, ASYM, F32C, T, WAVES, 1, GR, SWI, PIPE><<<grid, 64 * WAVES, 0, s>>>(a); break;
+        case 2: w4_gemv_kernel<F32A, ASYM, F32C, T, WAVES, 2, GR, SWI, PIPE><<<grid, 64 * WAVES, 0, s>>>(a); break;
+        default: w4_gemv_kernel<F32A, ASYM, F32C, T, WAVES, 4, GR, SWI, PIPE><<<grid, 64 * WAVES, 0, s>>>(a); break;
     }
 }
 
@@ -1781,10 +1902,10 @@ int grouped_w4(const char* who, const uint16_t* A, const int32_t* offsets, const
 // 32-row blocks (RB = 1, 2), so they do not pay for the MFMAs of 64.
 // 2..16 rows run 16 x 128 tiles with K in two halves inside the workgroup
 // (L = 2).  Measured on MI355X (us, ordinary launch / split), (K, N) at 16
-// rows: (8192, 8192) 16.3 / 14.4, (28672, 8192) 50.2 / 30.8, (16384, 4096)
-// 18.7 / 15.5, (11008, 4096) 14.0 / 13.6, (4096, 11008) 13.2 / 12.6; at 8
-// rows (28672, 8192) 41.8 / 29.1 but (8192, 8192) 13.5 / 14.5; at 4 rows
-// (28672, 8192) 36.3 / 29.0 but (8192, 8192) 11.1 / 14.0.
+// rows: (28672, 8192) 40.4 / 28.9, (8192, 10240) 21.4 / 17.5, (16384, 4096)
+// 19.4 / 15.3, (8192, 28672) 34.9 / 31.7, but (8192, 8192) 13.2 / 14.3; at
+// 12 rows (4096, 11008) 11.5 / 12.5; at 8 rows (28672, 8192) 33.4 / 29.3;
+// at 2 rows (28672, 8192) 28.7 / 29.3.
 // ---------------------------------------------------------------------------
 struct TilePlan {
     bool split = false;  // false: the entry point's ordinary launch
@@ -1838,11 +1959,18 @@ TilePlan plan_thin(const W4Args& a, int64_t ws_cap) {
     const int64_t fill = ceil_div64(cus, wgs);
     const int64_t want = (t.RB == 1) ? std::max<int64_t>(fill, ceil_div(a.Kt, 28)) : fill;
     int S = static_cast<int>(std::min<int64_t>(want, std::max(1, a.Kt / kSplitMinKt)));
-    // 2..16 rows: the split costs about the same at any row count, the
-    // ordinary launch (decode or 16-row kernel) grows with the rows, so it
-    // takes a grid at most half full unsplit, three splits or more, and up
-    // to 8 rows K >= 16384 and N >= 8192
-    if (env_s == 0 && t.RB == 1 && (fill < 2 || S < 3 || (a.M <= 8 && (a.K < 16384 || a.N < 8192)))) return t;
+    // 2..16 rows: the split costs about the same at any row count, while
+    // the ordinary launch (decode or 16-row kernel) grows with the rows and
+    // with K per wave, and loses most where its workgroups need more than
+    // one round of the CUs (N > 8192).  So a split takes a grid at most half
+    // full unsplit, three splits or more, and either K >= 16384 (from 4
+    // rows; up to 8 rows with N >= 8192) or, from 9 rows, K >= 8192 with
+    // N > 8192.
+    if (env_s == 0 && t.RB == 1) {
+        const bool long_k = a.K >= 16384 && a.M >= 4 && (a.M >= 9 || a.N >= 8192);
+        const bool wide = a.M >= 9 && a.K >= 8192 && a.N > 8192;
+        if (fill < 2 || S < 3 || !(long_k || wide)) return t;
+    }
     if (env_s >= 1) S = std::min(env_s, a.Kt);
     const int64_t per_split = static_cast<int64_t>(a.M) * a.N * 4;
     if (ws_cap >= 0) S = static_cast<int>(std::min<int64_t>(S, std::max<int64_t>(1, ws_cap / per_split)));

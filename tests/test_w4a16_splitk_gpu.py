@@ -43,9 +43,9 @@ def _case(oracle, ops, M, K, N, G, seed):
 # kernel or the weights hold K * N >= 32 Mi values (2..16 rows: at least
 # three splits and larger weights the fewer the rows)
 @pytest.mark.parametrize("M,K,N,G", [
-    (16, 8192, 8192, 128),    # 16-row blocks, 4 splits
+    (16, 8192, 10240, 128),   # 16-row blocks, 4 splits
     (11, 8192, 10248, 256),   # 16-row blocks, 11 live rows, N % 16 != 0, G = 256
-    (3, 16384, 8192, 128),    # 3 rows, K >= 16384
+    (4, 16384, 8192, 128),    # 4 rows, K >= 16384
     (17, 4096, 8200, 128),    # 32-row blocks, N % 16 != 0
     (32, 2048, 16400, 256),   # G = 256: two K tiles per scale group
     (48, 2048, 1024, 128),    # 64-row blocks, 48 live rows
@@ -94,7 +94,9 @@ def test_splitk_workspace_bytes_rules(ops):
     assert f(64, 4096, 8192, 64) == 0        # the tile kernel needs G >= 128
     assert f(64, 4160, 8192, 64) == 0        # (and so K % 128 == 0)
     assert f(0, 8192, 8192, 128) == 0
-    assert f(16, 8192, 8192, 128) == 4 * 16 * 8192 * 4   # 16-row blocks, 4 splits
+    assert f(16, 8192, 10240, 128) == 4 * 16 * 10240 * 4   # 16-row blocks, 4 splits
+    assert f(16, 8192, 8192, 128) == 0       # one round of the 16-row kernel
+    assert f(2, 28672, 8192, 128) == 0       # 2 rows: the 16-row kernel
     assert f(16, 8192, 57344, 128) == 0      # 2 splits would not pay at 16 rows
     assert f(8, 8192, 8192, 128) == 0        # nor K < 16384 at 8 rows or fewer
     assert f(8, 28672, 8192, 128) > 0
