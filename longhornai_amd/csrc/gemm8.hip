@@ -544,7 +544,6 @@ __global__ __launch_bounds__(NTHREADS) void gemm8_kernel(Gemm8Args p) {
 constexpr int DS_BK = 64;                     // k bytes per stage
 constexpr int DS_STAGES = 4;                  // LDS buffers (default)
 constexpr int DS_OP_BYTES = BM * DS_BK;       // one operand of one stage (16 KiB)
-constexpr int DS_DMA_PER_STAGE = 2 * DS_OP_BYTES / 1024 / 4;  // per wave (8)
 constexpr int DS_SCALE_BYTES = (BM + BN) * 4;                 // int8 scales of one tile
 
 #define LHQ_LDS_AS __attribute__((address_space(3)))
