@@ -351,30 +351,30 @@ __global__ __launch_bounds__(64 * WAVES) void w4_gemv_kernel(W4Args p) {
     } else {
         for (int kt = kb; kt < ke; ++kt) {
             u32x4_t w[T];
-    #pragma unroll
+#pragma unroll
             for (int t = 0; t < T; ++t)
                 w[t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(
                     qw + ((static_cast<int64_t>(ntc[t]) * p.Kt + kt) * 64 + lane) * 16));
             u32x4_t ah[4], al[4];
-    #pragma unroll
+#pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int k = kt * kW4TileK + 32 * j + 8 * (lane >> 4);
                 load_a8<F32A>(A, static_cast<int64_t>(row) * p.K + k, row_ok && k < p.K, ah[j], al[j]);
             }
-    #pragma unroll
+#pragma unroll
             for (int s = 0; s < SEGS; ++s) {
                 f32x4_t xs = {0.f, 0.f, 0.f, 0.f};
-    #pragma unroll
+#pragma unroll
                 for (int jj = 0; jj < BPS; ++jj) {
                     const int j = s * BPS + jj;
                     xs = mfma_bf16_16x16x32(ah[j], ones, xs);
                     if constexpr (F32A) xs = mfma_bf16_16x16x32(al[j], ones, xs);
                 }
                 const int g = (BPS < 4) ? min(group_of<BPS>(kt, s, p.gmul), p.NG - 1) : group_of<BPS>(kt, s, p.gmul);
-    #pragma unroll
+#pragma unroll
                 for (int t = 0; t < T; ++t) {
                     f32x4_t acc_t = {0.f, 0.f, 0.f, 0.f};
-    #pragma unroll
+#pragma unroll
                     for (int jj = 0; jj < BPS; ++jj) {
                         const int j = s * BPS + jj;
                         const u32x4_t b = w4_operand(w[t][j]);
@@ -391,7 +391,7 @@ __global__ __launch_bounds__(64 * WAVES) void w4_gemv_kernel(W4Args p) {
                         sc = static_cast<const float*>(scales)[si];
                         zc = kW4Bias + 8.0f;  // implied zero point 8
                     }
-    #pragma unroll
+#pragma unroll
                     for (int i = 0; i < 4; ++i)
                         acc[t][i] = __builtin_fmaf(sc, __builtin_fmaf(-zc, xs[i], acc_t[i]), acc[t][i]);
                 }
