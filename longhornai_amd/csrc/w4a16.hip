@@ -1162,17 +1162,27 @@ constexpr int MM_CT = 4;  // column tiles per wave
 // fp32 partial sums to p.ws[split][M][N] for w4_splitk_reduce_kernel to add
 // in split order.  RB (L != 0): 16-row blocks per wave, 64 rows at RB = 4;
 // RB = 1 or 2 serve up to 16 or 32 rows without the MFMAs of 64.
-template <int BPS, bool GBIG, bool GR, bool SWI, int L, bool SK = false, int RB = 4>
+// F32 (the reference interface, gemm_quant.cpp:54-82): fp32 activations,
+// symmetric weights (implied zero point 8) with fp32 scales, fp32 output
+// with alpha / beta.  The activation tile is staged in LDS as fp32 (512
+// bytes per row) and each fragment is split into bf16 hi + lo operands as it
+// is read, so every product runs twice on the bf16 MFMA (product error near
+// 2^-17 relative, as in the 16-row kernel's fp32 form); 64 x 256 tiles only.
+template <int BPS, bool GBIG, bool GR, bool SWI, int L, bool SK = false, int RB = 4, bool F32 = false>
 __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_kernel(W4Args p) {
     static_assert(RB == 4 || (RB <= 2 && L != 0 && !GR), "16- and 32-row blocks on plain launches, not 128 x 128");
     static_assert(!SK || (!GR && !SWI), "split-K on plain launches only");
     static_assert(L != 4 || SK, "the 8-wave 64 x 256 layout on split-K launches only");
+    static_assert(!F32 || (!GR && !SWI && !SK && L == 1 && RB == 4), "the fp32 interface: plain 64 x 256 tiles");
     constexpr int SEGS = 4 / BPS;
     constexpr int NW = (L >= 3) ? 8 : 4;                                  // waves
     constexpr int NK = (L == 2 || L == 4) ? 2 : (L == 3) ? 4 : 1;        // K parts
     constexpr int BM = (L == 0) ? 128 : 16 * RB, WN = (L == 1 || L == 4) ? 4 : 2;
     constexpr int RR = (L == 0) ? 64 : 16 * RB;                          // rows per LDS region
-    constexpr int A_BYTES = ((L == 0) ? 128 : NK * RR) * kW4TileK * 2;
+    constexpr int EA = F32 ? 4 : 2;                                      // activation bytes
+    constexpr int RBYTES = kW4TileK * EA;                                // LDS bytes per row
+    constexpr int CPR = RBYTES / 16;                                     // 16-byte chunks per row
+    constexpr int A_BYTES = ((L == 0) ? 128 : NK * RR) * RBYTES;
     constexpr int DMA = A_BYTES / 1024 / NW;  // activation DMAs per wave per K tile
     extern __shared__ __attribute__((aligned(1024))) uint8_t mm_lds[];  // 2 x A_BYTES
     const int lane = threadIdx.x & 63;
@@ -1208,6 +1218,8 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
         zs = p.zeros + z * p.z_bs;
     }
     const uint16_t* A = static_cast<const uint16_t*>(p.A) + (GR ? 0 : z * p.a_bs);
+    const float* Af = static_cast<const float*>(p.A) + (GR ? 0 : z * p.a_bs);
+    const float* scf = static_cast<const float*>(p.scales) + (GR ? 0 : z * p.s_bs);
     const int col = lane & 15;
 
     // activation DMA q of this wave: chunk idx = (DMA*wave + q)*64 + lane is
@@ -1225,9 +1237,10 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
 #pragma unroll
     for (int q = 0; q < DMA; ++q) {
         const int idx = (DMA * wave + q) * 64 + lane;
-        const int r = idx >> 4, slot = idx & 15;  // LDS row r: region r / RR (this wave's, wr)
+        const int r = idx / CPR, slot = idx % CPR;  // LDS row r: region r / RR (this wave's, wr)
         const int row = min(m0 + ((NK > 1) ? (r % RR) : r), m_end - 1);
-        a_off[q] = static_cast<uint32_t>(row) * static_cast<uint32_t>(p.K) + static_cast<uint32_t>((slot ^ (r & 15)) * 8);
+        a_off[q] = static_cast<uint32_t>(row) * static_cast<uint32_t>(p.K) +
+                   static_cast<uint32_t>((slot ^ (r & 15)) * (16 / EA));
     }
     // this wave's column tiles (clamped to the last one) and their bases
     uint32_t w_base[MM_CT], s_base[MM_CT], z_base[MM_CT];
@@ -1235,7 +1248,8 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
     for (int c = 0; c < MM_CT; ++c) {
         const int nt = min(static_cast<int>(blockIdx.x) * WN * MM_CT + wn * MM_CT + c, p.Nt - 1);
         w_base[c] = static_cast<uint32_t>(nt * p.Kt) * kW4TileBytes + static_cast<uint32_t>(lane * 16);
-        s_base[c] = static_cast<uint32_t>(nt * p.NG * 16 + (col & ~1));  // fp16 pair holding this column
+        // fp16 pair holding this column (fp32: the column's own scale)
+        s_base[c] = static_cast<uint32_t>(nt * p.NG * 16 + (F32 ? col : (col & ~1)));
         z_base[c] = static_cast<uint32_t>(nt * p.NG8 * 16 + col);
     }
     const uint32_t s_half = 16u * (col & 1);
@@ -1250,16 +1264,21 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
         const int kt = min(kt_in + kofs, p.Kt - 1);
         const uint32_t k0 = static_cast<uint32_t>(kt * kW4TileK);
 #pragma unroll
-        for (int q = 0; q < DMA; ++q)
-            __builtin_amdgcn_global_load_lds(A + (a_off[q] + k0), (LHQ_LDS_AS void*)(buf + (DMA * wave + q) * 1024),
-                                             16, 0, 0);
+        for (int q = 0; q < DMA; ++q) {
+            LHQ_LDS_AS void* dst = (LHQ_LDS_AS void*)(buf + (DMA * wave + q) * 1024);
+            if constexpr (F32) __builtin_amdgcn_global_load_lds(Af + (a_off[q] + k0), dst, 16, 0, 0);
+            else __builtin_amdgcn_global_load_lds(A + (a_off[q] + k0), dst, 16, 0, 0);
+        }
 #pragma unroll
         for (int c = 0; c < MM_CT; ++c) {
-            R.zw[c] = zs[z_base[c] + static_cast<uint32_t>((group_of_c<BPS, GBIG>(kt, 0, p.gmul) >> 3) * 16)];
+            if constexpr (!F32)
+                R.zw[c] = zs[z_base[c] + static_cast<uint32_t>((group_of_c<BPS, GBIG>(kt, 0, p.gmul) >> 3) * 16)];
 #pragma unroll
-            for (int s = 0; s < SEGS; ++s)
-                R.sw[c][s] = *reinterpret_cast<const uint32_t*>(
-                    sc + s_base[c] + static_cast<uint32_t>(group_of_c<BPS, GBIG>(kt, s, p.gmul) * 16));
+            for (int s = 0; s < SEGS; ++s) {
+                const uint32_t go = static_cast<uint32_t>(group_of_c<BPS, GBIG>(kt, s, p.gmul) * 16);
+                if constexpr (F32) R.sw[c][s] = *reinterpret_cast<const uint32_t*>(scf + s_base[c] + go);
+                else R.sw[c][s] = *reinterpret_cast<const uint32_t*>(sc + s_base[c] + go);
+            }
             R.w[c] = *reinterpret_cast<const u32x4_t*>(qw + (w_base[c] + static_cast<uint32_t>(kt * kW4TileBytes)));
         }
     };
@@ -1272,7 +1291,7 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
     const u32x4_t m144 = {kM144Bf16x2, kM144Bf16x2, kM144Bf16x2, kM144Bf16x2};
     // fragment (row block i, k block j): LDS row 64*wr + 16*i + (lane & 15), k
     // chunk 4j + (lane >> 4), stored in slot chunk ^ (lane & 15)
-    const uint32_t a_frag = static_cast<uint32_t>((wr * RR + col) * 256);
+    const uint32_t a_frag = static_cast<uint32_t>((wr * RR + col) * RBYTES);
 
     // a wave whose 64 rows all lie past the block's last row (a ragged
     // group's tail block, or M <= 64) has nothing to compute; it still
@@ -1282,6 +1301,55 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
     auto compute = [&](const uint8_t* buf, const Regs& R, int kt_in) {
         const int kt = kt_in + kofs;
         if (!live || kt >= ke) return;  // the last K part may be short
+        if constexpr (F32) {
+            // symmetric codes: 16 - 8 in every byte; the weights are decoded
+            // once and each row block's fragments are split as they are read
+            u32x4_t b[MM_CT][4];
+            float scv[MM_CT];
+#pragma unroll
+            for (int c = 0; c < MM_CT; ++c) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) b[c][j] = w4_operand_z(R.w[c][j], 0x08080808u);
+                scv[c] = __uint_as_float(R.sw[c][0]);
+            }
+#pragma unroll
+            for (int i = 0; i < RB; ++i) {
+                u32x4_t ah[4], al[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    // 8 fp32 activations: chunks 8j + 2(lane >> 4) and the next
+                    const int c0 = 8 * j + 2 * (lane >> 4);
+                    const uint8_t* rowp = buf + a_frag + i * 16 * RBYTES;
+                    const f32x4_t x0 = *reinterpret_cast<const f32x4_t*>(rowp + ((c0 ^ col) * 16));
+                    const f32x4_t x1 = *reinterpret_cast<const f32x4_t*>(rowp + (((c0 + 1) ^ col) * 16));
+                    const float v[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint16_t h0 = f32_to_bf16(v[2 * e]), h1 = f32_to_bf16(v[2 * e + 1]);
+                        ah[j][e] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
+                        al[j][e] = pack_bf16x2(v[2 * e] - bf16_to_f32(h0), v[2 * e + 1] - bf16_to_f32(h1));
+                    }
+                }
+                f32x4_t xs = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    xs = mfma_bf16_16x16x32(ah[j], m144, xs);
+                    xs = mfma_bf16_16x16x32(al[j], m144, xs);
+                }
+#pragma unroll
+                for (int c = 0; c < MM_CT; ++c) {
+                    f32x4_t t = xs;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        t = mfma_bf16_16x16x32(ah[j], b[c][j], t);
+                        t = mfma_bf16_16x16x32(al[j], b[c][j], t);
+                    }
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[i][c][r] = __builtin_fmaf(scv[c], t[r], acc[i][c][r]);
+                }
+            }
+            return;
+        }
         u32x4_t a[RB][4];
 #pragma unroll
         for (int i = 0; i < RB; ++i)
@@ -1448,7 +1516,10 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = m0 + wm * 64 + i * 16 + 4 * (lane >> 4) + r;
-                if (row < m_end) C[static_cast<int64_t>(row) * p.N + cn] = f32_to_bf16(acc[i][c][r]);
+                if (row >= m_end) continue;
+                // F32: the reference's alpha / beta epilogue on fp32 C
+                if constexpr (F32) w4_store<true>(p, z * p.c_bs + static_cast<int64_t>(row) * p.N + cn, acc[i][c][r]);
+                else C[static_cast<int64_t>(row) * p.N + cn] = f32_to_bf16(acc[i][c][r]);
             }
     }
 }
@@ -1646,6 +1717,17 @@ int launch_mma(const W4Args& a, int64_t rows, int groups, int batch, hipStream_t
     else if (l == 1) launch_mma_l<GR, SWI, 1>(a, t, b, s);
     else if (l == 2) launch_mma_l<GR, SWI, 2>(a, t, b, s);
     else launch_mma_l<GR, SWI, 3>(a, t, b, s);
+    return check_launch(who);
+}
+
+// The fp32 interface on the tile kernel (64 x 256 tiles, plain launches).
+int launch_mma_f32(const W4Args& a, hipStream_t s, const char* who) {
+    const int64_t tiles = ceil_div64(a.M, 64);
+    LHQ_SUPPORTED(tiles <= 65535, "%s: %lld row tiles exceed the grid limit", who, static_cast<long long>(tiles));
+    constexpr size_t lds = 2 * 64 * kW4TileK * 4;
+    const dim3 grid(ceil_div(a.Nt, 4 * MM_CT), static_cast<unsigned>(tiles), 1);
+    if (a.gmul) w4_mma_kernel<4, true, false, false, 1, false, 4, true><<<grid, 256, lds, s>>>(a);
+    else w4_mma_kernel<4, false, false, false, 1, false, 4, true><<<grid, 256, lds, s>>>(a);
     return check_launch(who);
 }
 
@@ -2107,6 +2189,7 @@ int lhq_gemm_w4a16(const float* A, const uint8_t* qweight, const float* scales, 
     LHQ_REQUIRE(qweight && scales && C && (A || M == 0), "gemm_w4a16: null pointer");
     if (M == 0) return LHQ_OK;
     W4Args a = make_args(A, qweight, scales, nullptr, C, M, N, K, G, alpha, beta);
+    if (mma_applies(a, M, M)) return launch_mma_f32(a, as_stream(stream), "w4a16 prefill (fp32)");
     return launch_w4<true, false, true>(a, 1, as_stream(stream));
 }
 

@@ -76,6 +76,58 @@ def test_w4a16_f32_beta0_ignores_nan_in_c(oracle, ops):
     assert rel_frobenius(got, want) <= TOL_F32
 
 
+# The fp32 interface on the prefill tile kernel (48+ rows, G >= 128, K a
+# multiple of 128): fp32 activations split into bf16 hi + lo operands.
+@pytest.mark.parametrize("M,K,N,G,alpha,beta", [
+    (48, 512, 64, 128, 1.0, 0.0),
+    (64, 1024, 272, 128, 1.0, 0.0),      # ragged column group
+    (130, 2048, 512, 256, 1.0, 0.0),     # ragged row tile (2 rows), G = 256
+    (96, 1024, 256, 128, 0.5, 2.0),
+    (96, 1024, 256, 128, -1.25, 0.0),
+    (256, 8192, 1024, 128, 1.0, 1.0),
+])
+def test_w4a16_f32_prefill_tile(oracle, ops, M, K, N, G, alpha, beta):
+    got, want = _sym_case(oracle, ops, M, K, N, G, seed=300 + M, alpha=alpha, beta=beta)
+    err = rel_frobenius(got, want)
+    assert err <= TOL_F32, f"rel Frobenius {err:.3e}"
+
+
+def test_w4a16_f32_prefill_tile_beta0_ignores_nan_in_c(oracle, ops):
+    M, K, N, G = 64, 512, 256, 128
+    A = D.uniform((M, K), -1, 1, 11)
+    W = D.uniform((K, N), -1, 1, 12)
+    Bp, Bs = oracle.q4_quantize_groupwise(W, G)
+    want = oracle.gemm_w4a16_groupwise(A, Bp, Bs, N, G)
+    w = ops.prepack_w4_sym(ops.dev(Bp), ops.dev(Bs), K, N, G)
+    C = ops.dev(np.full((M, N), np.nan, np.float32))
+    ops.gemm_w4a16(ops.dev(A), w, C, 1.0, 0.0)
+    got = ops.host(C)
+    assert np.isfinite(got).all()
+    assert rel_frobenius(got, want) <= TOL_F32
+
+
+def test_w4a16_f32_prefill_config5_sampled(oracle, ops):
+    """The fp32 interface at M=4096 on config 5's K=8192, N=28672: whole
+    output on the GPU, sampled rows x columns against the oracle."""
+    import torch
+    M, K, N, G = 4096, 8192, 28672, 128
+    g = D.rng(4096 + N)
+    Bp = g.integers(0, 256, (K // 2, N), dtype=np.uint8)
+    Bs = g.uniform(0.001, 0.01, (K // G, N)).astype(np.float32)
+    A = g.uniform(-1, 1, (M, K)).astype(np.float32)
+    w = ops.prepack_w4_sym(ops.dev(Bp), ops.dev(Bs), K, N, G)
+    C = ops.zeros((M, N), np.float32)
+    ops.gemm_w4a16(ops.dev(A), w, C, 1.0, 0.0)
+    Ch = ops.host(C)
+    del w, C
+    torch.cuda.empty_cache()
+    rows = np.unique(np.concatenate([g.choice(M, 10, replace=False), [0, 63, 64, M - 1]]))
+    cols = np.unique(np.concatenate([g.choice(N, 40, replace=False), np.arange(16), np.arange(N - 16, N)]))
+    want = oracle.gemm_w4a16_groupwise(np.ascontiguousarray(A[rows]), np.ascontiguousarray(Bp[:, cols]),
+                                       np.ascontiguousarray(Bs[:, cols]), len(cols), G)
+    assert rel_frobenius(Ch[np.ix_(rows, cols)], want) <= TOL_F32
+
+
 def _asym_case(oracle, ops, M, K, N, G, seed):
     A = D.to_bf16_bits(oracle, D.normal((M, K), 1.0, seed))
     W = D.normal((K, N), 0.02, seed + 1)
