@@ -1302,8 +1302,15 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
         const int kt = kt_in + kofs;
         if (!live || kt >= ke) return;  // the last K part may be short
         if constexpr (F32) {
-            // symmetric codes: 16 - 8 in every byte; the weights are decoded
-            // once and each row block's fragments are split as they are read
+            // Symmetric codes: 16 - 8 in every byte.  The VALU phase decodes
+            // the weights and splits this wave's own row block (wave w: rows
+            // 16w ..) into bf16 hi + lo in place: each lane overwrites the two
+            // fp32 chunks it read with their hi and lo halves, so no lane
+            // writes what another still reads.  It also computes that block's
+            // sums xs into LDS.  After a barrier the matrix phase, at raised
+            // priority, reads every row block's hi / lo fragments and sums.
+            static_assert(RB == NW, "one row block per wave");
+            f32x4_t* const xs_l = reinterpret_cast<f32x4_t*>(mm_lds + 2 * A_BYTES);
             u32x4_t b[MM_CT][4];
             float scv[MM_CT];
 #pragma unroll
@@ -1312,16 +1319,18 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
                 for (int j = 0; j < 4; ++j) b[c][j] = w4_operand_z(R.w[c][j], 0x08080808u);
                 scv[c] = __uint_as_float(R.sw[c][0]);
             }
-#pragma unroll
-            for (int i = 0; i < RB; ++i) {
+            // fp32 chunk c0 = 8j + 2(lane >> 4) of a row and the next hold 8
+            // activations; after the split they hold their hi and lo halves
+            auto chunk = [&](int i, int j, int h) {
+                const int c0 = 8 * j + 2 * (lane >> 4) + h;
+                return const_cast<uint8_t*>(buf) + a_frag + i * 16 * RBYTES + ((c0 ^ col) * 16);
+            };
+            {
                 u32x4_t ah[4], al[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    // 8 fp32 activations: chunks 8j + 2(lane >> 4) and the next
-                    const int c0 = 8 * j + 2 * (lane >> 4);
-                    const uint8_t* rowp = buf + a_frag + i * 16 * RBYTES;
-                    const f32x4_t x0 = *reinterpret_cast<const f32x4_t*>(rowp + ((c0 ^ col) * 16));
-                    const f32x4_t x1 = *reinterpret_cast<const f32x4_t*>(rowp + (((c0 + 1) ^ col) * 16));
+                    const f32x4_t x0 = *reinterpret_cast<const f32x4_t*>(chunk(wave, j, 0));
+                    const f32x4_t x1 = *reinterpret_cast<const f32x4_t*>(chunk(wave, j, 1));
                     const float v[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
@@ -1329,6 +1338,8 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
                         ah[j][e] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
                         al[j][e] = pack_bf16x2(v[2 * e] - bf16_to_f32(h0), v[2 * e + 1] - bf16_to_f32(h1));
                     }
+                    *reinterpret_cast<u32x4_t*>(chunk(wave, j, 0)) = ah[j];
+                    *reinterpret_cast<u32x4_t*>(chunk(wave, j, 1)) = al[j];
                 }
                 f32x4_t xs = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1336,6 +1347,25 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
                     xs = mfma_bf16_16x16x32(ah[j], m144, xs);
                     xs = mfma_bf16_16x16x32(al[j], m144, xs);
                 }
+                xs_l[wave * 64 + lane] = xs;
+            }
+            // every wave's splits and sums are in LDS (lgkmcnt(0); the next
+            // tile's loads stay in flight); the empty asm statements keep the
+            // compiler from moving LDS accesses across the barrier
+            __builtin_amdgcn_s_waitcnt(0xC07F);
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+            for (int i = 0; i < RB; ++i) {
+                u32x4_t ah[4], al[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    ah[j] = *reinterpret_cast<const u32x4_t*>(chunk(i, j, 0));
+                    al[j] = *reinterpret_cast<const u32x4_t*>(chunk(i, j, 1));
+                }
+                const f32x4_t xs = xs_l[i * 64 + lane];
 #pragma unroll
                 for (int c = 0; c < MM_CT; ++c) {
                     f32x4_t t = xs;
@@ -1348,6 +1378,7 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
                     for (int r = 0; r < 4; ++r) acc[i][c][r] = __builtin_fmaf(scv[c], t[r], acc[i][c][r]);
                 }
             }
+            __builtin_amdgcn_s_setprio(0);
             return;
         }
         static_assert(SEGS == 1, "one scale segment per K tile");
@@ -1780,10 +1811,15 @@ int launch_mma(const W4Args& a, int64_t rows, int groups, int batch, hipStream_t
 int launch_mma_f32(const W4Args& a, hipStream_t s, const char* who) {
     const int64_t tiles = ceil_div64(a.M, 64);
     LHQ_SUPPORTED(tiles <= 65535, "%s: %lld row tiles exceed the grid limit", who, static_cast<long long>(tiles));
-    constexpr size_t lds = 2 * 64 * kW4TileK * 4;
+    constexpr size_t lds = 2 * 64 * kW4TileK * 4 + 4 * 64 * 16;  // two fp32 tiles and the row blocks' sums
     const dim3 grid(ceil_div(a.Nt, 4 * MM_CT), static_cast<unsigned>(tiles), 1);
-    if (a.gmul) w4_mma_kernel<4, true, false, false, 1, false, 4, true><<<grid, 256, lds, s>>>(a);
-    else w4_mma_kernel<4, false, false, false, 1, false, 4, true><<<grid, 256, lds, s>>>(a);
+    if (a.gmul) {
+        allow_cu_lds<&w4_mma_kernel<4, true, false, false, 1, false, 4, true>>();
+        w4_mma_kernel<4, true, false, false, 1, false, 4, true><<<grid, 256, lds, s>>>(a);
+    } else {
+        allow_cu_lds<&w4_mma_kernel<4, false, false, false, 1, false, 4, true>>();
+        w4_mma_kernel<4, false, false, false, 1, false, 4, true><<<grid, 256, lds, s>>>(a);
+    }
     return check_launch(who);
 }
 
