@@ -80,6 +80,8 @@ def test_w4a16_f32_beta0_ignores_nan_in_c(oracle, ops):
 # multiple of 128): fp32 activations split into bf16 hi + lo operands.
 @pytest.mark.parametrize("M,K,N,G,alpha,beta", [
     (48, 512, 64, 128, 1.0, 0.0),
+    (64, 128, 128, 128, 1.0, 0.0),       # one K tile
+    (50, 384, 320, 128, 1.0, 0.0),       # three K tiles (an odd count), 14 dead rows
     (64, 1024, 272, 128, 1.0, 0.0),      # ragged column group
     (130, 2048, 512, 256, 1.0, 0.0),     # ragged row tile (2 rows), G = 256
     (96, 1024, 256, 128, 0.5, 2.0),
