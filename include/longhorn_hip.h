@@ -306,13 +306,15 @@ int lhq_gemm_f32_batched(const float* A, const float* B, float* C, int batch, in
  * {non-NaN mismatches, NaN mismatches}; both are 0 on a conforming device. */
 int lhq_selftest_bf16(unsigned long long* counts, void* stream);
 /* Matrix-core rate probe: `blocks` workgroups of 4 waves, each wave running
- * `iters` rounds of 4 independent MFMAs on register operands (no memory
- * traffic), so the launch time gives the sustained MFMA rate with the GPU
- * loaded.  kind 0: v_mfma_i32_32x32x32_i8 (65,536 ops each), 1:
- * v_mfma_f32_16x16x32_bf16 (16,384 flops), 2: v_mfma_f32_32x32x16_bf16
- * (32,768 flops), 3: v_mfma_i32_16x16x64_i8 (32,768 ops); 4, 5: kind 1 with
- * 2 or 4 independent integer VALU operations per MFMA (whether VALU work
- * overlaps the matrix core's); one launch performs blocks * 4 * iters * 4
+ * `iters` rounds of 4 MFMAs on register operands (no memory traffic), so the
+ * launch time gives the sustained MFMA rate with the GPU loaded.  Kinds 0..5
+ * rotate over 4 independent accumulators: 0: v_mfma_i32_32x32x32_i8 (65,536
+ * ops each), 1: v_mfma_f32_16x16x32_bf16 (16,384 flops), 2:
+ * v_mfma_f32_32x32x16_bf16 (32,768 flops), 3: v_mfma_i32_16x16x64_i8
+ * (32,768 ops); 4, 5: kind 1 with 2 or 4 independent integer VALU operations
+ * per MFMA (whether VALU work overlaps the matrix core's).  Kinds 6, 7: one
+ * dependent chain (each MFMA accumulates onto the previous result) of kind 1's
+ * and kind 3's instruction.  One launch performs blocks * 4 * iters * 4
  * MFMAs.  sink: `blocks` device ints (written). */
 int lhq_probe_mfma_rate(int kind, int blocks, int iters, int* sink, void* stream);
 

@@ -1,5 +1,7 @@
 // selftest.hip -- on-device checks of conversion instructions the kernels
 // rely on (library diagnostics, not part of the reference interface).
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace lhq {
@@ -73,6 +75,35 @@ __global__ __launch_bounds__(256) void mfma_rate_kernel(int iters, int* sink) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) r += c0[j] ^ c1[j] ^ c2[j] ^ c3[j];
         if (t == 0) sink[blockIdx.x] = r;
+    } else if constexpr (KIND == 6 || KIND == 7) {
+        // one dependent chain: every MFMA accumulates onto the previous one's
+        // result (bf16 16x16x32, or int8 16x16x64)
+        using acc_t = typename std::conditional<KIND == 6, f32x4_t, i32x4_t>::type;
+        acc_t c0 = {};
+        for (int i = 0; i < iters; ++i) {
+            if constexpr (KIND == 6) {
+                c0 = mfma_bf16_16x16x32(a, b, c0);
+                c0 = mfma_bf16_16x16x32(b, a, c0);
+                c0 = mfma_bf16_16x16x32(a, a, c0);
+                c0 = mfma_bf16_16x16x32(b, b, c0);
+            } else {
+                c0 = mfma_i8_16x16x64(a, b, c0);
+                c0 = mfma_i8_16x16x64(b, a, c0);
+                c0 = mfma_i8_16x16x64(a, a, c0);
+                c0 = mfma_i8_16x16x64(b, b, c0);
+            }
+        }
+        if constexpr (KIND == 6) {
+            float r = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) r += c0[j];
+            if (t == 0) sink[blockIdx.x] = __float_as_int(r);
+        } else {
+            int r = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) r += c0[j];
+            if (t == 0) sink[blockIdx.x] = r;
+        }
     } else if constexpr (KIND == 4 || KIND == 5) {
         constexpr int NV = KIND == 4 ? 2 : 4;  // VALU operations per MFMA
         f32x4_t c0 = {}, c1 = {}, c2 = {}, c3 = {};
@@ -117,7 +148,7 @@ using namespace lhq;
 
 extern "C" int lhq_probe_mfma_rate(int kind, int blocks, int iters, int* sink, void* stream) {
     LHQ_REQUIRE(sink, "probe_mfma_rate: null sink");
-    LHQ_REQUIRE(kind >= 0 && kind <= 5, "probe_mfma_rate: kind %d (0..5)", kind);
+    LHQ_REQUIRE(kind >= 0 && kind <= 7, "probe_mfma_rate: kind %d (0..7)", kind);
     LHQ_REQUIRE(blocks >= 1 && iters >= 1, "probe_mfma_rate: blocks %d, iters %d", blocks, iters);
     hipStream_t s = as_stream(stream);
     if (kind == 0) mfma_rate_kernel<0><<<blocks, 256, 0, s>>>(iters, sink);
@@ -125,7 +156,9 @@ extern "C" int lhq_probe_mfma_rate(int kind, int blocks, int iters, int* sink, v
     else if (kind == 2) mfma_rate_kernel<2><<<blocks, 256, 0, s>>>(iters, sink);
     else if (kind == 3) mfma_rate_kernel<3><<<blocks, 256, 0, s>>>(iters, sink);
     else if (kind == 4) mfma_rate_kernel<4><<<blocks, 256, 0, s>>>(iters, sink);
-    else mfma_rate_kernel<5><<<blocks, 256, 0, s>>>(iters, sink);
+    else if (kind == 5) mfma_rate_kernel<5><<<blocks, 256, 0, s>>>(iters, sink);
+    else if (kind == 6) mfma_rate_kernel<6><<<blocks, 256, 0, s>>>(iters, sink);
+    else mfma_rate_kernel<7><<<blocks, 256, 0, s>>>(iters, sink);
     return check_launch("probe_mfma_rate");
 }
 

@@ -28,7 +28,7 @@ def test_mfma_rate_probe_runs_and_rejects_bad_arguments(lib):
     import torch
     from longhornai_amd import ops
     sink = torch.full((16,), -1, dtype=torch.int32, device="cuda")
-    for kind in range(6):
+    for kind in range(8):
         lib.call("lhq_probe_mfma_rate", kind, 16, 8, sink.data_ptr(), ops.stream())
     torch.cuda.synchronize()
-    assert lib.status("lhq_probe_mfma_rate", 6, 16, 8, sink.data_ptr(), ops.stream()) != 0
+    assert lib.status("lhq_probe_mfma_rate", 8, 16, 8, sink.data_ptr(), ops.stream()) != 0
