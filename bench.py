@@ -156,6 +156,48 @@ def make_w4_sets(ops, K: int, N: int, G: int, nsets: int, seed: int):
     return sets
 
 
+def bench_w4a16_f32(ops, M, K, N, G, steps, warmup, seed=0, min_rotate_bytes=2 * INFINITY_CACHE_BYTES + (1 << 26)):
+    """The reference interface (lhq_gemm_w4a16, gemm_quant.cpp:54-82): fp32
+    activations and output, symmetric int4 weights with fp32 group scales,
+    alpha = 1, beta = 0; timed over rotating weight sets like the bf16 legs.
+    Bytes: K*N/2 codes + (K/G)*N*4 scales + M*K*4 + M*N*4."""
+    import numpy as np
+    import torch
+    per = K * N // 2 + (K // G) * N * 4 + M * K * 4 + M * N * 4
+    nsets = max(2, -(-min_rotate_bytes // per))
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    sets = []
+    for _ in range(nsets):
+        packed = torch.randint(0, 256, (K // 2, N), dtype=torch.uint8, device="cuda", generator=gen)
+        sc = torch.rand((K // G, N), device="cuda", generator=gen) * 0.01
+        sets.append(ops.prepack_w4_sym(packed, sc, K, N, G))
+        del packed, sc
+    A = [torch.randn((M, K), generator=gen, device="cuda") for _ in range(nsets)]
+    C = [torch.zeros((M, N), device="cuda") for _ in range(nsets)]
+    fn = ops.lib().cdll.lhq_gemm_w4a16
+
+    def launch(i):
+        j = i % nsets
+        st = fn(A[j].data_ptr(), sets[j].qweight.data_ptr(), sets[j].scales.data_ptr(), C[j].data_ptr(),
+                M, N, K, G, 1.0, 0.0, ops.stream())
+        if st:
+            raise RuntimeError(f"lhq_gemm_w4a16: {ops.lib().last_error()}")
+
+    timer = GraphTimer(launch, nsets, chunk=nsets * max(1, 64 // nsets))
+    ms, _ = timer.time(steps, warmup)
+    us = ms * 1e3 / steps
+    res = {"leg": "w4a16_f32_interface", "M": M, "K": K, "N": N, "G": G, "entry": "lhq_gemm_w4a16",
+           "us_per_call": round(us, 2), "gbs": round(per / (us * 1e-6) / 1e9, 1),
+           "hbm_frac": round(per / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+           "tflops": round(2.0 * M * K * N / (us * 1e-6) / 1e12, 1),
+           "mfma_frac": round(2.0 * M * K * N / (us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4)}
+    del timer, sets, A, C
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_w4a16(ops, M, K, N, G, steps, warmup, seed=0, min_rotate_bytes=2 * INFINITY_CACHE_BYTES + (1 << 26),
                 workspace=False):
     """W4A16 bf16 timed over rotating weight sets.  workspace: through
@@ -678,7 +720,7 @@ def main() -> int:
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a 1 GiB device copy (PMC calibration kernel)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the W4A16 prefill and MoE legs")
-    ap.add_argument("--only", choices=["w4a16", "w8a8", "prefill", "moe", "fp8", "configs", "mfma"], default=None,
+    ap.add_argument("--only", choices=["w4a16", "w8a8", "prefill", "moe", "fp8", "configs", "mfma", "f32"], default=None,
                     help="run one leg only (profiling); prints that leg's summary, not the bench line")
     ap.add_argument("--moe-tokens", type=int, default=512,
                     help="tokens of the --only moe leg (512 = config 4; 1-4 run the grouped decode kernel)")
@@ -717,6 +759,16 @@ def main() -> int:
         return 0
     if args.only == "mfma":
         print(json.dumps({"leg": "mfma_ceiling", **mfma_ceiling(ops)}), flush=True)
+        return 0
+    if args.only == "f32":
+        # the reference interface: decode shapes on the integer decode and
+        # 16-row kernels, prefill shapes on the tile kernel
+        for m, k, n, st in ((1, 8192, 28672, 500), (16, 8192, 28672, 200), (256, 8192, 8192, 100),
+                            (1024, 8192, 8192, 40), (4096, 8192, 8192, 20)):
+            r = bench_w4a16_f32(ops, m, k, n, G, st, max(3, st // 10))
+            log(f"w4a16 fp32 interface M={m} K={k} N={n}: {r['us_per_call']:.1f} us  {r['gbs']:.0f} GB/s "
+                f"({100 * r['hbm_frac']:.1f}% HBM)  {r['tflops']:.0f} TFLOPS ({100 * r['mfma_frac']:.1f}% bf16)")
+            print(json.dumps(r), flush=True)
         return 0
     if args.only == "configs":
         print(json.dumps({"leg": "w4a16_config2", "shapes": config_sweep(ops, "config 2", *CONFIG2)}), flush=True)
