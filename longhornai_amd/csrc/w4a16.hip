@@ -1410,8 +1410,8 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
             // per CU) drift into opposite phases, and the priority lets the
             // wave in its matrix phase issue first, so one wave's decode runs
             // under the other's MFMAs (measured at M=4096, K=8192, N=28672:
-            // 1949 against 2055 us with the interleaved schedule; the same
-            // split without the priority change, 2143 against 2095).
+            // 1870-1880 against 2029 us with the interleaved schedule; the
+            // same split without the priority change was 3% slower than it).
             u32x4_t b[MM_CT][4];
             float scs[MM_CT];
 #pragma unroll
