@@ -1150,6 +1150,9 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512) void w4_decode_i8_kernel(W4Arg
 // (the activations are not zero-padded in LDS).
 // ---------------------------------------------------------------------------
 constexpr int MM_CT = 4;  // column tiles per wave
+// word 3 of a raw buffer resource (gfx9 family): 32-bit data format, no
+// swizzle, offsets taken as given
+constexpr int kBufWord3 = 0x00020000;
 // rows per workgroup tile: L == 0 ? 128 : 16 * RB; column tiles per
 // workgroup: (L == 1 || L == 4 ? 4 : 2) * MM_CT; K parts: 2 (L == 2, 4) or
 // 4 (L == 3); one activation buffer: 128 rows (L == 0) or one region of
@@ -1225,34 +1228,54 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
     // activation DMA q of this wave: chunk idx = (DMA*wave + q)*64 + lane is
     // LDS row idx >> 4, LDS slot idx & 15, global chunk slot ^ (row & 15);
     // LDS row r lies in region r / RR, the region of the K part whose waves
-    // issue it (DMA*4 rows per wave); element offsets are 32-bit (the
-    // launcher bounds rows * K)
+    // issue it (DMA*4 rows per wave); offsets are taken from the workgroup's
+    // first row (64 rows x K elements at most)
     // (a fixed bound: a bound that depends on a template parameter, with the
     // array captured by the lambdas below, makes hipcc's host pass drop the
     // kernel's launch stub without a diagnostic; entries past DMA are unused)
     static_assert(DMA >= 1 && DMA <= 8, "activation DMAs per wave");
     static_assert(NK == 1 || (RR % (DMA * 4) == 0 && RR / (DMA * 4) == NW / NK),
                   "each wave's DMA rows lie in its own K part's region");
-    uint32_t a_off[8];
+    uint32_t a_voff[8];  // byte offsets from the workgroup's first row
 #pragma unroll
     for (int q = 0; q < DMA; ++q) {
         const int idx = (DMA * wave + q) * 64 + lane;
         const int r = idx / CPR, slot = idx % CPR;  // LDS row r: region r / RR (this wave's, wr)
         const int row = min(m0 + ((NK > 1) ? (r % RR) : r), m_end - 1);
-        a_off[q] = static_cast<uint32_t>(row) * static_cast<uint32_t>(p.K) +
-                   static_cast<uint32_t>((slot ^ (r & 15)) * (16 / EA));
-    }
-    // this wave's column tiles (clamped to the last one) and their bases
-    uint32_t w_base[MM_CT], s_base[MM_CT], z_base[MM_CT];
-#pragma unroll
-    for (int c = 0; c < MM_CT; ++c) {
-        const int nt = min(static_cast<int>(blockIdx.x) * WN * MM_CT + wn * MM_CT + c, p.Nt - 1);
-        w_base[c] = static_cast<uint32_t>(nt * p.Kt) * kW4TileBytes + static_cast<uint32_t>(lane * 16);
-        // fp16 pair holding this column (fp32: the column's own scale)
-        s_base[c] = static_cast<uint32_t>(nt * p.NG * 16 + (F32 ? col : (col & ~1)));
-        z_base[c] = static_cast<uint32_t>(nt * p.NG8 * 16 + col);
+        a_voff[q] = (static_cast<uint32_t>(row - m0) * static_cast<uint32_t>(p.K) +
+                     static_cast<uint32_t>((slot ^ (r & 15)) * (16 / EA))) * EA;
     }
     const uint32_t s_half = 16u * (col & 1);
+    // Buffer resources based at this workgroup's first row and this wave's
+    // first column tile: the per-lane part of each address is fixed for the
+    // whole K loop (voffset) and the per-tile part is scalar (soffset), so
+    // a tile's loads take no vector address arithmetic (and a read past a
+    // resource's extent returns zero instead of faulting).
+    constexpr int ES = F32 ? 4 : 2;  // scale bytes
+    const int nt0 = min(static_cast<int>(blockIdx.x) * WN * MM_CT + wn * MM_CT, p.Nt - 1);
+    int dnt[MM_CT];
+#pragma unroll
+    for (int c = 0; c < MM_CT; ++c) dnt[c] = min(nt0 + c, p.Nt - 1) - nt0;
+    const int nt_left = p.Nt - nt0;
+    // extents in bytes, at most 2^32 - 1 (offsets within them are 32-bit)
+    auto extent = [](int64_t bytes) { return static_cast<int>(static_cast<uint32_t>(min(bytes, int64_t{0xFFFFFFFF}))); };
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(qw) + static_cast<int64_t>(nt0) * p.Kt * kW4TileBytes, 0,
+        extent(static_cast<int64_t>(nt_left) * p.Kt * kW4TileBytes), kBufWord3);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        F32 ? static_cast<void*>(const_cast<float*>(scf) + static_cast<int64_t>(nt0) * p.NG * 16)
+            : static_cast<void*>(const_cast<uint16_t*>(sc) + static_cast<int64_t>(nt0) * p.NG * 16),
+        0, extent(static_cast<int64_t>(nt_left) * p.NG * 16 * ES), kBufWord3);
+    const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(zs) + static_cast<int64_t>(nt0) * p.NG8 * 16, 0,
+        extent(static_cast<int64_t>(nt_left) * p.NG8 * 16 * 4), kBufWord3);
+    const __amdgpu_buffer_rsrc_t ra_ = __builtin_amdgcn_make_buffer_rsrc(
+        F32 ? static_cast<void*>(const_cast<float*>(Af) + static_cast<int64_t>(m0) * p.K)
+            : static_cast<void*>(const_cast<uint16_t*>(A) + static_cast<int64_t>(m0) * p.K),
+        0, extent(static_cast<int64_t>(m_end - m0) * p.K * EA), kBufWord3);
+    const int w_voff = lane * 16;
+    const int s_voff = (F32 ? col : (col & ~1)) * ES;
+    const int z_voff = col * 4;
 
     struct Regs {
         u32x4_t w[MM_CT];
@@ -1262,24 +1285,20 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
     // all loads of K tile kt (clamped) into LDS buffer buf and registers R
     auto issue = [&](uint8_t* buf, Regs& R, int kt_in) {
         const int kt = min(kt_in + kofs, p.Kt - 1);
-        const uint32_t k0 = static_cast<uint32_t>(kt * kW4TileK);
 #pragma unroll
-        for (int q = 0; q < DMA; ++q) {
-            LHQ_LDS_AS void* dst = (LHQ_LDS_AS void*)(buf + (DMA * wave + q) * 1024);
-            if constexpr (F32) __builtin_amdgcn_global_load_lds(Af + (a_off[q] + k0), dst, 16, 0, 0);
-            else __builtin_amdgcn_global_load_lds(A + (a_off[q] + k0), dst, 16, 0, 0);
-        }
+        for (int q = 0; q < DMA; ++q)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra_, (LHQ_LDS_AS void*)(buf + (DMA * wave + q) * 1024), 16,
+                                                     a_voff[q], kt * kW4TileK * EA, 0, 0);
 #pragma unroll
         for (int c = 0; c < MM_CT; ++c) {
             if constexpr (!F32)
-                R.zw[c] = zs[z_base[c] + static_cast<uint32_t>((group_of_c<BPS, GBIG>(kt, 0, p.gmul) >> 3) * 16)];
+                R.zw[c] = __builtin_amdgcn_raw_buffer_load_b32(
+                    rz, z_voff, (dnt[c] * p.NG8 + (group_of_c<BPS, GBIG>(kt, 0, p.gmul) >> 3)) * 16 * 4, 0);
 #pragma unroll
-            for (int s = 0; s < SEGS; ++s) {
-                const uint32_t go = static_cast<uint32_t>(group_of_c<BPS, GBIG>(kt, s, p.gmul) * 16);
-                if constexpr (F32) R.sw[c][s] = *reinterpret_cast<const uint32_t*>(scf + s_base[c] + go);
-                else R.sw[c][s] = *reinterpret_cast<const uint32_t*>(sc + s_base[c] + go);
-            }
-            R.w[c] = *reinterpret_cast<const u32x4_t*>(qw + (w_base[c] + static_cast<uint32_t>(kt * kW4TileBytes)));
+            for (int s = 0; s < SEGS; ++s)
+                R.sw[c][s] = __builtin_amdgcn_raw_buffer_load_b32(
+                    rs, s_voff, (dnt[c] * p.NG + group_of_c<BPS, GBIG>(kt, s, p.gmul)) * 16 * ES, 0);
+            R.w[c] = __builtin_amdgcn_raw_buffer_load_b128(rw, w_voff, (dnt[c] * p.Kt + kt) * kW4TileBytes, 0);
         }
     };
 
