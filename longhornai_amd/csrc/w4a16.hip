@@ -2175,6 +2175,16 @@ TilePlan plan_thin(const W4Args& a, int64_t ws_cap) {
     const int kps = ceil_div(a.Kt, std::max(S, 1));
     S = ceil_div(a.Kt, kps);
     if (S <= 1) return t;
+    // 17..64 rows with K >= 16384: 64 x 128 (or 32 x 128) tiles with K in
+    // two halves inside the workgroup, twice the workgroups of the 64 x 256
+    // grid at the same split count (two workgroups per CU).  Measured with
+    // the plan's split count, L = 1 against L = 2 (us): 64 rows, K = 28672,
+    // N = 8192: 57.0-58.2 / 53.0-53.6; 48 rows 53.1-53.5 / 49.8-50.7; 32 rows
+    // 41.2 / 38.5-39.4; 24 rows 38.8-40.7 / 34.4-37.0; 64 rows, K = 16384:
+    // 36.3-37.8 / 33.9-35.4; K = 20480 42.8-43.1 / 40.7-42.9.  At K = 8192
+    // L = 1 stays ahead (24.4 / 24.9), and halving the splits with L = 2
+    // loses everywhere.
+    if (env_l == 0 && t.RB >= 2 && a.Kt >= 128) t.L = 2;
     t.split = true;
     t.S = S;
     t.kps = kps;
@@ -2216,6 +2226,7 @@ void launch_split_tiles(const W4Args& a, const TilePlan& t, hipStream_t s) {
 #endif
     if (t.L == 3) launch_split_rb<3, 4>(a, t.S, s);
     else if (t.L == 2 && t.RB == 1) launch_split_rb<2, 1>(a, t.S, s);
+    else if (t.L == 2 && t.RB == 2) launch_split_rb<2, 2>(a, t.S, s);
     else if (t.L == 2) launch_split_rb<2, 4>(a, t.S, s);
     else if (t.RB == 2) launch_split_rb<1, 2>(a, t.S, s);
     else launch_split_rb<1, 4>(a, t.S, s);

@@ -3,12 +3,13 @@
 At 2..64 rows the tile kernel's output grid cannot fill the GPU, so K is
 split across workgroups: each split writes fp32 partial sums to the
 workspace and a second kernel adds them in split order.  Checked here: the
-three row-block forms (16, 32 and 64 rows per wave; 16-row blocks with K in
-two halves inside the workgroup), ragged M and N, split boundaries
-inside scale groups, G = 128, 256 and 384, the workspace-size rules (none,
-smaller than asked, exactly asked) and bit-for-bit determinism across calls.  Bars as the
-other bf16 tests: relative Frobenius <= 1e-2, and > 99.9% of elements within
-one bf16 ulp of the correctly rounded oracle value."""
+three row-block forms (16, 32 and 64 rows per wave; 16-row blocks, and 32-
+or 64-row blocks at K >= 16384, with K in two halves inside the workgroup),
+ragged M and N, split boundaries inside scale groups, G = 128, 256 and 384,
+the workspace-size rules (none, smaller than asked, exactly asked) and
+bit-for-bit determinism across calls.  Bars as the other bf16 tests:
+relative Frobenius <= 1e-2, and > 99.9% of elements within one bf16 ulp of
+the correctly rounded oracle value."""
 import numpy as np
 import pytest
 
@@ -52,6 +53,8 @@ def _case(oracle, ops, M, K, N, G, seed):
     (56, 1152, 2048, 384),    # G = 384: split boundary inside a scale group
     (64, 8192, 1024, 128),    # config 5 K
     (64, 4096, 4104, 128),    # ragged N at 64 rows
+    (24, 16384, 2064, 128),   # K >= 16384: 32-row blocks, K halves in the workgroup, odd K tiles per split
+    (64, 16384, 1040, 128),   # K >= 16384: 64-row blocks, K halves in the workgroup, ragged N
 ])
 def test_splitk_matches_oracle(oracle, ops, M, K, N, G):
     A, w, want = _case(oracle, ops, M, K, N, G, seed=700 + M + N)
