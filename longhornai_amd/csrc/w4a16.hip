@@ -2123,10 +2123,11 @@ constexpr int kSplitMinKt = 4;  // K tiles per split at least
 // split, but (4096, 11008) 19.9 against 15.6 and (8192, 8192) 22.0 against
 // 17.0.  S brings the grid to about one workgroup per CU, with at least 4 K
 // tiles per split (M = 64, K = N = 8192: 48.5 us unsplit, 24.5 with 8
-// splits, 27.3 with 16).  The plain 64 x 256 layout with a K split beat the
-// in-workgroup split layouts with a K split as well (M = 64, K = N = 8192:
-// 24.3 us against 24.3 and 25.1; K = 28672: 58.0 against 56.2 and 58.8;
-// M = 32, K = 8192, N = 57344: 69.5 against 97.2 and 112.2).
+// splits, 27.3 with 16).  At K < 16384 the plain 64 x 256 layout with a K
+// split matched or beat the in-workgroup split layouts with a K split (M =
+// 64, K = N = 8192: 24.3 us against 24.3 and 25.1; M = 32, K = 8192, N =
+// 57344: 69.5 against 97.2 and 112.2); from K = 16384 on, K halves inside
+// the workgroup win (below).
 TilePlan plan_thin(const W4Args& a, int64_t ws_cap) {
     TilePlan t;
     // (read on every call in a tuning build, so one process can sweep them)
