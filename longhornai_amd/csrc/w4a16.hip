@@ -2147,11 +2147,11 @@ TilePlan plan_thin(const W4Args& a, int64_t ws_cap) {
     const int64_t wgs =
         static_cast<int64_t>(ceil_div(a.Nt, (t.L == 1 || t.L == 4 ? 4 : 2) * MM_CT)) * ceil_div(a.M, 16 * t.RB);
     const int cus = std::max(device_cus(), 1);
-    // 64-row blocks with a quarter of the CUs' worth of column groups or
-    // more: the ordinary launch's split-K layouts (K in two or four parts
-    // inside a workgroup) do as well or better (M = 64, K = 8192: N = 28672
-    // 57.2 us against 61.2 split, N = 57344 100.6 against 100.5)
-    if (env_s == 0 && env_l == 0 && tile && t.RB == 4 && 4 * wgs >= cus) return t;
+    // 64-row blocks with more than half a CU's worth of column groups: the
+    // ordinary launch (64 x 128 tiles with K halves in the workgroup) does
+    // as well or better (M = 64, K = 8192, N = 57344: 88.2-89.9 us against
+    // 92.1-92.4 with 2 splits, 104.9-107.1 with 3)
+    if (env_s == 0 && env_l == 0 && tile && t.RB == 4 && 2 * wgs > cus) return t;
     // about one workgroup per CU, and for 16-row blocks at most 28 K tiles
     // per split (16 rows, K = 28672: 8 splits 30.8 us, 6 34.3, 4 37.4)
     const int64_t fill = ceil_div64(cus, wgs);
@@ -2169,6 +2169,21 @@ TilePlan plan_thin(const W4Args& a, int64_t ws_cap) {
         const bool wide = a.M >= 9 && a.K >= 8192 && a.N > 8192;
         if (fill < 2 || S < 3 || !(long_k || wide)) return t;
     }
+    // 64-row blocks: about two workgroups per CU, so the two-phase K loop
+    // has a second workgroup's wave on every SIMD to alternate with -- by
+    // splitting further (at least 8 K tiles per split, and at most two
+    // workgroups per CU: a third round costs more than it saves), unless K
+    // is long enough for K halves inside the workgroup at one split per CU
+    // (the layout switch below).  Measured (us, M = 64, one split per CU or
+    // unsplit / this rule): K = 8192, N = 28672 61.1-62.4 / 51.9-52.7 (4
+    // splits; 5 splits, 560 workgroups, 63.4-65.3); N = 14336 34.6-35.2 /
+    // 33.0-33.4 (8); K = 4096, N = 28672 34.4-34.7 / 32.0-33.1 (4); K =
+    // 28672, N = 28672 179.9-181.1 / 148.3-150.0 (4); 48 rows, K = 8192,
+    // N = 28672 53.3-53.7 / 46.4-48.4 (4).
+    if (env_s == 0 && t.RB == 4 && !(a.Kt >= 128 && S * wgs <= cus)) {
+        const int two = static_cast<int>(std::min<int64_t>(2 * cus / wgs, a.Kt / 8));
+        S = std::max(S, two);
+    }
     if (env_s >= 1) S = std::min(env_s, a.Kt);
     const int64_t per_split = static_cast<int64_t>(a.M) * a.N * 4;
     if (ws_cap >= 0) S = static_cast<int>(std::min<int64_t>(S, std::max<int64_t>(1, ws_cap / per_split)));
@@ -2185,7 +2200,7 @@ TilePlan plan_thin(const W4Args& a, int64_t ws_cap) {
     // 36.3-37.8 / 33.9-35.4; K = 20480 42.8-43.1 / 40.7-42.9.  At K = 8192
     // L = 1 stays ahead (24.4 / 24.9), and halving the splits with L = 2
     // loses everywhere.
-    if (env_l == 0 && t.RB >= 2 && a.Kt >= 128) t.L = 2;
+    if (env_l == 0 && t.RB >= 2 && a.Kt >= 128 && static_cast<int64_t>(S) * wgs <= cus) t.L = 2;
     t.split = true;
     t.S = S;
     t.kps = kps;

@@ -108,6 +108,9 @@ def test_splitk_workspace_bytes_rules(ops):
     assert f(32, 4096, 4096, 128) == 0       # small weights: the 16-row kernel
     assert f(32, 4096, 8192, 128) > 0
     assert f(64, 8192, 8192, 128) == 8 * 64 * 8192 * 4   # 8 splits of 8 K tiles
+    assert f(64, 8192, 14336, 128) == 8 * 64 * 14336 * 4  # two workgroups per CU, 8 K tiles each
+    assert f(64, 8192, 28672, 128) == 4 * 64 * 28672 * 4  # 448 workgroups, not 560
+    assert f(64, 8192, 57344, 128) == 0      # more than half a CU's worth of column groups
 
 
 @pytest.mark.parametrize("M,K,N,G", [(4, 4096, 4096, 128), (64, 4160, 1024, 64)])
@@ -121,7 +124,8 @@ def test_unsplit_shapes_through_ws_entry(oracle, ops, M, K, N, G):
     assert _ulp_close(got, want, oracle)
 
 
-@pytest.mark.parametrize("K,N", [(8192, 10240), (8192, 8192), (8192, 57344), (28672, 8192)])
+@pytest.mark.parametrize("K,N", [(8192, 10240), (8192, 8192), (8192, 57344), (28672, 8192), (8192, 28672),
+                                 (8192, 14336)])
 def test_splitk_config5_m64_sampled(oracle, ops, K, N):
     """Config 5 at M = 64 through the workspace entry point, whole output on
     the GPU, sampled rows x columns against the oracle on column slices."""
