@@ -318,11 +318,14 @@ def bench_fp8(ops, M, K, N, steps, warmup, seed=0):
     ms, _ = GraphTimer(launch, 1, chunk=16).time(steps, warmup)
     us = ms * 1e3 / steps
     tf = 2 * M * K * N / (us * 1e-6) / 1e12
+    # the register-only MFMA rate on these same e4m3 values
+    same = operand_probe(ops, 1, A8, Bt, iters=2000)
     del Bt, A8, C
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     return {"leg": "fp8_e4m3_gemm", "M": M, "K": K, "N": N, "us_per_call": round(us, 2), "tflops": round(tf, 1),
-            "peak": FP8_PEAK_TFLOPS, "mfma_frac": round(tf / FP8_PEAK_TFLOPS, 4)}
+            "peak": FP8_PEAK_TFLOPS, "mfma_frac": round(tf / FP8_PEAK_TFLOPS, 4),
+            "sustained_same_operands": same, "frac_of_sustained": round(tf / same["value"], 4)}
 
 
 def bench_moe_layer(ops, steps, warmup, seed=0, T=512, E=8, topk=2, H=4096, I=14336, G=128):
@@ -463,6 +466,21 @@ def bench_w8a8(ops, M, K, N, steps, warmup, seed=0):
     ms, _ = GraphTimer(launch, 1, chunk=16).time(steps, warmup)
     us = ms * 1e3 / steps
     ops_per = 2 * M * K * N
+    # the register-only MFMA rate on these same quantized values, and the same
+    # GEMM on all-zero operands (the clock under the power limit depends on
+    # the values the matrix cores multiply)
+    same = operand_probe(ops, 0, Aq, Bt)
+    Az = torch.zeros_like(Aq)
+    Bz = torch.zeros_like(Bt)
+
+    def zlaunch(_i):
+        st = fn(Az.data_ptr(), Bz.data_ptr(), As.data_ptr(), Bs.data_ptr(), C.data_ptr(), M, N, K, ops.stream())
+        if st:
+            raise RuntimeError(f"lhq_gemm_w8a8_bf16: {ops.lib().last_error()}")
+
+    zms, _ = GraphTimer(zlaunch, 1, chunk=16).time(steps, warmup)
+    zus = zms * 1e3 / steps
+    del Az, Bz
     qms, _ = GraphTimer(qlaunch, 1, chunk=16).time(steps, warmup)
     qus = qms * 1e3 / steps
     qbytes = M * K * 2 + M * K + M * 4
@@ -485,10 +503,60 @@ def bench_w8a8(ops, M, K, N, steps, warmup, seed=0):
            "act_quant_us": qus, "act_quant_gbs": qbytes / (qus * 1e-6) / 1e9,
            "weight_quant_us": wus, "weight_quant_gbs": wbytes / (wus * 1e-6) / 1e9}
     res["mfma_frac"] = res["tops"] / INT8_PEAK_TOPS
+    res["sustained_same_operands"] = same
+    res["frac_of_sustained"] = res["tops"] / same["value"]
+    res["us_zero_operands"] = zus
+    res["tops_zero_operands"] = ops_per / (zus * 1e-6) / 1e12
     del Bt, Xb, Aq, As, C
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     return res
+
+
+PROBE_OPS_PER_MFMA = {0: 65536, 1: 131072, 2: 16384}
+
+
+def operand_probe(ops, kind: int, A, B, iters: int = 4000, steps: int = 5, warmup: int = 2):
+    """The matrix cores' rate on given operand values: lhq_probe_mfma_operands
+    with one workgroup of 4 waves per CU (one wave per SIMD, the W8A8 / FP8
+    tiles' occupancy), each wave issuing MFMAs on 16 accumulators in turn from
+    fragments it loaded once.  The fragments are bytes from the start of the
+    device tensors A and B (A blocks from A, B blocks from B), so the figure is
+    the register-only rate on the values a GEMM multiplies; the MFMA's power
+    draw, and with it the clock under the power limit, depends on them.
+    Returns the rate and the sustained shader clock (s_memtime over
+    s_memrealtime ticks)."""
+    import numpy as np
+    import torch
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    a = A.reshape(-1).view(torch.uint8)
+    b = B.reshape(-1).view(torch.uint8)
+    # [set][fragment: 4 A blocks, 4 B blocks][64 lanes x 16 bytes]; kind 1
+    # takes the fragments' high halves from the next 8 KiB of each operand
+    halves = []
+    for h in range(2 if kind == 1 else 1):
+        fa = a[h * 8192:(h + 1) * 8192].reshape(2, 4, 1024)
+        fb = b[h * 8192:(h + 1) * 8192].reshape(2, 4, 1024)
+        halves.append(torch.cat([fa, fb], dim=1).reshape(-1))
+    buf = torch.zeros(32768, dtype=torch.uint8, device="cuda")
+    src = torch.cat(halves)
+    buf[:src.numel()] = src
+    sink = ops.empty((cus,), np.int32)
+    clocks = torch.zeros(2 * cus, dtype=torch.int64, device="cuda")
+
+    def launch(_i):
+        st = ops.lib().cdll.lhq_probe_mfma_operands(kind, buf.data_ptr(), cus, iters, sink.data_ptr(),
+                                                    clocks.data_ptr(), ops.stream())
+        if st:
+            raise RuntimeError(f"lhq_probe_mfma_operands: {ops.lib().last_error()}")
+
+    ms, _ = GraphTimer(launch, 1, chunk=steps).time(steps, warmup)
+    rate = cus * 4 * iters * 32 * PROBE_OPS_PER_MFMA[kind] * steps / (ms * 1e-3) / 1e12
+    c = clocks.view(cus, 2).double()
+    ghz = float((c[:, 0] / c[:, 1]).mean()) * 0.1
+    del buf, sink, clocks
+    return {"value": round(rate, 1), "unit": "TOPS" if kind == 0 else "TFLOPS", "ghz": round(ghz, 3),
+            "us_per_launch": round(ms * 1e3 / steps, 1)}
 
 
 def mfma_ceiling(ops, steps: int = 5, warmup: int = 2):
@@ -525,6 +593,23 @@ def mfma_ceiling(ops, steps: int = 5, warmup: int = 2):
         out[name] = {"value": round(rate, 1), "unit": "TOPS" if kind in (0, 3, 7) else "TFLOPS", "peak": peak,
                      "frac": round(rate / peak, 4), "us_per_launch": round(ms * 1e3 / steps, 1)}
     del sink
+    # the W8A8 / FP8 tiles' order on operands from memory: uniformly random
+    # bytes (bf16: N(0,1) values) and zero bytes, which bound the rate a GEMM's
+    # own values give
+    import torch
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(7)
+    rnd = torch.randint(0, 256, (2, 16384), dtype=torch.uint8, device="cuda", generator=gen)
+    nrm = torch.randn((2, 8192), generator=gen, device="cuda").to(torch.bfloat16)
+    zero = torch.zeros((2, 16384), dtype=torch.uint8, device="cuda")
+    for kind, name, peak, data in ((0, "int8_32x32x32_tile_order", INT8_PEAK_TOPS, {"random": rnd, "zero": zero}),
+                                   (1, "fp8_32x32x64_tile_order", FP8_PEAK_TFLOPS, {"random": rnd, "zero": zero}),
+                                   (2, "bf16_16x16x32_tile_order", BF16_PEAK_TFLOPS, {"normal": nrm, "zero": zero})):
+        for dn, d in data.items():
+            r = operand_probe(ops, kind, d[0], d[1], iters={0: 4000, 1: 2000, 2: 8000}[kind])
+            r.update(peak=peak, frac=round(r["value"] / peak, 4))
+            out[f"{name}_{dn}"] = r
+    del rnd, nrm, zero
     return out
 
 
@@ -748,13 +833,18 @@ def main() -> int:
     if args.only == "w8a8":
         for m in (4096, 2048):
             r = bench_w8a8(ops, m, 4096, 14336, args.w8a8_steps, max(10, args.w8a8_steps // 10))
+            log(f"w8a8 M={m} K=4096 N=14336: {r['us_per_call']:.1f} us  {r['tops']:.0f} TOPS "
+                f"({100 * r['mfma_frac']:.1f}% of int8 peak, {100 * r['frac_of_sustained']:.1f}% of the "
+                f"{r['sustained_same_operands']['value']:.0f} TOPS the MFMAs sustain on these values at "
+                f"{r['sustained_same_operands']['ghz']:.2f} GHz); zero operands {r['us_zero_operands']:.1f} us")
             print(json.dumps({"leg": "w8a8_prefill", **r}), flush=True)
         return 0
     if args.only == "fp8":
         for m in (4096, 2048):
             r = bench_fp8(ops, m, 4096, 14336, args.w8a8_steps, max(10, args.w8a8_steps // 10))
             log(f"fp8 e4m3 GEMM M={m} K=4096 N=14336: {r['us_per_call']:.1f} us  {r['tflops']:.0f} TFLOPS "
-                f"({100 * r['mfma_frac']:.1f}% of fp8 peak)")
+                f"({100 * r['mfma_frac']:.1f}% of fp8 peak, {100 * r['frac_of_sustained']:.1f}% of the "
+                f"{r['sustained_same_operands']['value']:.0f} TFLOPS the MFMAs sustain on these values)")
             print(json.dumps(r), flush=True)
         return 0
     if args.only == "mfma":
@@ -798,6 +888,10 @@ def main() -> int:
             log(f"  {r['us_per_call']:.1f} us/call  {r['tops']:.0f} TOPS ({100 * r['mfma_frac']:.1f}% of int8 peak); "
                 f"act quant {r['act_quant_us']:.1f} us ({r['act_quant_gbs']:.0f} GB/s); "
                 f"weight quant (per column) {r['weight_quant_us']:.1f} us ({r['weight_quant_gbs']:.0f} GB/s)")
+            so = r["sustained_same_operands"]
+            log(f"  register-only MFMAs on the same values: {so['value']:.0f} TOPS at {so['ghz']:.2f} GHz "
+                f"(the GEMM reaches {100 * r['frac_of_sustained']:.1f}% of it); "
+                f"the GEMM on zero operands: {r['us_zero_operands']:.1f} us ({r['tops_zero_operands']:.0f} TOPS)")
             w8.append(r)
 
     ceiling = None
@@ -807,14 +901,18 @@ def main() -> int:
         log(f"matrix-core ceiling (register-only MFMA probe, all CUs): int8 at one wave per SIMD {c8['value']:.0f} TOPS "
             f"({100 * c8['frac']:.1f}% of peak); bf16 {ceiling['bf16_16x16x32']['value']:.0f} TFLOPS "
             f"({100 * ceiling['bf16_16x16x32']['frac']:.1f}%)")
-        for r in w8:
-            log(f"  w8a8 M={r['M']}: {100 * r['tops'] / c8['value']:.1f}% of the sustained int8 rate")
+        cr = ceiling["int8_32x32x32_tile_order_random"]
+        cz = ceiling["int8_32x32x32_tile_order_zero"]
+        log(f"  int8 in the tile's order on operands from memory: random bytes {cr['value']:.0f} TOPS at "
+            f"{cr['ghz']:.2f} GHz, zero bytes {cz['value']:.0f} TOPS at {cz['ghz']:.2f} GHz")
 
     fp8 = []
     if not args.no_w8a8:
         log(f"fp8 e4m3 GEMM M=4096 K=4096 N=14336: {args.w8a8_steps} steps")
         r = bench_fp8(ops, 4096, 4096, 14336, args.w8a8_steps, max(10, args.w8a8_steps // 10))
-        log(f"  {r['us_per_call']:.1f} us/call  {r['tflops']:.0f} TFLOPS ({100 * r['mfma_frac']:.1f}% of fp8 peak)")
+        log(f"  {r['us_per_call']:.1f} us/call  {r['tflops']:.0f} TFLOPS ({100 * r['mfma_frac']:.1f}% of fp8 peak; "
+            f"{100 * r['frac_of_sustained']:.1f}% of the {r['sustained_same_operands']['value']:.0f} TFLOPS the MFMAs "
+            f"sustain on these values)")
         fp8.append(r)
 
     pre = [] if args.no_prefill else prefill_legs(ops)
@@ -858,7 +956,9 @@ def main() -> int:
              "value": round(r["tops"], 1), "unit": "TOPS", "peak": INT8_PEAK_TOPS,
              "frac": round(r["mfma_frac"], 4), "act_quant_us": round(r["act_quant_us"], 2),
              "weight_quant_us": round(r["weight_quant_us"], 2), "weight_quant_gbs": round(r["weight_quant_gbs"], 1),
-             "frac_of_sustained": (round(r["tops"] / ceiling["int8_32x32x32_one_wave"]["value"], 4) if ceiling else None)}
+             "sustained_same_operands": r["sustained_same_operands"],
+             "frac_of_sustained": round(r["frac_of_sustained"], 4),
+             "us_zero_operands": round(r["us_zero_operands"], 2)}
             for r in w8],
         "mfma_ceiling": ceiling,
         "w8a8_cpu_baseline": cpu_w8,

@@ -317,6 +317,21 @@ int lhq_selftest_bf16(unsigned long long* counts, void* stream);
  * and kind 3's instruction.  One launch performs blocks * 4 * iters * 4
  * MFMAs.  sink: `blocks` device ints (written). */
 int lhq_probe_mfma_rate(int kind, int blocks, int iters, int* sink, void* stream);
+/* Matrix-core rate on the caller's operand values: `blocks` workgroups of 4
+ * waves; each wave loads two sets of 8 fragments (4 A blocks, 4 B blocks)
+ * from `operands` once, then runs `iters` rounds of 32 MFMAs: two k steps,
+ * each one MFMA on each of 16 accumulators in turn (the W8A8 / FP8 tiles'
+ * order).  The rate depends on the values through the power limit.  Kinds:
+ * 0: v_mfma_i32_32x32x32_i8 (65,536 ops each), 1:
+ * v_mfma_scale_f32_32x32x64_f8f6f4, e4m3 with unit scales (131,072 flops),
+ * 2: v_mfma_f32_16x16x32_bf16 (16,384 flops).  operands: 32 KiB of device
+ * memory; fragment x (0..7) of set s (0..1) for lane l is the 16 bytes at
+ * ((8s + x) * 64 + l) * 16 (kind 1: the fragment's low half there, its high
+ * half 16 KiB further).  sink: `blocks` device ints (written).  clocks: null,
+ * or 2 * `blocks` device uint64 set to {shader-clock ticks, 100 MHz ticks}
+ * over wave 0's loop in each workgroup. */
+int lhq_probe_mfma_operands(int kind, const void* operands, int blocks, int iters, int* sink,
+                            unsigned long long* clocks, void* stream);
 
 #ifdef __cplusplus
 }

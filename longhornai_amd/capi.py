@@ -81,6 +81,7 @@ SIGNATURES = {
     "lhq_gemm_f32_batched": [_p, _p, _p, _i, _i, _i, _i, _f, _f, _p],
     "lhq_selftest_bf16": [_p, _p],
     "lhq_probe_mfma_rate": [_i, _i, _i, _p, _p],
+    "lhq_probe_mfma_operands": [_i, _p, _i, _i, _p, _p, _p],
 }
 _RESTYPES = {
     "lhq_status_string": C.c_char_p,

@@ -141,6 +141,78 @@ __global__ __launch_bounds__(256) void mfma_rate_kernel(int iters, int* sink) {
     }
 }
 
+
+// Matrix-core rate on operands read from memory, in a GEMM tile's issue
+// order.  Each wave loads two sets of 8 operand fragments (4 A blocks, 4 B
+// blocks) once; one round is two k steps, each issuing one MFMA on each of
+// the 16 accumulators (A block i x B block j) in turn, as the W8A8 and FP8
+// tiles do.  There is no memory traffic in the loop, but the operand values
+// are the caller's: the matrix cores draw more power on dense, changing bit
+// patterns, and under the power limit the clock falls with it.
+// KIND 0: v_mfma_i32_32x32x32_i8 (16-byte fragments), KIND 1:
+// v_mfma_scale_f32_32x32x64_f8f6f4 on e4m3 with unit scales (32-byte
+// fragments, low halves at ops, high halves at ops + 16 KiB), KIND 2:
+// v_mfma_f32_16x16x32_bf16 (16-byte fragments).  Fragment x of set s for
+// lane l: the 16 bytes at ops + ((8s + x) * 64 + l) * 16.
+// clocks (optional): per workgroup, wave 0's shader-clock ticks
+// (s_memtime) and 100 MHz reference ticks (s_memrealtime) over its loop.
+template <int KIND>
+__global__ __launch_bounds__(256) void mfma_operand_rate_kernel(const uint8_t* __restrict__ ops, int iters,
+                                                                int* sink, unsigned long long* clocks) {
+    const int lane = threadIdx.x & 63;
+    u32x4_t f[2][8], h[2][8];
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int x = 0; x < 8; ++x) {
+            const size_t off = static_cast<size_t>((8 * st + x) * 64 + lane) * 16;
+            f[st][x] = *reinterpret_cast<const u32x4_t*>(ops + off);
+            if constexpr (KIND == 1) h[st][x] = *reinterpret_cast<const u32x4_t*>(ops + 16384 + off);
+        }
+    using acc_t = typename std::conditional<KIND == 0, i32x16_t,
+                                            typename std::conditional<KIND == 1, f32x16_t, f32x4_t>::type>::type;
+    acc_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = acc_t{};
+    const unsigned long long t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                const int i = t / 4, j = t % 4;
+                if constexpr (KIND == 0)
+                    acc[i][j] = mfma_i8_32x32x32(f[kk][4 + j], f[kk][i], acc[i][j]);
+                else if constexpr (KIND == 1)
+                    acc[i][j] = mfma_fp8_32x32x64(f[kk][4 + j], h[kk][4 + j], f[kk][i], h[kk][i], acc[i][j]);
+                else
+                    acc[i][j] = mfma_bf16_16x16x32(f[kk][4 + j], f[kk][i], acc[i][j]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+    }
+    const unsigned long long t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+    int r = 0;
+    float rf = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < static_cast<int>(sizeof(acc_t) / 4); ++e) {
+                if constexpr (KIND == 0) r += acc[i][j][e];
+                else rf += acc[i][j][e];
+            }
+    if (threadIdx.x == 0) {
+        sink[blockIdx.x] = KIND == 0 ? r : __float_as_int(rf);
+        if (clocks) {
+            clocks[2 * blockIdx.x] = t1 - t0;
+            clocks[2 * blockIdx.x + 1] = r1 - r0;
+        }
+    }
+}
+
 }  // namespace
 }  // namespace lhq
 
@@ -160,6 +232,19 @@ extern "C" int lhq_probe_mfma_rate(int kind, int blocks, int iters, int* sink, v
     else if (kind == 6) mfma_rate_kernel<6><<<blocks, 256, 0, s>>>(iters, sink);
     else mfma_rate_kernel<7><<<blocks, 256, 0, s>>>(iters, sink);
     return check_launch("probe_mfma_rate");
+}
+
+extern "C" int lhq_probe_mfma_operands(int kind, const void* operands, int blocks, int iters, int* sink,
+                                       unsigned long long* clocks, void* stream) {
+    LHQ_REQUIRE(operands && sink, "probe_mfma_operands: null operands or sink");
+    LHQ_REQUIRE(kind >= 0 && kind <= 2, "probe_mfma_operands: kind %d (0..2)", kind);
+    LHQ_REQUIRE(blocks >= 1 && iters >= 1, "probe_mfma_operands: blocks %d, iters %d", blocks, iters);
+    hipStream_t s = as_stream(stream);
+    auto src = static_cast<const uint8_t*>(operands);
+    if (kind == 0) mfma_operand_rate_kernel<0><<<blocks, 256, 0, s>>>(src, iters, sink, clocks);
+    else if (kind == 1) mfma_operand_rate_kernel<1><<<blocks, 256, 0, s>>>(src, iters, sink, clocks);
+    else mfma_operand_rate_kernel<2><<<blocks, 256, 0, s>>>(src, iters, sink, clocks);
+    return check_launch("probe_mfma_operands");
 }
 
 extern "C" int lhq_selftest_bf16(unsigned long long* counts, void* stream) {

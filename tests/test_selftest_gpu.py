@@ -32,3 +32,33 @@ def test_mfma_rate_probe_runs_and_rejects_bad_arguments(lib):
         lib.call("lhq_probe_mfma_rate", kind, 16, 8, sink.data_ptr(), ops.stream())
     torch.cuda.synchronize()
     assert lib.status("lhq_probe_mfma_rate", 8, 16, 8, sink.data_ptr(), ops.stream()) != 0
+
+
+def test_mfma_operand_probe_runs_and_rejects_bad_arguments(lib):
+    """The matrix-core rate probe on operands from memory (bench.py's
+    same-operands figures): every kind completes and writes one value per
+    workgroup and two clock counts; the int8 kind's accumulators grow
+    linearly in the round count (integer MFMAs are exact); an unknown kind
+    and a null operand buffer are refused before any launch."""
+    import torch
+    from longhornai_amd import ops
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5)
+    src = torch.randint(0, 256, (32768,), dtype=torch.uint8, device="cuda", generator=gen)
+    sink = torch.full((16,), -1, dtype=torch.int32, device="cuda")
+    clocks = torch.zeros(32, dtype=torch.int64, device="cuda")
+    for kind in range(3):
+        lib.call("lhq_probe_mfma_operands", kind, src.data_ptr(), 16, 4, sink.data_ptr(), clocks.data_ptr(),
+                 ops.stream())
+        torch.cuda.synchronize()
+        c = clocks.view(16, 2).cpu()
+        assert bool((c[:, 1] > 0).all()) and bool((c[:, 0] > c[:, 1]).all()), c
+    sums = []
+    for iters in (1, 3):
+        lib.call("lhq_probe_mfma_operands", 0, src.data_ptr(), 16, iters, sink.data_ptr(), 0, ops.stream())
+        torch.cuda.synchronize()
+        sums.append(sink.cpu().tolist())
+    assert len(set(sums[0])) == 1 and sums[0][0] != 0
+    assert all((3 * a - b) % 2**32 == 0 for a, b in zip(sums[0], sums[1]))
+    assert lib.status("lhq_probe_mfma_operands", 3, src.data_ptr(), 16, 4, sink.data_ptr(), 0, ops.stream()) != 0
+    assert lib.status("lhq_probe_mfma_operands", 0, 0, 16, 4, sink.data_ptr(), 0, ops.stream()) != 0
