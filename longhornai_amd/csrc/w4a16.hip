@@ -1800,20 +1800,25 @@ int device_cus() {
 
 // The tile kernel over `rows` rows (dense / batched), or over a ragged group
 // table of `groups` groups holding `rows` rows in all: each group adds at
-// most one partial row tile.  Layout 1 (64 x 256) unless its grid holds
-// fewer than two workgroups per CU (two fit, by LDS and registers) and K is
-// long: then layout 2 splits K for twice the workgroups, and where even its
-// grid holds at most one workgroup per CU, layout 3 (eight waves, K in four
+// most one partial row tile.  Layout 1 (64 x 256) unless its grid holds at
+// most one workgroup per CU (two fit, by LDS and registers) and K is long:
+// then layout 2 splits K for twice the workgroups, and where even its grid
+// holds at most one workgroup per CU, layout 3 (eight waves, K in four
 // parts, 128 KiB of LDS) doubles the waves again.  Measured on MI355X:
 // 64 x 256 beat 128 x 128 on every shape tried (M=4096 K=8192 N=28672 2104
-// vs 2215 us; config 4's grouped GEMM 196 vs 229 us).  LHQ_W4_MMA_L (0..3)
+// vs 2215 us; config 4's grouped GEMM 196 vs 229 us).  Between one and two
+// workgroups per CU layout 1 beats layout 2 (us, layout 1 vs 2): K=8192
+// N=28672 M=192 118-120 vs 127-128, M=256 132 vs 144-146; M=320 K=4096
+// N=14336 59 vs 66; config 4's grouped down projection (K=14336, N=4096,
+// 384 workgroups) 195 vs 215.  At or below one per CU layout 2 wins: M=128
+// K=8192 N=28672 83 vs 102, M=448 K=N=8192 74 vs 95.  LHQ_W4_MMA_L (0..3)
 // forces a layout.
 template <bool GR, bool SWI = false>
 int launch_mma(const W4Args& a, int64_t rows, int groups, int batch, hipStream_t s, const char* who) {
     static const int env_l = tuning_knob("LHQ_W4_MMA_L", -1);
     int l = 1;
     const int64_t wgs1 = static_cast<int64_t>(ceil_div(a.Nt, 4 * MM_CT)) * (ceil_div64(rows, 64) + groups) * batch;
-    if (wgs1 < 2 * static_cast<int64_t>(device_cus()) && a.Kt >= 16) l = 2;
+    if (wgs1 <= static_cast<int64_t>(device_cus()) && a.Kt >= 16) l = 2;
     if (2 * wgs1 <= static_cast<int64_t>(device_cus()) && a.Kt >= 32) l = 3;
     if (env_l >= 0 && env_l <= 3) l = env_l;
     const int64_t tiles = ceil_div64(rows, l == 0 ? 128 : 64) + groups;
