@@ -133,6 +133,33 @@ class GraphTimer:
         wall = (time.perf_counter() - t0) * 1e3
         return ev0.elapsed_time(ev1), wall
 
+    def chunk_percentiles(self, steps: int):
+        """A second pass over `steps` launches with a HIP event after every
+        graph replay (a chunk of back-to-back launches): returns the 50th and
+        90th percentiles over the chunks of the time per launch, in us.  Run
+        apart from time() so its events do not enter the reported total."""
+        torch = self.torch
+        self.prepare(steps)
+        torch.cuda.synchronize()
+        torch.cuda._sleep(1_000_000)
+        evs = [torch.cuda.Event(enable_timing=True)]
+        evs[0].record()
+        sizes = []
+        done = 0
+        while done < steps:
+            n = min(self.chunk, steps - done)
+            self._graph(n, done).replay()
+            e = torch.cuda.Event(enable_timing=True)
+            e.record()
+            evs.append(e)
+            sizes.append(n)
+            done += n
+        torch.cuda.synchronize()
+        per = sorted(evs[i].elapsed_time(evs[i + 1]) * 1e3 / sizes[i] for i in range(len(sizes)))
+        def pct(q):
+            return per[min(len(per) - 1, int(round(q * (len(per) - 1))))]
+        return pct(0.5), pct(0.9)
+
 
 def make_w4_sets(ops, K: int, N: int, G: int, nsets: int, seed: int):
     """`nsets` distinct asymmetric int4 weight sets quantized on the device
@@ -230,10 +257,12 @@ def bench_w4a16(ops, M, K, N, G, steps, warmup, seed=0, min_rotate_bytes=2 * INF
     timer = GraphTimer(launch, nsets, chunk=nsets * max(1, 64 // nsets))
     ms, wall = timer.time(steps, warmup)
     us = ms * 1e3 / steps
+    p50, p90 = timer.chunk_percentiles(steps)
     res = {"M": M, "K": K, "N": N, "G": G, "entry": name, "workspace_bytes": ws_bytes,
            "bytes_per_call": per, "weight_sets": nsets,
            "rotate_bytes": per * nsets, "us_per_call": us, "gbs": per / (us * 1e-6) / 1e9,
-           "elapsed_ms": ms, "wall_ms": wall}
+           "elapsed_ms": ms, "wall_ms": wall, "chunk_launches": timer.chunk,
+           "us_p50_chunk": p50, "us_p90_chunk": p90}
     res["hbm_frac"] = res["gbs"] / HBM_PEAK_GBS
     del timer, sets, A, C, ws
     torch.cuda.synchronize()
@@ -463,8 +492,10 @@ def bench_w8a8(ops, M, K, N, steps, warmup, seed=0):
 
     qlaunch(0)
     torch.cuda.synchronize()
-    ms, _ = GraphTimer(launch, 1, chunk=16).time(steps, warmup)
+    timer = GraphTimer(launch, 1, chunk=16)
+    ms, _ = timer.time(steps, warmup)
     us = ms * 1e3 / steps
+    p50, p90 = timer.chunk_percentiles(steps)
     ops_per = 2 * M * K * N
     # the register-only MFMA rate on these same quantized values, and the same
     # GEMM on all-zero operands (the clock under the power limit depends on
@@ -503,6 +534,7 @@ def bench_w8a8(ops, M, K, N, steps, warmup, seed=0):
            "act_quant_us": qus, "act_quant_gbs": qbytes / (qus * 1e-6) / 1e9,
            "weight_quant_us": wus, "weight_quant_gbs": wbytes / (wus * 1e-6) / 1e9}
     res["mfma_frac"] = res["tops"] / INT8_PEAK_TOPS
+    res["us_p50_chunk"], res["us_p90_chunk"] = p50, p90
     res["sustained_same_operands"] = same
     res["frac_of_sustained"] = res["tops"] / same["value"]
     res["us_zero_operands"] = zus
@@ -874,7 +906,9 @@ def main() -> int:
     log(f"w4a16 decode M={M} K={K} N={N} G={G}: {args.warmup} warmup + {args.steps} timed steps")
     w4 = bench_w4a16(ops, M, K, N, G, args.steps, args.warmup)
     log(f"  {w4['us_per_call']:.2f} us/call  {w4['gbs']:.1f} GB/s  ({100 * w4['hbm_frac']:.1f}% of HBM peak), "
-        f"{w4['weight_sets']} rotating sets = {w4['rotate_bytes'] / 2**20:.0f} MiB")
+        f"{w4['weight_sets']} rotating sets = {w4['rotate_bytes'] / 2**20:.0f} MiB; per-launch time over "
+        f"{w4['chunk_launches']}-launch chunks (a second pass): p50 {w4['us_p50_chunk']:.2f} us, "
+        f"p90 {w4['us_p90_chunk']:.2f} us")
 
     if args.only == "w4a16":
         print(json.dumps({"leg": "w4a16_decode", **w4}), flush=True)
@@ -950,12 +984,15 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(w4["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(w4["hbm_frac"], 4), "traffic": traffic,
                      "kernel": "w4_decode_i8_kernel", "algorithmic_bytes": w4["bytes_per_call"],
-                     "us_per_launch": round(w4["us_per_call"], 3)},
+                     "us_per_launch": round(w4["us_per_call"], 3),
+                     "us_per_launch_p50_p90": [round(w4["us_p50_chunk"], 3), round(w4["us_p90_chunk"], 3)],
+                     "p50_p90_over": f"{w4['chunk_launches']}-launch chunks of a second timed pass"},
         "w8a8_prefill": [
             {"M": r["M"], "K": r["K"], "N": r["N"], "us_per_call": round(r["us_per_call"], 2),
              "value": round(r["tops"], 1), "unit": "TOPS", "peak": INT8_PEAK_TOPS,
              "frac": round(r["mfma_frac"], 4), "act_quant_us": round(r["act_quant_us"], 2),
              "weight_quant_us": round(r["weight_quant_us"], 2), "weight_quant_gbs": round(r["weight_quant_gbs"], 1),
+             "us_per_call_p50_p90": [round(r["us_p50_chunk"], 2), round(r["us_p90_chunk"], 2)],
              "sustained_same_operands": r["sustained_same_operands"],
              "frac_of_sustained": round(r["frac_of_sustained"], 4),
              "us_zero_operands": round(r["us_zero_operands"], 2)}
