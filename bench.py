@@ -347,14 +347,27 @@ def bench_fp8(ops, M, K, N, steps, warmup, seed=0):
     ms, _ = GraphTimer(launch, 1, chunk=16).time(steps, warmup)
     us = ms * 1e3 / steps
     tf = 2 * M * K * N / (us * 1e-6) / 1e12
-    # the register-only MFMA rate on these same e4m3 values
+    # the register-only MFMA rate on these same e4m3 values, and the same
+    # GEMM on all-zero operands (which hold a higher clock)
     same = operand_probe(ops, 1, A8, Bt, iters=2000)
-    del Bt, A8, C
+    Az = torch.zeros_like(A8)
+    Bz = torch.zeros_like(Bt)
+
+    def zlaunch(_i):
+        st = fn(Az.data_ptr(), Bz.data_ptr(), sA.data_ptr(), sB.data_ptr(), C.data_ptr(), M, N, K, 1.0, 0.0,
+                ops.stream())
+        if st:
+            raise RuntimeError(f"lhq_gemm_fp8_e4m3: {L.last_error()}")
+
+    zms, _ = GraphTimer(zlaunch, 1, chunk=16).time(steps, warmup)
+    zus = zms * 1e3 / steps
+    del Bt, A8, C, Az, Bz
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     return {"leg": "fp8_e4m3_gemm", "M": M, "K": K, "N": N, "us_per_call": round(us, 2), "tflops": round(tf, 1),
             "peak": FP8_PEAK_TFLOPS, "mfma_frac": round(tf / FP8_PEAK_TFLOPS, 4),
-            "sustained_same_operands": same, "frac_of_sustained": round(tf / same["value"], 4)}
+            "sustained_same_operands": same, "frac_of_sustained": round(tf / same["value"], 4),
+            "us_zero_operands": round(zus, 2)}
 
 
 def bench_moe_layer(ops, steps, warmup, seed=0, T=512, E=8, topk=2, H=4096, I=14336, G=128):
@@ -876,7 +889,8 @@ def main() -> int:
             r = bench_fp8(ops, m, 4096, 14336, args.w8a8_steps, max(10, args.w8a8_steps // 10))
             log(f"fp8 e4m3 GEMM M={m} K=4096 N=14336: {r['us_per_call']:.1f} us  {r['tflops']:.0f} TFLOPS "
                 f"({100 * r['mfma_frac']:.1f}% of fp8 peak, {100 * r['frac_of_sustained']:.1f}% of the "
-                f"{r['sustained_same_operands']['value']:.0f} TFLOPS the MFMAs sustain on these values)")
+                f"{r['sustained_same_operands']['value']:.0f} TFLOPS the MFMAs sustain on these values); "
+                f"zero operands {r['us_zero_operands']:.1f} us")
             print(json.dumps(r), flush=True)
         return 0
     if args.only == "mfma":
@@ -946,7 +960,7 @@ def main() -> int:
         r = bench_fp8(ops, 4096, 4096, 14336, args.w8a8_steps, max(10, args.w8a8_steps // 10))
         log(f"  {r['us_per_call']:.1f} us/call  {r['tflops']:.0f} TFLOPS ({100 * r['mfma_frac']:.1f}% of fp8 peak; "
             f"{100 * r['frac_of_sustained']:.1f}% of the {r['sustained_same_operands']['value']:.0f} TFLOPS the MFMAs "
-            f"sustain on these values)")
+            f"sustain on these values); zero operands {r['us_zero_operands']:.1f} us")
         fp8.append(r)
 
     pre = [] if args.no_prefill else prefill_legs(ops)
