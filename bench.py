@@ -558,7 +558,8 @@ def bench_w8a8(ops, M, K, N, steps, warmup, seed=0):
     return res
 
 
-PROBE_OPS_PER_MFMA = {0: 65536, 1: 131072, 2: 16384}
+PROBE_OPS_PER_MFMA = {0: 65536, 1: 131072, 2: 16384, 3: 65536, 4: 65536, 5: 32768, 6: 32768}
+PROBE_MFMAS_PER_ITER = {0: 32, 1: 32, 2: 32, 3: 32, 4: 64, 5: 64, 6: 32}
 
 
 def operand_probe(ops, kind: int, A, B, iters: int = 4000, steps: int = 5, warmup: int = 2):
@@ -596,11 +597,11 @@ def operand_probe(ops, kind: int, A, B, iters: int = 4000, steps: int = 5, warmu
             raise RuntimeError(f"lhq_probe_mfma_operands: {ops.lib().last_error()}")
 
     ms, _ = GraphTimer(launch, 1, chunk=steps).time(steps, warmup)
-    rate = cus * 4 * iters * 32 * PROBE_OPS_PER_MFMA[kind] * steps / (ms * 1e-3) / 1e12
+    rate = cus * 4 * iters * PROBE_MFMAS_PER_ITER[kind] * PROBE_OPS_PER_MFMA[kind] * steps / (ms * 1e-3) / 1e12
     c = clocks.view(cus, 2).double()
     ghz = float((c[:, 0] / c[:, 1]).mean()) * 0.1
     del buf, sink, clocks
-    return {"value": round(rate, 1), "unit": "TOPS" if kind == 0 else "TFLOPS", "ghz": round(ghz, 3),
+    return {"value": round(rate, 1), "unit": "TOPS" if kind in (0, 3, 4, 5, 6) else "TFLOPS", "ghz": round(ghz, 3),
             "us_per_launch": round(ms * 1e3 / steps, 1)}
 
 
@@ -649,9 +650,14 @@ def mfma_ceiling(ops, steps: int = 5, warmup: int = 2):
     zero = torch.zeros((2, 16384), dtype=torch.uint8, device="cuda")
     for kind, name, peak, data in ((0, "int8_32x32x32_tile_order", INT8_PEAK_TOPS, {"random": rnd, "zero": zero}),
                                    (1, "fp8_32x32x64_tile_order", FP8_PEAK_TFLOPS, {"random": rnd, "zero": zero}),
-                                   (2, "bf16_16x16x32_tile_order", BF16_PEAK_TFLOPS, {"normal": nrm, "zero": zero})):
+                                   (2, "bf16_16x16x32_tile_order", BF16_PEAK_TFLOPS, {"normal": nrm, "zero": zero}),
+                                   (3, "int8_32x32x32_k_chain2", INT8_PEAK_TOPS, {"random": rnd}),
+                                   (4, "int8_32x32x32_k_chain4", INT8_PEAK_TOPS, {"random": rnd}),
+                                   (5, "int8_16x16x64_k_chain4", INT8_PEAK_TOPS, {"random": rnd, "zero": zero}),
+                                   (6, "int8_16x16x64_tile_order", INT8_PEAK_TOPS, {"random": rnd})):
         for dn, d in data.items():
-            r = operand_probe(ops, kind, d[0], d[1], iters={0: 4000, 1: 2000, 2: 8000}[kind])
+            r = operand_probe(ops, kind, d[0], d[1],
+                              iters={0: 4000, 1: 2000, 2: 8000, 3: 4000, 4: 2000, 5: 4000, 6: 8000}[kind])
             r.update(peak=peak, frac=round(r["value"] / peak, 4))
             out[f"{name}_{dn}"] = r
     del rnd, nrm, zero

@@ -152,7 +152,11 @@ __global__ __launch_bounds__(256) void mfma_rate_kernel(int iters, int* sink) {
 // KIND 0: v_mfma_i32_32x32x32_i8 (16-byte fragments), KIND 1:
 // v_mfma_scale_f32_32x32x64_f8f6f4 on e4m3 with unit scales (32-byte
 // fragments, low halves at ops, high halves at ops + 16 KiB), KIND 2:
-// v_mfma_f32_16x16x32_bf16 (16-byte fragments).  Fragment x of set s for
+// v_mfma_f32_16x16x32_bf16 (16-byte fragments), KINDs 3 and 4: KIND 0's
+// instruction and operands issued as k chains of 2 and 4 on one accumulator
+// (32 and 64 MFMAs per iteration; KIND 0-2 issue 32), KINDs 5 and 6:
+// v_mfma_i32_16x16x64_i8 on the same fragments as k chains of 4 (64 MFMAs
+// per iteration) and one per accumulator in turn (32).  Fragment x of set s for
 // lane l: the 16 bytes at ops + ((8s + x) * 64 + l) * 16.
 // clocks (optional): per workgroup, wave 0's shader-clock ticks
 // (s_memtime) and 100 MHz reference ticks (s_memrealtime) over its loop.
@@ -169,28 +173,60 @@ __global__ __launch_bounds__(256) void mfma_operand_rate_kernel(const uint8_t* _
             f[st][x] = *reinterpret_cast<const u32x4_t*>(ops + off);
             if constexpr (KIND == 1) h[st][x] = *reinterpret_cast<const u32x4_t*>(ops + 16384 + off);
         }
-    using acc_t = typename std::conditional<KIND == 0, i32x16_t,
+    using acc_t = typename std::conditional<KIND == 0 || KIND >= 3, i32x16_t,
                                             typename std::conditional<KIND == 1, f32x16_t, f32x4_t>::type>::type;
     acc_t acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = acc_t{};
+    i32x4_t acc4[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc4[i][j] = i32x4_t{};
     const unsigned long long t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
     for (int it = 0; it < iters; ++it) {
+        if constexpr (KIND == 5 || KIND == 6) {
+            // v_mfma_i32_16x16x64_i8 on the same fragments (16 bytes of a
+            // 16x64 block per lane): KIND 5 as k chains of 4 on one
+            // accumulator, KIND 6 one MFMA per accumulator in turn
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
+            for (int r = 0; r < (KIND == 5 ? 16 : 2); ++r)
 #pragma unroll
-            for (int t = 0; t < 16; ++t) {
-                const int i = t / 4, j = t % 4;
-                if constexpr (KIND == 0)
+                for (int c = 0; c < (KIND == 5 ? 4 : 16); ++c) {
+                    const int t = KIND == 5 ? r : c, kk = KIND == 5 ? (c & 1) : r;
+                    const int i = t / 4, j = t % 4;
+                    acc4[i][j] = mfma_i8_16x16x64(f[kk][4 + j], f[kk][i], acc4[i][j]);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+        } else if constexpr (KIND == 3 || KIND == 4) {
+            // k chains: 2 (KIND 3) or 4 (KIND 4) MFMAs in a row on one
+            // accumulator, each taking the previous one's result as SrcC
+            constexpr int kChain = KIND == 3 ? 2 : 4;
+#pragma unroll
+            for (int t = 0; t < 16; ++t)
+#pragma unroll
+                for (int c = 0; c < kChain; ++c) {
+                    const int i = t / 4, j = t % 4, kk = c & 1;
                     acc[i][j] = mfma_i8_32x32x32(f[kk][4 + j], f[kk][i], acc[i][j]);
-                else if constexpr (KIND == 1)
-                    acc[i][j] = mfma_fp8_32x32x64(f[kk][4 + j], h[kk][4 + j], f[kk][i], h[kk][i], acc[i][j]);
-                else
-                    acc[i][j] = mfma_bf16_16x16x32(f[kk][4 + j], f[kk][i], acc[i][j]);
-                __builtin_amdgcn_sched_barrier(0);
-            }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+        } else {
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                for (int t = 0; t < 16; ++t) {
+                    const int i = t / 4, j = t % 4;
+                    if constexpr (KIND == 0)
+                        acc[i][j] = mfma_i8_32x32x32(f[kk][4 + j], f[kk][i], acc[i][j]);
+                    else if constexpr (KIND == 1)
+                        acc[i][j] = mfma_fp8_32x32x64(f[kk][4 + j], h[kk][4 + j], f[kk][i], h[kk][i], acc[i][j]);
+                    else
+                        acc[i][j] = mfma_bf16_16x16x32(f[kk][4 + j], f[kk][i], acc[i][j]);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+        }
     }
     const unsigned long long t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
     int r = 0;
@@ -201,11 +237,17 @@ __global__ __launch_bounds__(256) void mfma_operand_rate_kernel(const uint8_t* _
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int e = 0; e < static_cast<int>(sizeof(acc_t) / 4); ++e) {
-                if constexpr (KIND == 0) r += acc[i][j][e];
+                if constexpr (KIND == 0 || KIND >= 3) r += acc[i][j][e];
                 else rf += acc[i][j][e];
             }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) r += acc4[i][j][e];
     if (threadIdx.x == 0) {
-        sink[blockIdx.x] = KIND == 0 ? r : __float_as_int(rf);
+        sink[blockIdx.x] = (KIND == 0 || KIND >= 3) ? r : __float_as_int(rf);
         if (clocks) {
             clocks[2 * blockIdx.x] = t1 - t0;
             clocks[2 * blockIdx.x + 1] = r1 - r0;
@@ -237,13 +279,17 @@ extern "C" int lhq_probe_mfma_rate(int kind, int blocks, int iters, int* sink, v
 extern "C" int lhq_probe_mfma_operands(int kind, const void* operands, int blocks, int iters, int* sink,
                                        unsigned long long* clocks, void* stream) {
     LHQ_REQUIRE(operands && sink, "probe_mfma_operands: null operands or sink");
-    LHQ_REQUIRE(kind >= 0 && kind <= 2, "probe_mfma_operands: kind %d (0..2)", kind);
+    LHQ_REQUIRE(kind >= 0 && kind <= 6, "probe_mfma_operands: kind %d (0..6)", kind);
     LHQ_REQUIRE(blocks >= 1 && iters >= 1, "probe_mfma_operands: blocks %d, iters %d", blocks, iters);
     hipStream_t s = as_stream(stream);
     auto src = static_cast<const uint8_t*>(operands);
     if (kind == 0) mfma_operand_rate_kernel<0><<<blocks, 256, 0, s>>>(src, iters, sink, clocks);
     else if (kind == 1) mfma_operand_rate_kernel<1><<<blocks, 256, 0, s>>>(src, iters, sink, clocks);
-    else mfma_operand_rate_kernel<2><<<blocks, 256, 0, s>>>(src, iters, sink, clocks);
+    else if (kind == 2) mfma_operand_rate_kernel<2><<<blocks, 256, 0, s>>>(src, iters, sink, clocks);
+    else if (kind == 3) mfma_operand_rate_kernel<3><<<blocks, 256, 0, s>>>(src, iters, sink, clocks);
+    else if (kind == 4) mfma_operand_rate_kernel<4><<<blocks, 256, 0, s>>>(src, iters, sink, clocks);
+    else if (kind == 5) mfma_operand_rate_kernel<5><<<blocks, 256, 0, s>>>(src, iters, sink, clocks);
+    else mfma_operand_rate_kernel<6><<<blocks, 256, 0, s>>>(src, iters, sink, clocks);
     return check_launch("probe_mfma_operands");
 }
 

@@ -38,7 +38,8 @@ def test_mfma_operand_probe_runs_and_rejects_bad_arguments(lib):
     """The matrix-core rate probe on operands from memory (bench.py's
     same-operands figures): every kind completes and writes one value per
     workgroup and two clock counts; the int8 kind's accumulators grow
-    linearly in the round count (integer MFMAs are exact); an unknown kind
+    linearly in the round count (integer MFMAs are exact) and the k-chain
+    kinds reach the same integer sums; an unknown kind
     and a null operand buffer are refused before any launch."""
     import torch
     from longhornai_amd import ops
@@ -47,7 +48,7 @@ def test_mfma_operand_probe_runs_and_rejects_bad_arguments(lib):
     src = torch.randint(0, 256, (32768,), dtype=torch.uint8, device="cuda", generator=gen)
     sink = torch.full((16,), -1, dtype=torch.int32, device="cuda")
     clocks = torch.zeros(32, dtype=torch.int64, device="cuda")
-    for kind in range(3):
+    for kind in range(7):
         lib.call("lhq_probe_mfma_operands", kind, src.data_ptr(), 16, 4, sink.data_ptr(), clocks.data_ptr(),
                  ops.stream())
         torch.cuda.synchronize()
@@ -60,5 +61,11 @@ def test_mfma_operand_probe_runs_and_rejects_bad_arguments(lib):
         sums.append(sink.cpu().tolist())
     assert len(set(sums[0])) == 1 and sums[0][0] != 0
     assert all((3 * a - b) % 2**32 == 0 for a, b in zip(sums[0], sums[1]))
-    assert lib.status("lhq_probe_mfma_operands", 3, src.data_ptr(), 16, 4, sink.data_ptr(), 0, ops.stream()) != 0
+    # the k-chain kinds issue the same products per round (kind 3) or twice
+    # them (kind 4): integer sums equal to kind 0's, or double
+    for kind, mult in ((3, 1), (4, 2)):
+        lib.call("lhq_probe_mfma_operands", kind, src.data_ptr(), 16, 3, sink.data_ptr(), 0, ops.stream())
+        torch.cuda.synchronize()
+        assert all((mult * b - c) % 2**32 == 0 for b, c in zip(sums[1], sink.cpu().tolist())), kind
+    assert lib.status("lhq_probe_mfma_operands", 7, src.data_ptr(), 16, 4, sink.data_ptr(), 0, ops.stream()) != 0
     assert lib.status("lhq_probe_mfma_operands", 0, 0, 16, 4, sink.data_ptr(), 0, ops.stream()) != 0
