@@ -558,8 +558,8 @@ def bench_w8a8(ops, M, K, N, steps, warmup, seed=0):
     return res
 
 
-PROBE_OPS_PER_MFMA = {0: 65536, 1: 131072, 2: 16384, 3: 65536, 4: 65536, 5: 32768, 6: 32768}
-PROBE_MFMAS_PER_ITER = {0: 32, 1: 32, 2: 32, 3: 32, 4: 64, 5: 64, 6: 32}
+PROBE_OPS_PER_MFMA = {0: 65536, 1: 131072, 2: 16384, 3: 65536, 4: 65536, 5: 32768, 6: 32768, 7: 32768}
+PROBE_MFMAS_PER_ITER = {0: 32, 1: 32, 2: 32, 3: 32, 4: 64, 5: 64, 6: 32, 7: 32}
 
 
 def operand_probe(ops, kind: int, A, B, iters: int = 4000, steps: int = 5, warmup: int = 2):
@@ -601,7 +601,7 @@ def operand_probe(ops, kind: int, A, B, iters: int = 4000, steps: int = 5, warmu
     c = clocks.view(cus, 2).double()
     ghz = float((c[:, 0] / c[:, 1]).mean()) * 0.1
     del buf, sink, clocks
-    return {"value": round(rate, 1), "unit": "TOPS" if kind in (0, 3, 4, 5, 6) else "TFLOPS", "ghz": round(ghz, 3),
+    return {"value": round(rate, 1), "unit": "TOPS" if kind in (0, 3, 4, 5, 6, 7) else "TFLOPS", "ghz": round(ghz, 3),
             "us_per_launch": round(ms * 1e3 / steps, 1)}
 
 
@@ -654,10 +654,11 @@ def mfma_ceiling(ops, steps: int = 5, warmup: int = 2):
                                    (3, "int8_32x32x32_k_chain2", INT8_PEAK_TOPS, {"random": rnd}),
                                    (4, "int8_32x32x32_k_chain4", INT8_PEAK_TOPS, {"random": rnd}),
                                    (5, "int8_16x16x64_k_chain4", INT8_PEAK_TOPS, {"random": rnd, "zero": zero}),
-                                   (6, "int8_16x16x64_tile_order", INT8_PEAK_TOPS, {"random": rnd})):
+                                   (6, "int8_16x16x64_tile_order", INT8_PEAK_TOPS, {"random": rnd}),
+                                   (7, "int8_16x16x64_k_chain2", INT8_PEAK_TOPS, {"random": rnd})):
         for dn, d in data.items():
             r = operand_probe(ops, kind, d[0], d[1],
-                              iters={0: 4000, 1: 2000, 2: 8000, 3: 4000, 4: 2000, 5: 4000, 6: 8000}[kind])
+                              iters={0: 4000, 1: 2000, 2: 8000, 3: 4000, 4: 2000, 5: 4000, 6: 8000, 7: 8000}[kind])
             r.update(peak=peak, frac=round(r["value"] / peak, 4))
             out[f"{name}_{dn}"] = r
     del rnd, nrm, zero

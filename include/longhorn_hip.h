@@ -327,7 +327,8 @@ int lhq_probe_mfma_rate(int kind, int blocks, int iters, int* sink, void* stream
  * 2: v_mfma_f32_16x16x32_bf16 (16,384 flops), 3 and 4: kind 0 issued as
  * k chains of 2 and 4 MFMAs on one accumulator (each round 32 and 64 MFMAs),
  * 5 and 6: v_mfma_i32_16x16x64_i8 (32,768 ops) on the same fragments, as k
- * chains of 4 (64 per round) and one per accumulator in turn (32 per round).
+ * chains of 4 (64 per round) and one per accumulator in turn (32 per round),
+ * 7: that instruction as k chains of 2 (32 per round).
  * operands: 32 KiB of device
  * memory; fragment x (0..7) of set s (0..1) for lane l is the 16 bytes at
  * ((8s + x) * 64 + l) * 16 (kind 1: the fragment's low half there, its high

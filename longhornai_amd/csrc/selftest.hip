@@ -156,7 +156,8 @@ __global__ __launch_bounds__(256) void mfma_rate_kernel(int iters, int* sink) {
 // instruction and operands issued as k chains of 2 and 4 on one accumulator
 // (32 and 64 MFMAs per iteration; KIND 0-2 issue 32), KINDs 5 and 6:
 // v_mfma_i32_16x16x64_i8 on the same fragments as k chains of 4 (64 MFMAs
-// per iteration) and one per accumulator in turn (32).  Fragment x of set s for
+// per iteration) and one per accumulator in turn (32), KIND 7: the same
+// as k chains of 2 (32).  Fragment x of set s for
 // lane l: the 16 bytes at ops + ((8s + x) * 64 + l) * 16.
 // clocks (optional): per workgroup, wave 0's shader-clock ticks
 // (s_memtime) and 100 MHz reference ticks (s_memrealtime) over its loop.
@@ -187,7 +188,17 @@ __global__ __launch_bounds__(256) void mfma_operand_rate_kernel(const uint8_t* _
         for (int j = 0; j < 4; ++j) acc4[i][j] = i32x4_t{};
     const unsigned long long t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
     for (int it = 0; it < iters; ++it) {
-        if constexpr (KIND == 5 || KIND == 6) {
+        if constexpr (KIND == 7) {
+            // v_mfma_i32_16x16x64_i8 as k chains of 2 (32 MFMAs per iteration)
+#pragma unroll
+            for (int t = 0; t < 16; ++t)
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    const int i = t / 4, j = t % 4;
+                    acc4[i][j] = mfma_i8_16x16x64(f[kk][4 + j], f[kk][i], acc4[i][j]);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+        } else if constexpr (KIND == 5 || KIND == 6) {
             // v_mfma_i32_16x16x64_i8 on the same fragments (16 bytes of a
             // 16x64 block per lane): KIND 5 as k chains of 4 on one
             // accumulator, KIND 6 one MFMA per accumulator in turn
@@ -279,7 +290,7 @@ extern "C" int lhq_probe_mfma_rate(int kind, int blocks, int iters, int* sink, v
 extern "C" int lhq_probe_mfma_operands(int kind, const void* operands, int blocks, int iters, int* sink,
                                        unsigned long long* clocks, void* stream) {
     LHQ_REQUIRE(operands && sink, "probe_mfma_operands: null operands or sink");
-    LHQ_REQUIRE(kind >= 0 && kind <= 6, "probe_mfma_operands: kind %d (0..6)", kind);
+    LHQ_REQUIRE(kind >= 0 && kind <= 7, "probe_mfma_operands: kind %d (0..7)", kind);
     LHQ_REQUIRE(blocks >= 1 && iters >= 1, "probe_mfma_operands: blocks %d, iters %d", blocks, iters);
     hipStream_t s = as_stream(stream);
     auto src = static_cast<const uint8_t*>(operands);
@@ -289,7 +300,8 @@ extern "C" int lhq_probe_mfma_operands(int kind, const void* operands, int block
     else if (kind == 3) mfma_operand_rate_kernel<3><<<blocks, 256, 0, s>>>(src, iters, sink, clocks);
     else if (kind == 4) mfma_operand_rate_kernel<4><<<blocks, 256, 0, s>>>(src, iters, sink, clocks);
     else if (kind == 5) mfma_operand_rate_kernel<5><<<blocks, 256, 0, s>>>(src, iters, sink, clocks);
-    else mfma_operand_rate_kernel<6><<<blocks, 256, 0, s>>>(src, iters, sink, clocks);
+    else if (kind == 6) mfma_operand_rate_kernel<6><<<blocks, 256, 0, s>>>(src, iters, sink, clocks);
+    else mfma_operand_rate_kernel<7><<<blocks, 256, 0, s>>>(src, iters, sink, clocks);
     return check_launch("probe_mfma_operands");
 }
 

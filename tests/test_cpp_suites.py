@@ -27,29 +27,6 @@ def test_cpp_dtypes_suite():
     assert "[  PASSED  ] 3 tests." in out
 
 
-REF_SUITES = os.path.join(ROOT, "oracle", "_ref", "ref_suites")
-
-
-@pytest.mark.gpu
-@pytest.mark.skipif(not os.path.exists(REF_SUITES),
-                    reason="oracle/_ref/ref_suites is built only where the reference tree is present")
-def test_reference_suites_on_dropin():
-    """The reference's own test_dtypes / test_gemm / test_quant /
-    test_gemm_quant suites (tests/CMakeLists.txt:18-52), compiled unchanged
-    where they lie against the lh:: drop-in headers and linked to the GPU
-    library: all 24 of their TESTs pass on the GPU backend."""
-    print("running oracle/_ref/ref_suites", flush=True)
-    r = subprocess.run([REF_SUITES], capture_output=True, text=True, timeout=110)
-    out = r.stdout + r.stderr
-    print(out[-4000:], flush=True)
-    assert r.returncode == 0, f"ref_suites failed:\n{out[-4000:]}"
-    assert "[  PASSED  ] 24 tests." in out
-    for name in ("Dtypes.Fp8E4m3RoundTrip", "Gemm.Grouped", "Quant.Q4GetMatchesDequantize",
-                 "GemmQuant.W8A8MatchesFp32WithinTolerance", "GemmQuant.W4A16MatchesFp32WithinTolerance",
-                 "GemmQuant.Fp8MatchesFp32WithinTolerance", "GemmQuant.W8A8RespectsBeta"):
-        assert f"[       OK ] {name}" in out, name
-
-
 @pytest.mark.gpu
 def test_cpp_kernel_suites():
     out = _run("lh_kernel_tests", 110)

@@ -48,7 +48,7 @@ def test_mfma_operand_probe_runs_and_rejects_bad_arguments(lib):
     src = torch.randint(0, 256, (32768,), dtype=torch.uint8, device="cuda", generator=gen)
     sink = torch.full((16,), -1, dtype=torch.int32, device="cuda")
     clocks = torch.zeros(32, dtype=torch.int64, device="cuda")
-    for kind in range(7):
+    for kind in range(8):
         lib.call("lhq_probe_mfma_operands", kind, src.data_ptr(), 16, 4, sink.data_ptr(), clocks.data_ptr(),
                  ops.stream())
         torch.cuda.synchronize()
@@ -67,5 +67,5 @@ def test_mfma_operand_probe_runs_and_rejects_bad_arguments(lib):
         lib.call("lhq_probe_mfma_operands", kind, src.data_ptr(), 16, 3, sink.data_ptr(), 0, ops.stream())
         torch.cuda.synchronize()
         assert all((mult * b - c) % 2**32 == 0 for b, c in zip(sums[1], sink.cpu().tolist())), kind
-    assert lib.status("lhq_probe_mfma_operands", 7, src.data_ptr(), 16, 4, sink.data_ptr(), 0, ops.stream()) != 0
+    assert lib.status("lhq_probe_mfma_operands", 8, src.data_ptr(), 16, 4, sink.data_ptr(), 0, ops.stream()) != 0
     assert lib.status("lhq_probe_mfma_operands", 0, 0, 16, 4, sink.data_ptr(), 0, ops.stream()) != 0
