@@ -7,7 +7,10 @@
 // fp32 and adds ((alpha*sA)*sB)*acc.
 //
 // Here a 256-thread workgroup owns a 256x256 output tile; the four waves
-// (2x2) each own 128x128 = 4x4 blocks of 32x32 MFMA accumulators.  A (row
+// (2x2) each own 128x128 of it: 8x8 blocks of 16x16 int8 MFMA accumulators
+// in the W8A8 kernel (dma_tile_m16), 4x4 blocks of 32x32 in the FP8 and
+// register-staged kernels (and the 32x32x32 int8 tile dma_tile, kept for
+// comparison in tuning builds).  A (row
 // major [M,K]) and the prepacked k-contiguous B^T ([Np,Kp], lhq_b8_prepack)
 // are staged through double-buffered LDS tiles of 256 x 128 bytes with a
 // 16-byte row pad (conflict-free 128-bit LDS reads).  Integer accumulation is
@@ -223,8 +226,11 @@ constexpr int STAGED_PITCH = 4 * (128 + 4);
 // C = beta-applied C + combined * acc; with beta = 0, 0 + x is kept as an
 // add: an fp32 accumulator can be small enough for the product to underflow,
 // where fma(s, acc, +0) could return -0).
-template <int EPI, bool EDGE, int JB = 4, bool FP8 = false, typename Acc = i32x16_t>
-__device__ __forceinline__ void gemm8_store_staged(const Gemm8Args& p, const Acc (&acc)[4][4], int m0, int n0,
+// AI = 8: acc holds 8 x 2JB blocks of 16x16 (the 16x16x64 tile): block
+// (i, j) in lane l is row 16i + (l & 15), columns 16j + 4(l >> 4) ..+3 of
+// the quadrant, one 16-byte row piece per block.
+template <int EPI, bool EDGE, int JB = 4, bool FP8 = false, typename Acc = i32x16_t, int AI = 4, int AJ = 4>
+__device__ __forceinline__ void gemm8_store_staged(const Gemm8Args& p, const Acc (&acc)[AI][AJ], int m0, int n0,
                                                    int wm, int wn, int lane, const float* ls, uint8_t* area) {
     constexpr int WQ = 32 * JB;                   // quadrant width
     constexpr int CPL = EPI == EPI_BF16 ? 8 : 4;  // columns per lane (16 output bytes)
@@ -253,13 +259,25 @@ __device__ __forceinline__ void gemm8_store_staged(const Gemm8Args& p, const Acc
     const bool vec_ok = !EDGE || (p.c_vec && cols_left >= CPL && p.N % CPL == 0);
     // 1. raw accumulators of block i, row lr, columns 32j + 4lh + 8q ..+3
     auto stage_block = [&](int i) {
+        if constexpr (AI == 8) {
+            // rows 32i .. 32i+31 are 16x16 block rows 2i and 2i + 1
 #pragma unroll
-        for (int j = 0; j < JB; ++j)
+            for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-                *reinterpret_cast<i32x4_t*>(area + lr * STAGED_PITCH + (j * 32 + 4 * lh + 8 * q) * 4) =
-                    __builtin_bit_cast(i32x4_t, decltype(acc[i][j].xyzw){acc[i][j][4 * q], acc[i][j][4 * q + 1],
-                                                                          acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]});
+                for (int j = 0; j < 2 * JB; ++j)
+                    *reinterpret_cast<i32x4_t*>(area + (16 * h + (lane & 15)) * STAGED_PITCH +
+                                                (16 * j + 4 * (lane >> 4)) * 4) =
+                        __builtin_bit_cast(i32x4_t, acc[2 * i + h][j]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < JB; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    *reinterpret_cast<i32x4_t*>(area + lr * STAGED_PITCH + (j * 32 + 4 * lh + 8 * q) * 4) =
+                        __builtin_bit_cast(i32x4_t,
+                                           decltype(acc[i][j].xyzw){acc[i][j][4 * q], acc[i][j][4 * q + 1],
+                                                                    acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]});
+        }
     };
     auto wave_sync = [&]() {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -707,6 +725,146 @@ __device__ __forceinline__ void dma_tile(const Gemm8Args& p, uint8_t* ds_lds, in
         gemm8_store_staged<EPI, true, JB>(p, acc, m0, n0, wm, wn, lane, lds_scales, area);
 }
 
+// The same tile on v_mfma_i32_16x16x64_i8.  Each wave's 128 x 64*JB
+// quadrant is 8 x 2JB blocks of 16x16 (4 accumulator registers each, the
+// same 256 in all); a 64-byte k stage is ONE MFMA per block.  DMA pipeline,
+// LDS layout and swizzle are dma_tile's.  Fragment of 16-row block x: row
+// (lane & 15), global k chunk (lane >> 4), i.e. LDS slot (lane >> 4) ^
+// ((row >> 2) & 3).  B is the MFMA's first operand, so lane l of block
+// (i, j) holds C row 16i + (l & 15), columns 16j + 4(l >> 4) ..+3.
+// Stage s (its fragments fa / fb in registers on entry):
+//   rendezvous: stage s+1 landed (this wave's DMAs; s+2, s+3 may still be
+//     in flight), this wave's reads of stage s's buffer done, every wave
+//     here (the buffer is free for stage s + STAGES);
+//   block rows 0..3, all columns, one MFMA per block; the DMAs of stage
+//     s + STAGES one per MFMA; after row i the next stage's A fragment of
+//     row i (read in place);
+//   block rows 4..7 column by column; after column j the next stage's B
+//     fragment of column j, after the last column the A fragments of rows
+//     4..7.
+// Register-only, on random int8 operands, this instruction in turn over
+// the accumulators sustains ~12% more than the 32x32x32 form (a higher
+// clock under the power limit).
+template <int EPI, int JB>
+__device__ __forceinline__ void dma_tile_m16(const Gemm8Args& p, uint8_t* ds_lds, int m0, int n0,
+                                             i32x4_t (&acc)[8][8]) {
+    constexpr int STAGES = 4;
+    constexpr int DPS = 4 + JB;  // DMAs per wave per stage: 4 of A, JB of B
+    constexpr int NB = 2 * JB;   // 16-column blocks per wave
+    static_assert(DPS * (STAGES - 2) <= 63, "vmcnt range");
+    static_assert(STAGES * 2 * DS_OP_BYTES + DS_SCALE_BYTES <= 160 * 1024, "LDS");
+    static_assert(4 * 32 * STAGED_PITCH <= STAGES * 2 * DS_OP_BYTES, "epilogue staging fits the stages");
+    auto stage_buf = [&](int u) { return ds_lds + u * 2 * DS_OP_BYTES; };
+    float* const lds_scales = reinterpret_cast<float*>(ds_lds + STAGES * 2 * DS_OP_BYTES);
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+
+    uint32_t a_row[4], b_src[JB];
+    int kca[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int c = (4 * wave + i) * 64 + lane;
+        const int r = c >> 2;
+        kca[i] = ((c & 3) ^ ((r >> 2) & 3)) * 16;
+        a_row[i] = static_cast<uint32_t>(min(m0 + r, p.M - 1)) * static_cast<uint32_t>(p.K);
+    }
+#pragma unroll
+    for (int i = 0; i < JB; ++i) {
+        const int c = (JB * wave + i) * 64 + lane;
+        const int r = c >> 2;
+        b_src[i] = static_cast<uint32_t>(n0 + r) * static_cast<uint32_t>(p.Kp) +
+                   static_cast<uint32_t>(((c & 3) ^ ((r >> 2) & 3)) * 16);
+    }
+    const int nk = p.Kp / DS_BK;
+    // stages past the last reload the last one (no branch in the MFMA
+    // stream); they land in buffers no later stage reads
+    auto dma = [&](uint8_t* buf, int s, int d) {
+        const int k0 = min(s, nk - 1) * DS_BK;
+        const bool is_b = d < 2 * JB && (d & 1);
+        const int i = d < 2 * JB ? d >> 1 : d - JB;
+        if (!is_b) {
+            const uint32_t ka = static_cast<uint32_t>(min(k0 + kca[i], p.K - 16));
+            __builtin_amdgcn_global_load_lds(p.A + (a_row[i] + ka), (LHQ_LDS_AS void*)(buf + (4 * wave + i) * 1024),
+                                             16, 0, 0);
+        } else {
+            __builtin_amdgcn_global_load_lds(p.Bt + (b_src[i] + static_cast<uint32_t>(k0)),
+                                             (LHQ_LDS_AS void*)(buf + DS_OP_BYTES + (JB * wave + i) * 1024), 16, 0, 0);
+        }
+    };
+
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) acc[i][j] = i32x4_t{};
+
+    const int r16 = lane & 15;
+    const int off = ((lane >> 4) ^ ((r16 >> 2) & 3)) * 16;
+    const int a_base = (wm * 128 + r16) * DS_BK + off;
+    const int b_base = DS_OP_BYTES + (wn * 32 * JB + r16) * DS_BK + off;
+    auto rd_a = [&](const uint8_t* buf, int x) {
+        return *reinterpret_cast<const u32x4_t*>(buf + a_base + x * 16 * DS_BK);
+    };
+    auto rd_b = [&](const uint8_t* buf, int x) {
+        return *reinterpret_cast<const u32x4_t*>(buf + b_base + x * 16 * DS_BK);
+    };
+    u32x4_t fa[8], fb[NB];
+    auto mma = [&](int i, int j) { acc[i][j] = mfma_i8_16x16x64(fb[j], fa[i], acc[i][j]); };
+
+    if constexpr (EPI != EPI_I32) {
+        const int r = min(m0 + 64 * wave + lane, p.M - 1), c = min(n0 + 64 * wave + lane, p.N - 1);
+        __builtin_amdgcn_global_load_lds(p.As + r, (LHQ_LDS_AS void*)(lds_scales + 64 * wave), 4, 0, 0);
+        __builtin_amdgcn_global_load_lds(p.Bs + c, (LHQ_LDS_AS void*)(lds_scales + BM + 64 * wave), 4, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < STAGES; ++u)
+#pragma unroll
+        for (int d = 0; d < DPS; ++d) dma(stage_buf(u), u, d);
+    // stage 0 (and the scales) landed everywhere
+    asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(DPS * (STAGES - 1)) : "memory");
+#pragma unroll
+    for (int x = 0; x < 8; ++x) fa[x] = rd_a(stage_buf(0), x);
+#pragma unroll
+    for (int x = 0; x < NB; ++x) fb[x] = rd_b(stage_buf(0), x);
+    auto step = [&](uint8_t* cur, const uint8_t* nxt, int s) {
+        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(DPS * (STAGES - 2)) : "memory");
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                mma(i, j);
+                const int d = i * NB + j;
+                if (d < DPS) dma(cur, s + STAGES, d);
+                if (j == NB - 1) fa[i] = rd_a(nxt, i);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int i = 4; i < 8; ++i) {
+                mma(i, j);
+                if (i == 7) fb[j] = rd_b(nxt, j);
+                if (j == NB - 1) fa[i] = rd_a(nxt, i);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+    };
+    for (int s = 0; s < nk; s += STAGES) {
+#pragma unroll
+        for (int u = 0; u < STAGES; ++u)
+            if (u == 0 || s + u < nk) step(stage_buf(u), stage_buf((u + 1) % STAGES), s + u);
+    }
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    // every wave's DMAs have landed and every wave is done with the stage
+    // buffers: the epilogue may reuse them
+    __syncthreads();
+    uint8_t* const area = ds_lds + wave * 32 * STAGED_PITCH;
+    if (m0 + BM <= p.M && n0 + 64 * JB <= p.N && p.N % 8 == 0 && p.c_vec)
+        gemm8_store_staged<EPI, false, JB, false, i32x4_t, 8, 8>(p, acc, m0, n0, wm, wn, lane, lds_scales, area);
+    else
+        gemm8_store_staged<EPI, true, JB, false, i32x4_t, 8, 8>(p, acc, m0, n0, wm, wn, lane, lds_scales, area);
+}
+
 // The kernel.  A plain launch has one workgroup per tile (gridDim.x ==
 // tiles), in tile_of's order.  A persistent launch has G = gridDim.x < tiles
 // workgroups, one per CU: R = tiles / G rounds of full tiles, then the
@@ -716,7 +874,7 @@ __device__ __forceinline__ void dma_tile(const Gemm8Args& p, uint8_t* ds_lds, in
 // of 4 rounds with the last one half empty.  Persistent full tiles keep
 // tile_of's locality: XCD x (workgroups x, x+8, ...) walks the contiguous id
 // range x*R*G/8 .. (x+1)*R*G/8, G/8 tiles per round.
-template <int EPI, int STAGES>
+template <int EPI, int STAGES, bool M16>
 __global__ __launch_bounds__(NTHREADS) void gemm8_dma_kernel(Gemm8Args p) {
     // Dynamic LDS: the compiler does not see the DMA as a store into it, so
     // it may neither assume its contents nor insert its own waits for it;
@@ -726,13 +884,16 @@ __global__ __launch_bounds__(NTHREADS) void gemm8_dma_kernel(Gemm8Args p) {
     const int total = p.tiles_m * p.tiles_n;
     const int R = total / G, rem = total - R * G;
     const int per_xcd = G / 8, xcd = b % 8, slot = b / 8;
-    i32x16_t acc[4][4];
+    // (each call site names its tile width: a shared helper taking the width
+    // at run time is not inlined, and the accumulators then live in scratch)
+    typename std::conditional<M16, i32x4_t[8][8], i32x16_t[4][4]>::type acc;
     if constexpr (EPI != EPI_BF16) {
         // fp32 / int32 outputs keep one tile per workgroup: their epilogues
         // need more registers than a persistent loop leaves without spills
         int tm, tn;
         tile_of(b, p, tm, tn);
-        dma_tile<EPI, STAGES, 4>(p, ds_lds, tm * BM, tn * BN, acc);
+        if constexpr (M16) dma_tile_m16<EPI, 4>(p, ds_lds, tm * BM, tn * BN, acc);
+        else dma_tile<EPI, STAGES, 4>(p, ds_lds, tm * BM, tn * BN, acc);
         return;
     }
     for (int r = 0; r < R; ++r) {
@@ -742,13 +903,15 @@ __global__ __launch_bounds__(NTHREADS) void gemm8_dma_kernel(Gemm8Args p) {
         else
             tile_of_id(xcd * R * per_xcd + r * per_xcd + slot, p, tm, tn);
         if (r > 0) __syncthreads();  // the previous epilogue's LDS reads are done
-        dma_tile<EPI, STAGES, 4>(p, ds_lds, tm * BM, tn * BN, acc);
+        if constexpr (M16) dma_tile_m16<EPI, 4>(p, ds_lds, tm * BM, tn * BN, acc);
+        else dma_tile<EPI, STAGES, 4>(p, ds_lds, tm * BM, tn * BN, acc);
     }
     if (b < 2 * rem) {
         int tm, tn;
         tile_of_id(R * G + (b >> 1), p, tm, tn);
         __syncthreads();
-        dma_tile<EPI, STAGES, 2>(p, ds_lds, tm * BM, tn * BN + (b & 1) * (BN / 2), acc);
+        if constexpr (M16) dma_tile_m16<EPI, 2>(p, ds_lds, tm * BM, tn * BN + (b & 1) * (BN / 2), acc);
+        else dma_tile<EPI, STAGES, 2>(p, ds_lds, tm * BM, tn * BN + (b & 1) * (BN / 2), acc);
     }
 }
 
@@ -960,11 +1123,12 @@ int device_cus() {
     return cus;
 }
 
-template <int EPI, int STAGES>
+template <int EPI, int STAGES, bool M16>
 int launch_dma(const Gemm8Args& p, int tiles, void* stream, const char* who) {
+    static_assert(!M16 || STAGES == 4, "the 16x16x64 tile runs four stages");
     constexpr size_t lds = static_cast<size_t>(STAGES) * 2 * DS_OP_BYTES + DS_SCALE_BYTES;
     static const hipError_t attr =
-        hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm8_dma_kernel<EPI, STAGES>),
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm8_dma_kernel<EPI, STAGES, M16>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     if (attr != hipSuccess)
         return set_error(LHQ_ERR_HIP, "%s: dynamic LDS attribute: %s", who, hipGetErrorString(attr));
@@ -977,10 +1141,10 @@ int launch_dma(const Gemm8Args& p, int tiles, void* stream, const char* who) {
     const int G = cus;
     const int rem = G > 0 ? tiles % G : 0;
     if (EPI == EPI_BF16 && persist && G > 0 && G % 8 == 0 && tiles > G && rem != 0 && 2 * rem <= G) {
-        gemm8_dma_kernel<EPI, STAGES><<<G, NTHREADS, lds, as_stream(stream)>>>(p);
+        gemm8_dma_kernel<EPI, STAGES, M16><<<G, NTHREADS, lds, as_stream(stream)>>>(p);
         return check_launch(who);
     }
-    gemm8_dma_kernel<EPI, STAGES><<<tiles, NTHREADS, lds, as_stream(stream)>>>(p);
+    gemm8_dma_kernel<EPI, STAGES, M16><<<tiles, NTHREADS, lds, as_stream(stream)>>>(p);
     return check_launch(who);
 }
 
@@ -1033,10 +1197,13 @@ int launch_gemm8(const uint8_t* A, const uint8_t* Bt, const float* As, const flo
             return check_launch(who);
         }
         if (use_dma) {
+            // the 16x16x64 tile (LHQ_GEMM8_M16=0: the 32x32x32 one)
+            static const int m16 = env_int("LHQ_GEMM8_M16", 1);
             static const int stages = env_int("LHQ_GEMM8_STAGES", DS_STAGES);
+            if (m16) return launch_dma<EPI, 4, true>(p, tiles, stream, who);
             switch (stages) {
-                case 3: return launch_dma<EPI, 3>(p, tiles, stream, who);
-                default: return launch_dma<EPI, 4>(p, tiles, stream, who);
+                case 3: return launch_dma<EPI, 3, false>(p, tiles, stream, who);
+                default: return launch_dma<EPI, 4, false>(p, tiles, stream, who);
             }
         }
     }
