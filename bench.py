@@ -510,10 +510,12 @@ def bench_w8a8(ops, M, K, N, steps, warmup, seed=0):
     us = ms * 1e3 / steps
     p50, p90 = timer.chunk_percentiles(steps)
     ops_per = 2 * M * K * N
-    # the register-only MFMA rate on these same quantized values, and the same
-    # GEMM on all-zero operands (the clock under the power limit depends on
-    # the values the matrix cores multiply)
-    same = operand_probe(ops, 0, Aq, Bt)
+    # the register-only MFMA rate on these same quantized values, with the
+    # tile's instruction and order (v_mfma_i32_16x16x64_i8, one MFMA per
+    # accumulator in turn: probe kind 6), and the same GEMM on all-zero
+    # operands (the clock under the power limit depends on the values the
+    # matrix cores multiply)
+    same = operand_probe(ops, 6, Aq, Bt, iters=8000)
     Az = torch.zeros_like(Aq)
     Bz = torch.zeros_like(Bt)
 
@@ -958,8 +960,10 @@ def main() -> int:
             f"({100 * ceiling['bf16_16x16x32']['frac']:.1f}%)")
         cr = ceiling["int8_32x32x32_tile_order_random"]
         cz = ceiling["int8_32x32x32_tile_order_zero"]
-        log(f"  int8 in the tile's order on operands from memory: random bytes {cr['value']:.0f} TOPS at "
-            f"{cr['ghz']:.2f} GHz, zero bytes {cz['value']:.0f} TOPS at {cz['ghz']:.2f} GHz")
+        c6 = ceiling["int8_16x16x64_tile_order_random"]
+        log(f"  int8 on operands from memory, in turn over accumulators: 32x32x32 random bytes {cr['value']:.0f} TOPS "
+            f"at {cr['ghz']:.2f} GHz, zero bytes {cz['value']:.0f} TOPS at {cz['ghz']:.2f} GHz; 16x16x64 (the W8A8 "
+            f"tile's form) random bytes {c6['value']:.0f} TOPS at {c6['ghz']:.2f} GHz")
 
     fp8 = []
     if not args.no_w8a8:
