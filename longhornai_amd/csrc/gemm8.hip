@@ -747,12 +747,17 @@ __device__ __forceinline__ void dma_tile(const Gemm8Args& p, uint8_t* ds_lds, in
 //   rendezvous: stage s+1 landed (this wave's DMAs; s+2, s+3 may still be
 //     in flight), this wave's reads of stage s's buffer done, every wave
 //     here (the buffer is free for stage s + STAGES);
-//   block rows 0..3, all columns, one MFMA per block; the DMAs of stage
-//     s + STAGES one per MFMA; after row i the next stage's A fragment of
-//     row i (read in place);
+//   block rows 0..3, all columns, one MFMA per block; after row i the
+//     next stage's A fragment of row i (read in place);
 //   block rows 4..7 column by column; after column j the next stage's B
 //     fragment of column j, after the last column the A fragments of rows
-//     4..7.
+//     4..7;
+//   the DMAs of stage s + STAGES spread over the whole stage, one every
+//     8*NB / DPS MFMAs.  Issued back to back after the stage's first eight
+//     MFMAs they measured slower (M=4096: 212.5 against 206.7 us, zero
+//     operands 177 against 166 us; M=2048: 114 against 108.7 us): a wave
+//     issues in order, so a memory instruction that cannot issue holds
+//     back the MFMAs behind it.
 // Register-only, on random int8 operands, this instruction in turn over
 // the accumulators sustains ~12% more than the 32x32x32 form (a higher
 // clock under the power limit).
@@ -840,13 +845,16 @@ __device__ __forceinline__ void dma_tile_m16(const Gemm8Args& p, uint8_t* ds_lds
     for (int x = 0; x < NB; ++x) fb[x] = rd_b(stage_buf(0), x);
     auto step = [&](uint8_t* cur, const uint8_t* nxt, int s) {
         asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(DPS * (STAGES - 2)) : "memory");
+        // MFMA t of the stage (issue order) is followed by DMA t / SP when
+        // t % SP == SP / 2: one DMA every SP MFMAs over the whole stage
+        constexpr int SP = 8 * NB / DPS;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int j = 0; j < NB; ++j) {
                 mma(i, j);
-                const int d = i * NB + j;
-                if (d < DPS) dma(cur, s + STAGES, d);
+                const int t = i * NB + j;
+                if (t % SP == SP / 2 && t / SP < DPS) dma(cur, s + STAGES, t / SP);
                 if (j == NB - 1) fa[i] = rd_a(nxt, i);
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -855,6 +863,8 @@ __device__ __forceinline__ void dma_tile_m16(const Gemm8Args& p, uint8_t* ds_lds
 #pragma unroll
             for (int i = 4; i < 8; ++i) {
                 mma(i, j);
+                const int t = 4 * NB + 4 * j + (i - 4);
+                if (t % SP == SP / 2 && t / SP < DPS) dma(cur, s + STAGES, t / SP);
                 if (i == 7) fb[j] = rd_b(nxt, j);
                 if (j == NB - 1) fa[i] = rd_a(nxt, i);
                 __builtin_amdgcn_sched_barrier(0);
