@@ -70,15 +70,22 @@ def log(*a):
 # ---------------------------------------------------------------------------
 
 class GraphTimer:
-    """Times exactly `steps` launches of `launch(i)` captured in HIP graphs."""
+    """Times exactly `steps` launches of `launch(i)`, captured in HIP graphs
+    of `chunk` launches (direct=False) or launched straight onto the stream
+    (direct=True: for launches long enough that the host, enqueueing while a
+    spin kernel runs, stays ahead of the GPU; a graph replay adds a startup
+    cost of several microseconds on the GPU, which a short run amortizes
+    over few launches)."""
 
-    def __init__(self, launch, period: int, chunk: int):
+    def __init__(self, launch, period: int, chunk: int, direct: bool = False):
         import torch
         self.torch = torch
         self.launch = launch
         self.period = period
         self.chunk = max(1, chunk)
+        self.direct = direct
         self._graphs = {}
+        self.host_enqueue_ms = None
 
     def _graph(self, n: int, start: int):
         key = (n, start % self.period)
@@ -98,6 +105,10 @@ class GraphTimer:
         return g
 
     def run(self, steps: int) -> None:
+        if self.direct:
+            for i in range(steps):
+                self.launch(i)
+            return
         done = 0
         while done < steps:
             n = min(self.chunk, steps - done)
@@ -105,6 +116,8 @@ class GraphTimer:
             done += n
 
     def prepare(self, steps: int) -> None:
+        if self.direct:
+            return
         done = 0
         while done < steps:
             n = min(self.chunk, steps - done)
@@ -112,43 +125,58 @@ class GraphTimer:
             done += n
 
     def time(self, steps: int, warmup: int):
-        """Returns (elapsed ms of the timed region by HIP events, wall ms)."""
+        """Returns (elapsed ms of the timed region by HIP events, wall ms).
+        Order on the stream: a spin kernel (~1 ms; the host enqueues the
+        rest while it runs), the `warmup` untimed launches, the opening
+        event, exactly `steps` launches, the closing event.  The warm-up
+        launches run immediately before the timed ones, so the timed region
+        starts with clocks, caches and TLBs as the steady state has them,
+        and the events bracket the GPU's execution of the steps, not the
+        host's launch latency."""
         torch = self.torch
         self.prepare(steps)
         if warmup:
             self.prepare(warmup)
-            self.run(warmup)
         torch.cuda.synchronize()
         ev0 = torch.cuda.Event(enable_timing=True)
         ev1 = torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
-        # A spin kernel (~0.5 ms) ahead of the opening event: the host
-        # submits the graphs while it runs, so the events bracket the GPU's
-        # execution of the steps and not the host's launch latency.
-        torch.cuda._sleep(1_000_000)
+        torch.cuda._sleep(2_000_000)
+        if warmup:
+            self.run(warmup)
         ev0.record()
+        h0 = time.perf_counter()
         self.run(steps)
+        self.host_enqueue_ms = (time.perf_counter() - h0) * 1e3
         ev1.record()
         torch.cuda.synchronize()
         wall = (time.perf_counter() - t0) * 1e3
         return ev0.elapsed_time(ev1), wall
 
-    def chunk_percentiles(self, steps: int):
-        """A second pass over `steps` launches with a HIP event after every
-        graph replay (a chunk of back-to-back launches): returns the 50th and
-        90th percentiles over the chunks of the time per launch, in us.  Run
-        apart from time() so its events do not enter the reported total."""
+    def chunk_percentiles(self, steps: int, min_chunks: int = 10):
+        """A second pass with a HIP event after every graph replay (a chunk
+        of back-to-back launches), over max(steps, min_chunks * chunk)
+        launches so that the percentiles rest on at least `min_chunks`
+        chunks whatever `steps` is: returns the 50th and 90th percentiles
+        over the chunks of the time per launch, in us.  Run apart from
+        time() so its events do not enter the reported total."""
         torch = self.torch
+        steps = max(steps, min_chunks * self.chunk)
         self.prepare(steps)
         torch.cuda.synchronize()
-        torch.cuda._sleep(1_000_000)
+        torch.cuda._sleep(2_000_000)
+        self.run(self.chunk)  # one untimed chunk: the first timed one does not start cold
         evs = [torch.cuda.Event(enable_timing=True)]
         evs[0].record()
         sizes = []
         done = 0
         while done < steps:
             n = min(self.chunk, steps - done)
-            self._graph(n, done).replay()
+            if self.direct:
+                for i in range(done, done + n):
+                    self.launch(i)
+            else:
+                self._graph(n, done).replay()
             e = torch.cuda.Event(enable_timing=True)
             e.record()
             evs.append(e)
@@ -226,10 +254,11 @@ def bench_w4a16_f32(ops, M, K, N, G, steps, warmup, seed=0, min_rotate_bytes=2 *
 
 
 def bench_w4a16(ops, M, K, N, G, steps, warmup, seed=0, min_rotate_bytes=2 * INFINITY_CACHE_BYTES + (1 << 26),
-                workspace=False):
+                workspace=False, direct=False):
     """W4A16 bf16 timed over rotating weight sets.  workspace: through
     lhq_gemm_w4a16_bf16_ws with the workspace the shape asks for (K split
-    across workgroups where the grid is thin), else lhq_gemm_w4a16_bf16."""
+    across workgroups where the grid is thin), else lhq_gemm_w4a16_bf16.
+    direct: launches straight onto the stream instead of graph replays."""
     import numpy as np
     import torch
     per = w4a16_bytes(M, K, N, G)
@@ -254,14 +283,16 @@ def bench_w4a16(ops, M, K, N, G, steps, warmup, seed=0, min_rotate_bytes=2 * INF
         if st:
             raise RuntimeError(f"{name}: {ops.lib().last_error()}")
 
-    timer = GraphTimer(launch, nsets, chunk=nsets * max(1, 64 // nsets))
+    timer = GraphTimer(launch, nsets, chunk=nsets * max(1, 64 // nsets), direct=direct)
     ms, wall = timer.time(steps, warmup)
     us = ms * 1e3 / steps
+    host_ms = timer.host_enqueue_ms
     p50, p90 = timer.chunk_percentiles(steps)
     res = {"M": M, "K": K, "N": N, "G": G, "entry": name, "workspace_bytes": ws_bytes,
            "bytes_per_call": per, "weight_sets": nsets,
            "rotate_bytes": per * nsets, "us_per_call": us, "gbs": per / (us * 1e-6) / 1e9,
            "elapsed_ms": ms, "wall_ms": wall, "chunk_launches": timer.chunk,
+           "launch": "direct" if direct else "graph", "host_enqueue_ms": host_ms,
            "us_p50_chunk": p50, "us_p90_chunk": p90}
     res["hbm_frac"] = res["gbs"] / HBM_PEAK_GBS
     del timer, sets, A, C, ws
@@ -555,6 +586,78 @@ def bench_w8a8(ops, M, K, N, steps, warmup, seed=0):
     res["us_zero_operands"] = zus
     res["tops_zero_operands"] = ops_per / (zus * 1e-6) / 1e12
     del Bt, Xb, Aq, As, C
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_w8_gemv(ops, steps, warmup, seed=0, K=4096, N=4096, min_rotate_bytes=2 * INFINITY_CACHE_BYTES + (1 << 26)):
+    """Config 1: the W8 per-output-channel int8 GEMV through the reference's
+    gemm_quant path (gemm_quant.cpp:29-49 at M=1).  One step is the
+    reference's sequence: q8_quantize_per_row of the fp32 activation row
+    (quant.cpp:52-63), then gemm_w8a8 with fp32 output, alpha = 1, beta = 0.
+    Weights: fp32 N(0,0.02) [K,N] quantized per column on the device
+    (quant.cpp:75-96) and prepacked once, rotated over sets beyond the
+    Infinity Cache.  Also timed: the GEMV alone (the roofline figure, HBM:
+    K*N int8 codes + 4N scales + K int8 + 4 row scale + 4N fp32 out)."""
+    import numpy as np
+    import torch
+    M = 1
+    gemv_bytes = K * N + 4 * N + M * K + 4 * M + 4 * M * N
+    quant_bytes = 4 * M * K + M * K + 4 * M
+    nsets = max(2, -(-min_rotate_bytes // (K * N)))
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    sets = []
+    for _ in range(nsets):
+        W = torch.randn((K, N), generator=gen, device="cuda") * 0.02
+        Bq = ops.empty((K, N), np.int8)
+        Bs = ops.empty((N,), np.float32)
+        ops.lib().call("lhq_q8_quantize_per_col", W.data_ptr(), Bq.data_ptr(), Bs.data_ptr(), K, N, ops.stream())
+        del W
+        sets.append((ops.prepack_b8(Bq, K, N), Bs))
+        del Bq
+    A = [torch.randn((M, K), generator=gen, device="cuda") for _ in range(nsets)]
+    Aq = [ops.empty((M, K), np.int8) for _ in range(nsets)]
+    As = [ops.empty((M,), np.float32) for _ in range(nsets)]
+    C = [torch.zeros((M, N), device="cuda") for _ in range(nsets)]
+    qfn = ops.lib().cdll.lhq_q8_quantize_per_row
+    gfn = ops.lib().cdll.lhq_gemm_w8a8
+
+    def gemv(j):
+        st = gfn(Aq[j].data_ptr(), sets[j][0].data_ptr(), As[j].data_ptr(), sets[j][1].data_ptr(), C[j].data_ptr(),
+                 M, N, K, 1.0, 0.0, ops.stream())
+        if st:
+            raise RuntimeError(f"lhq_gemm_w8a8: {ops.lib().last_error()}")
+
+    def quant(j):
+        st = qfn(A[j].data_ptr(), Aq[j].data_ptr(), As[j].data_ptr(), M, K, ops.stream())
+        if st:
+            raise RuntimeError(f"lhq_q8_quantize_per_row: {ops.lib().last_error()}")
+
+    def step(i):
+        quant(i % nsets)
+        gemv(i % nsets)
+
+    chunk = nsets * max(1, 64 // nsets)
+    for j in range(nsets):
+        quant(j)
+    t_step = GraphTimer(step, nsets, chunk=chunk)
+    ms_step, _ = t_step.time(steps, warmup)
+    t_gemv = GraphTimer(lambda i: gemv(i % nsets), nsets, chunk=chunk)
+    ms_gemv, _ = t_gemv.time(steps, warmup)
+    p50, p90 = t_gemv.chunk_percentiles(steps)
+    us_step = ms_step * 1e3 / steps
+    us_gemv = ms_gemv * 1e3 / steps
+    res = {"leg": "w8_gemv_config1", "M": M, "K": K, "N": N, "kernel": "gemm8_skinny_kernel",
+           "weights": "int8 per output channel (column) scales, prepacked once", "weight_sets": nsets,
+           "rotate_bytes": nsets * K * N, "gemv_bytes": gemv_bytes,
+           "us_per_step_quant_plus_gemv": round(us_step, 3), "us_per_gemv": round(us_gemv, 3),
+           "us_per_gemv_p50_p90": [round(p50, 3), round(p90, 3)],
+           "gemv_gbs": round(gemv_bytes / (us_gemv * 1e-6) / 1e9, 1),
+           "step_gbs": round((gemv_bytes + quant_bytes) / (us_step * 1e-6) / 1e9, 1)}
+    res["hbm_frac"] = round(res["gemv_gbs"] / HBM_PEAK_GBS, 4)
+    del t_step, t_gemv, sets, A, Aq, As, C
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     return res
@@ -859,7 +962,8 @@ def main() -> int:
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a 1 GiB device copy (PMC calibration kernel)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the W4A16 prefill and MoE legs")
-    ap.add_argument("--only", choices=["w4a16", "w8a8", "prefill", "moe", "fp8", "configs", "mfma", "f32"], default=None,
+    ap.add_argument("--only", choices=["w4a16", "w8a8", "prefill", "moe", "fp8", "configs", "mfma", "f32", "w8gemv"],
+                    default=None,
                     help="run one leg only (profiling); prints that leg's summary, not the bench line")
     ap.add_argument("--moe-tokens", type=int, default=512,
                     help="tokens of the --only moe leg (512 = config 4; 1-4 run the grouped decode kernel)")
@@ -892,6 +996,12 @@ def main() -> int:
                 f"{r['sustained_same_operands']['value']:.0f} TOPS the MFMAs sustain on these values at "
                 f"{r['sustained_same_operands']['ghz']:.2f} GHz); zero operands {r['us_zero_operands']:.1f} us")
             print(json.dumps({"leg": "w8a8_prefill", **r}), flush=True)
+        return 0
+    if args.only == "w8gemv":
+        r = bench_w8_gemv(ops, 500, 50)
+        log(f"w8 gemv config 1 M=1 K=4096 N=4096: gemv {r['us_per_gemv']:.2f} us ({r['gemv_gbs']:.0f} GB/s, "
+            f"{100 * r['hbm_frac']:.1f}% of HBM peak); quant + gemv {r['us_per_step_quant_plus_gemv']:.2f} us")
+        print(json.dumps(r), flush=True)
         return 0
     if args.only == "fp8":
         for m in (4096, 2048):
@@ -927,7 +1037,7 @@ def main() -> int:
             print(json.dumps(r), flush=True)
         return 0
     log(f"w4a16 decode M={M} K={K} N={N} G={G}: {args.warmup} warmup + {args.steps} timed steps")
-    w4 = bench_w4a16(ops, M, K, N, G, args.steps, args.warmup)
+    w4 = bench_w4a16(ops, M, K, N, G, args.steps, args.warmup, direct=True)
     log(f"  {w4['us_per_call']:.2f} us/call  {w4['gbs']:.1f} GB/s  ({100 * w4['hbm_frac']:.1f}% of HBM peak), "
         f"{w4['weight_sets']} rotating sets = {w4['rotate_bytes'] / 2**20:.0f} MiB; per-launch time over "
         f"{w4['chunk_launches']}-launch chunks (a second pass): p50 {w4['us_p50_chunk']:.2f} us, "
@@ -950,6 +1060,13 @@ def main() -> int:
                 f"(the GEMM reaches {100 * r['frac_of_sustained']:.1f}% of it); "
                 f"the GEMM on zero operands: {r['us_zero_operands']:.1f} us ({r['tops_zero_operands']:.0f} TOPS)")
             w8.append(r)
+
+    w8gemv = None
+    if not args.no_w8a8:
+        log("w8 gemv (config 1) M=1 K=4096 N=4096: 500 steps")
+        w8gemv = bench_w8_gemv(ops, 500, 50)
+        log(f"  gemv {w8gemv['us_per_gemv']:.2f} us ({w8gemv['gemv_gbs']:.0f} GB/s, {100 * w8gemv['hbm_frac']:.1f}% of "
+            f"HBM peak); quant + gemv {w8gemv['us_per_step_quant_plus_gemv']:.2f} us")
 
     ceiling = None
     if not args.no_w8a8:
@@ -1011,7 +1128,11 @@ def main() -> int:
                      "kernel": "w4_decode_i8_kernel", "algorithmic_bytes": w4["bytes_per_call"],
                      "us_per_launch": round(w4["us_per_call"], 3),
                      "us_per_launch_p50_p90": [round(w4["us_p50_chunk"], 3), round(w4["us_p90_chunk"], 3)],
-                     "p50_p90_over": f"{w4['chunk_launches']}-launch chunks of a second timed pass"},
+                     "p50_p90_over": (f"{w4['chunk_launches']}-launch chunks of a second timed pass over "
+                                      f"max(steps, 10 chunks) launches"),
+                     "launch": ("direct stream launches enqueued while a spin kernel runs; the warm-up launches "
+                                "run immediately before the opening event"),
+                     "host_enqueue_ms": round(w4["host_enqueue_ms"], 3), "gpu_elapsed_ms": round(w4["elapsed_ms"], 3)},
         "w8a8_prefill": [
             {"M": r["M"], "K": r["K"], "N": r["N"], "us_per_call": round(r["us_per_call"], 2),
              "value": round(r["tops"], 1), "unit": "TOPS", "peak": INT8_PEAK_TOPS,
@@ -1022,6 +1143,7 @@ def main() -> int:
              "frac_of_sustained": round(r["frac_of_sustained"], 4),
              "us_zero_operands": round(r["us_zero_operands"], 2)}
             for r in w8],
+        "w8_gemv_config1": w8gemv,
         "mfma_ceiling": ceiling,
         "w8a8_cpu_baseline": cpu_w8,
         "fp8_gemm": fp8,
