@@ -145,7 +145,15 @@ int lhq_b8_prepack(const uint8_t* B, int K, int N, uint8_t* Bt, void* stream);
 /* ---- W4A16 GEMM: gemm_quant.hpp:47-57 / gemm_quant.cpp:54-82 ----------- */
 /* Reference semantics: fp32 A [M,K]; symmetric W4 prepacked by
  * lhq_w4_prepack_sym; C fp32 [M,N] = beta*C + alpha*A@W (beta == 0 never
- * reads C).  group_size must be a multiple of 32 that divides K. */
+ * reads C).  group_size must be a multiple of 32 that divides K.
+ * Non-finite activations (this and every W4A16 entry point below): the
+ * kernels sum x*(q - z) through exact group sums that subtract an
+ * activation sum, so a row of A holding +-Inf or NaN gives NaN in every
+ * output of that row; other rows are unaffected.  The reference's
+ * term-by-term sum (gemm_quant.cpp:78) gives +-Inf there (NaN only where a
+ * weight is zero or infinities of both signs meet).  Callers who need that
+ * propagation use lhq_q4_dequantize_groupwise + lhq_gemm_f32, as the lh::
+ * drop-in does when its host activations hold a non-finite value. */
 int lhq_gemm_w4a16(const float* A, const uint8_t* qweight, const float* scales,
                    float* C, int M, int N, int K, int group_size, float alpha, float beta,
                    void* stream);

@@ -7,6 +7,8 @@
 // launches the kernel and copies C back.
 #include "kernels/gemm_quant.hpp"
 
+#include <cmath>
+
 #include "kernels/device.hpp"
 #include "longhorn_hip.h"
 
@@ -33,6 +35,12 @@ void stage_a8(Buffer& dst, const void* A, int M, int K, int Kp) {
 // C staging: only read when beta != 0 (beta == 0 never reads C).
 void stage_c(Buffer& dC, const float* C, size_t count, float beta) {
     if (beta != 0.0f) dC.upload(C, count * sizeof(float));
+}
+
+bool all_finite(const float* x, size_t count) {
+    for (size_t i = 0; i < count; ++i)
+        if (!std::isfinite(x[i])) return false;
+    return true;
 }
 
 }  // namespace
@@ -87,7 +95,14 @@ void gemm_w4a16_groupwise(const float* A, const uint8_t* B_packed, const float* 
     dP.upload(B_packed, kn / 2);
     dS.upload(B_scales, ns * sizeof(float));
     stage_c(dC, C, mn, beta);
-    const bool mfma_groups = (G == 32 || G == 64 || G % 128 == 0);
+    // The MFMA kernels sum x * (q - z) through exact group sums that
+    // subtract an activation sum, so a non-finite activation turns its
+    // whole output row into NaN (Inf - Inf).  The reference adds
+    // a * (q * s) term by term (gemm_quant.cpp:74-79): +-Inf where the
+    // weight is nonzero, NaN where it is zero or infinities of both signs
+    // meet.  Host activations holding a non-finite value therefore take the
+    // dequantize + fp32 GEMM path, which adds products the same way.
+    const bool mfma_groups = (G == 32 || G == 64 || G % 128 == 0) && all_finite(A, nonneg(M) * nonneg(K));
     if (mfma_groups) {
         // int4 codes straight into the MFMA, group scales in fp32
         Buffer qw(static_cast<size_t>(lhq_w4_qweight_bytes(K, N)));
@@ -100,8 +115,9 @@ void gemm_w4a16_groupwise(const float* A, const uint8_t* B_packed, const float* 
                    "gemm_w4a16_groupwise");
     } else {
         // group sizes the MFMA segmentation cannot express (not 32, 64 or a
-        // multiple of 128): dequantize on the GPU (exact: float(q) * s, as
-        // gemm_quant.cpp:64-70 does) and run the fp32 GEMM on the GPU
+        // multiple of 128), or non-finite activations: dequantize on the GPU
+        // (exact: float(q) * s, as gemm_quant.cpp:64-70 does) and run the
+        // fp32 GEMM on the GPU
         Buffer dW(kn * sizeof(float));
         dev::check(lhq_q4_dequantize_groupwise(dP.as<uint8_t>(), dS.as<float>(), dW.as<float>(), K, N, G,
                                                dev::stream()),

@@ -5,6 +5,7 @@
 
 #include <cmath>
 #include <cstdint>
+#include <limits>
 #include <vector>
 
 #include "kernels/gemm.hpp"
@@ -63,6 +64,55 @@ TEST(GemmQuantParity, W4A16WithinFrobenius1e4) {
         const double err = lh_test::rel_frobenius(C, Co);
         EXPECT_LE(err, 1e-4) << "M=" << s.M << " N=" << s.N << " K=" << s.K << " G=" << s.G << " err=" << err;
     }
+}
+
+// Non-finite activations (+Inf, -Inf, NaN, and +Inf with -Inf in one row)
+// give the reference's pattern: +-Inf where the row's infinite products
+// agree in sign, NaN where an infinity meets a zero weight or the other
+// sign, NaN for a NaN activation; every other row within 1e-4.
+TEST(GemmQuantParity, W4A16NonFiniteActivationsFollowReference) {
+    const int M = 6, N = 96, K = 256, G = 128;
+    auto A = lh_test::uniform(static_cast<int64_t>(M) * K, 7100, -1.0f, 1.0f);
+    const float inf = std::numeric_limits<float>::infinity();
+    A[1 * K + 3] = inf;
+    A[2 * K + 200] = -inf;
+    A[3 * K + 17] = std::numeric_limits<float>::quiet_NaN();
+    A[4 * K + 5] = inf;
+    A[4 * K + 250] = -inf;
+    auto W = lh_test::uniform(static_cast<int64_t>(K) * N, 7101, -0.05f, 0.05f);
+    std::vector<uint8_t> Bp(W.size() / 2);
+    std::vector<float> Bs(static_cast<size_t>(K / G) * N);
+    lho_q4_quantize_groupwise(W.data(), Bp.data(), Bs.data(), K, N, G);
+    // a zero code under row 1's infinity in some columns: Inf * 0 = NaN there
+    for (int n = 0; n < N; n += 7) {
+        uint8_t& byte = Bp[static_cast<size_t>(3 / 2) * N + n];
+        byte = static_cast<uint8_t>(byte & 0x0f);  // k = 3 is the high nibble: code 0
+    }
+    std::vector<float> C(static_cast<size_t>(M) * N, 0.0f), Co(C);
+    lh::gemm_w4a16_groupwise(A.data(), Bp.data(), Bs.data(), C.data(), M, N, K, G, 1.0f, 0.0f);
+    lho_gemm_w4a16_groupwise(A.data(), Bp.data(), Bs.data(), Co.data(), M, N, K, G, 1.0f, 0.0f);
+    int nan_seen = 0, inf_seen = 0;
+    for (int m = 0; m < M; ++m) {
+        std::vector<float> row(C.begin() + m * N, C.begin() + (m + 1) * N), rowo(Co.begin() + m * N, Co.begin() + (m + 1) * N);
+        bool finite_row = true;
+        for (int n = 0; n < N; ++n) {
+            const float g = row[n], w = rowo[n];
+            if (std::isnan(w) || std::isinf(w)) finite_row = false;
+            if (std::isnan(w)) {
+                ++nan_seen;
+                EXPECT_TRUE(std::isnan(g)) << "m=" << m << " n=" << n << " got " << g;
+            } else if (std::isinf(w)) {
+                ++inf_seen;
+                EXPECT_EQ(g, w) << "m=" << m << " n=" << n;
+            }
+        }
+        if (finite_row) {
+            const double err = lh_test::rel_frobenius(row, rowo);
+            EXPECT_LE(err, 1e-4) << "row " << m << " err=" << err;
+        }
+    }
+    EXPECT_GT(nan_seen, 0);
+    EXPECT_GT(inf_seen, 0);
 }
 
 TEST(GemmQuantParity, Fp8WithinFrobenius1e5) {

@@ -464,3 +464,80 @@ def test_w4a16_grouped_prefill_empty_expert(oracle, ops):
     assert off[2] == off[1]
     assert rel_frobenius(got, want) <= TOL_BF16
     assert _ulp_close(got, want, oracle)
+
+
+# Non-finite activations on the C ABI.  The kernels sum x * (q - z) through
+# exact group sums that subtract an activation sum (t - (128 + z) * xs, or a
+# chain seeded with -144 * sum x, or a block exponent that becomes NaN), so
+# a row holding +Inf, -Inf or NaN comes out NaN in every column; every other
+# row is unaffected.  (The reference's term-by-term sum, gemm_quant.cpp:78,
+# gives +-Inf there, NaN only where a weight is zero; the lh:: drop-in routes
+# non-finite host activations to the dequantize + fp32 GEMM path for that.)
+NONFINITE_BF16 = [(1, 4096, 2048), (4, 4096, 1024), (16, 4096, 1024), (64, 1024, 512), (256, 1024, 512)]
+
+
+def _nonfinite_rows(M):
+    """(row, value) pairs to plant: one row each of +Inf, -Inf, NaN, and +Inf
+    with -Inf together, as many as the rows allow (M = 1: +Inf)."""
+    vals = [np.inf, -np.inf, np.nan, "both"]
+    return [(r * max(1, M // 4), v) for r, v in enumerate(vals[:max(1, min(4, M))])]
+
+
+def _check_nonfinite(got, want, bad, tol):
+    good = np.setdiff1d(np.arange(got.shape[0]), bad)
+    for r in bad:
+        assert np.isnan(got[r]).all(), f"row {r}: {np.isfinite(got[r]).sum()} finite outputs"
+    if len(good):
+        assert np.isfinite(got[good]).all()
+        assert rel_frobenius(got[good], want[good]) <= tol
+
+
+@pytest.mark.parametrize("M,K,N", NONFINITE_BF16)
+def test_w4a16_bf16_nonfinite_rows_are_nan(oracle, ops, M, K, N):
+    """M=1: the integer decode kernel; 4: the bf16 decode kernel; 16: the
+    16-row kernel; 64 / 256: the prefill tile kernel."""
+    G = 128
+    x = D.normal((M, K), 1.0, 4000 + M)
+    bad = []
+    for r, v in _nonfinite_rows(M):
+        if v == "both":
+            x[r, 5], x[r, K - 9] = np.inf, -np.inf
+        else:
+            x[r, (37 * r + 11) % K] = v
+        bad.append(r)
+    A = D.to_bf16_bits(oracle, x)
+    W = D.normal((K, N), 0.02, 4001)
+    p, s, z = oracle.q4a_quantize_groupwise(W, G)
+    w = ops.prepack_w4_asym(ops.dev(p), ops.dev(s), ops.dev(z), K, N, G)
+    got = D.bf16_bits_to_f32(ops.host(ops.gemm_w4a16_bf16(ops.dev(A), w), np.uint16))
+    good = np.setdiff1d(np.arange(M), bad)
+    want = np.zeros((M, N), np.float32)
+    if len(good):
+        want[good] = oracle.gemm_w4a16_asym(np.ascontiguousarray(A[good]), p, s, z, N, G)
+    _check_nonfinite(got, want, bad, TOL_BF16)
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 4096, 2048), (16, 4096, 1024), (64, 1024, 512)])
+def test_w4a16_f32_nonfinite_rows_are_nan(oracle, ops, M, K, N):
+    """The fp32 interface: integer decode (M=1), 16-row kernel (16), tile
+    kernel with the hi + lo activation split (64)."""
+    G = 128
+    A = D.uniform((M, K), -1, 1, 4100 + M)
+    bad = []
+    for r, v in _nonfinite_rows(M):
+        if v == "both":
+            A[r, 5], A[r, K - 9] = np.inf, -np.inf
+        else:
+            A[r, (37 * r + 11) % K] = v
+        bad.append(r)
+    W = D.uniform((K, N), -1, 1, 4101)
+    Bp, Bs = oracle.q4_quantize_groupwise(W, G)
+    w = ops.prepack_w4_sym(ops.dev(Bp), ops.dev(Bs), K, N, G)
+    C = ops.dev(np.zeros((M, N), np.float32))
+    ops.gemm_w4a16(ops.dev(A), w, C, 1.0, 0.0)
+    got = ops.host(C)
+    good = np.setdiff1d(np.arange(M), bad)
+    want = np.zeros((M, N), np.float32)
+    if len(good):
+        want[good] = oracle.gemm_w4a16_groupwise(np.ascontiguousarray(A[good]), Bp, Bs, N, G)
+    _check_nonfinite(got, want, bad, TOL_F32)
