@@ -663,12 +663,19 @@ def bench_w8_gemv(ops, steps, warmup, seed=0, K=4096, N=4096, min_rotate_bytes=2
     return res
 
 
+def diag_lib():
+    """liblonghorn_diag.so: the matrix-core rate probes (not the product library)."""
+    from longhornai_amd import capi
+    return capi.load_diag()
+
+
 PROBE_OPS_PER_MFMA = {0: 65536, 1: 131072, 2: 16384, 3: 65536, 4: 65536, 5: 32768, 6: 32768, 7: 32768}
 PROBE_MFMAS_PER_ITER = {0: 32, 1: 32, 2: 32, 3: 32, 4: 64, 5: 64, 6: 32, 7: 32}
 
 
 def operand_probe(ops, kind: int, A, B, iters: int = 4000, steps: int = 5, warmup: int = 2):
-    """The matrix cores' rate on given operand values: lhq_probe_mfma_operands
+    """The matrix cores' rate on given operand values: lhd_probe_mfma_operands
+    (the diagnostics library, include/longhorn_diag.h)
     with one workgroup of 4 waves per CU (one wave per SIMD, the W8A8 / FP8
     tiles' occupancy), each wave issuing MFMAs on 16 accumulators in turn from
     fragments it loaded once.  The fragments are bytes from the start of the
@@ -696,10 +703,10 @@ def operand_probe(ops, kind: int, A, B, iters: int = 4000, steps: int = 5, warmu
     clocks = torch.zeros(2 * cus, dtype=torch.int64, device="cuda")
 
     def launch(_i):
-        st = ops.lib().cdll.lhq_probe_mfma_operands(kind, buf.data_ptr(), cus, iters, sink.data_ptr(),
+        st = diag_lib().cdll.lhd_probe_mfma_operands(kind, buf.data_ptr(), cus, iters, sink.data_ptr(),
                                                     clocks.data_ptr(), ops.stream())
         if st:
-            raise RuntimeError(f"lhq_probe_mfma_operands: {ops.lib().last_error()}")
+            raise RuntimeError(f"lhd_probe_mfma_operands: {diag_lib().last_error()}")
 
     ms, _ = GraphTimer(launch, 1, chunk=steps).time(steps, warmup)
     rate = cus * 4 * iters * PROBE_MFMAS_PER_ITER[kind] * PROBE_OPS_PER_MFMA[kind] * steps / (ms * 1e-3) / 1e12
@@ -735,9 +742,9 @@ def mfma_ceiling(ops, steps: int = 5, warmup: int = 2):
             (7, "int8_16x16x64_chain", 32768, 5600, INT8_PEAK_TOPS, None)):
         blocks = 8 * cus if blocks is None else blocks
         def launch(i, kind=kind, iters=iters, blocks=blocks):
-            st = ops.lib().cdll.lhq_probe_mfma_rate(kind, blocks, iters, sink.data_ptr(), ops.stream())
+            st = diag_lib().cdll.lhd_probe_mfma_rate(kind, blocks, iters, sink.data_ptr(), ops.stream())
             if st:
-                raise RuntimeError(f"lhq_probe_mfma_rate: {ops.lib().last_error()}")
+                raise RuntimeError(f"lhd_probe_mfma_rate: {diag_lib().last_error()}")
         ms, _ = GraphTimer(launch, 1, chunk=steps).time(steps, warmup)
         per_launch = blocks * 4 * iters * 4 * per_op
         rate = per_launch * steps / (ms * 1e-3) / 1e12

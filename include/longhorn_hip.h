@@ -182,12 +182,14 @@ int lhq_gemm_w4a16_bf16_ws(const uint16_t* A, const uint8_t* qweight, const uint
  * graph capture, serving loops, harnesses that forbid hipMalloc); no
  * counterpart in the reference.  It allocates nothing: the split-K partial
  * sums go to a static 32 MiB device array of the library, one per GPU, held
- * until the process ends, whose address is looked up once per device.  The
- * split plan is lhq_gemm_w4a16_bf16_ws's with the workspace it asks for, so
- * the results are bit-identical to that entry point's; a shape whose plan
- * needs more than 32 MiB is rejected with LHQ_ERR_UNSUPPORTED (no shape up to
- * 64 rows does today).  Calls that overlap on one GPU share the array and
- * race: serialize them (one stream, or events). */
+ * until the process ends, whose address is looked up on the first call on
+ * each device (that call may be under graph capture).  The split plan is
+ * lhq_gemm_w4a16_bf16_ws's with a workspace of
+ * min(lhq_gemm_w4a16_bf16_workspace_bytes, 32 MiB) bytes, and the results
+ * are bit-identical to that call's: a shape whose plan asks for more than
+ * 32 MiB (2..16 rows at very long K, e.g. M=16, K=131072, N=16384) runs
+ * fewer splits.  Calls that overlap on one GPU share the array and race:
+ * serialize them (one stream, or events). */
 int lhq_gemm_w4a16_bf16_noalloc(const uint16_t* A, const uint8_t* qweight, const uint16_t* scales,
                                 const uint32_t* zeros, uint16_t* C, int M, int N, int K,
                                 int group_size, void* stream);
@@ -313,38 +315,8 @@ int lhq_gemm_f32_batched(const float* A, const float* B, float* C, int batch, in
  * reference's rule (dtypes.hpp:87-98).  counts: 2 device uint64, set to
  * {non-NaN mismatches, NaN mismatches}; both are 0 on a conforming device. */
 int lhq_selftest_bf16(unsigned long long* counts, void* stream);
-/* Matrix-core rate probe: `blocks` workgroups of 4 waves, each wave running
- * `iters` rounds of 4 MFMAs on register operands (no memory traffic), so the
- * launch time gives the sustained MFMA rate with the GPU loaded.  Kinds 0..5
- * rotate over 4 independent accumulators: 0: v_mfma_i32_32x32x32_i8 (65,536
- * ops each), 1: v_mfma_f32_16x16x32_bf16 (16,384 flops), 2:
- * v_mfma_f32_32x32x16_bf16 (32,768 flops), 3: v_mfma_i32_16x16x64_i8
- * (32,768 ops); 4, 5: kind 1 with 2 or 4 independent integer VALU operations
- * per MFMA (whether VALU work overlaps the matrix core's).  Kinds 6, 7: one
- * dependent chain (each MFMA accumulates onto the previous result) of kind 1's
- * and kind 3's instruction.  One launch performs blocks * 4 * iters * 4
- * MFMAs.  sink: `blocks` device ints (written). */
-int lhq_probe_mfma_rate(int kind, int blocks, int iters, int* sink, void* stream);
-/* Matrix-core rate on the caller's operand values: `blocks` workgroups of 4
- * waves; each wave loads two sets of 8 fragments (4 A blocks, 4 B blocks)
- * from `operands` once, then runs `iters` rounds of 32 MFMAs: two k steps,
- * each one MFMA on each of 16 accumulators in turn (the W8A8 / FP8 tiles'
- * order).  The rate depends on the values through the power limit.  Kinds:
- * 0: v_mfma_i32_32x32x32_i8 (65,536 ops each), 1:
- * v_mfma_scale_f32_32x32x64_f8f6f4, e4m3 with unit scales (131,072 flops),
- * 2: v_mfma_f32_16x16x32_bf16 (16,384 flops), 3 and 4: kind 0 issued as
- * k chains of 2 and 4 MFMAs on one accumulator (each round 32 and 64 MFMAs),
- * 5 and 6: v_mfma_i32_16x16x64_i8 (32,768 ops) on the same fragments, as k
- * chains of 4 (64 per round) and one per accumulator in turn (32 per round),
- * 7: that instruction as k chains of 2 (32 per round).
- * operands: 32 KiB of device
- * memory; fragment x (0..7) of set s (0..1) for lane l is the 16 bytes at
- * ((8s + x) * 64 + l) * 16 (kind 1: the fragment's low half there, its high
- * half 16 KiB further).  sink: `blocks` device ints (written).  clocks: null,
- * or 2 * `blocks` device uint64 set to {shader-clock ticks, 100 MHz ticks}
- * over wave 0's loop in each workgroup. */
-int lhq_probe_mfma_operands(int kind, const void* operands, int blocks, int iters, int* sink,
-                            unsigned long long* clocks, void* stream);
+/* The matrix-core rate probes bench.py uses are in the separate diagnostics
+ * library (include/longhorn_diag.h, liblonghorn_diag.so). */
 
 #ifdef __cplusplus
 }

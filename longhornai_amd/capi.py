@@ -80,8 +80,14 @@ SIGNATURES = {
     "lhq_gemm_f32_ref": [_p, _p, _p, _i, _i, _i, _f, _f, _p],
     "lhq_gemm_f32_batched": [_p, _p, _p, _i, _i, _i, _i, _f, _f, _p],
     "lhq_selftest_bf16": [_p, _p],
-    "lhq_probe_mfma_rate": [_i, _i, _i, _p, _p],
-    "lhq_probe_mfma_operands": [_i, _p, _i, _i, _p, _p, _p],
+}
+# The diagnostics library (include/longhorn_diag.h): matrix-core rate probes.
+DIAG_PATH = os.path.join(_HERE, "lib", "liblonghorn_diag.so")
+DIAG_HEADER = os.path.join(os.path.dirname(_HERE), "include", "longhorn_diag.h")
+DIAG_SIGNATURES = {
+    "lhd_last_error": [],
+    "lhd_probe_mfma_rate": [_i, _i, _i, _p, _p],
+    "lhd_probe_mfma_operands": [_i, _p, _i, _i, _p, _p, _p],
 }
 _RESTYPES = {
     "lhq_status_string": C.c_char_p,
@@ -100,11 +106,12 @@ class LhqError(RuntimeError):
         self.status = status
 
 
-def header_symbols(path: str = HEADER) -> list[str]:
-    """Every function name declared in include/longhorn_hip.h."""
+def header_symbols(path: str = HEADER, prefix: str = "lhq_") -> list[str]:
+    """Every function name declared in include/longhorn_hip.h (or, with
+    path=DIAG_HEADER and prefix="lhd_", in include/longhorn_diag.h)."""
     text = open(path).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(lhq_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(" + prefix + r"\w+)\s*\(", text)))
 
 
 class _Lib:
@@ -146,3 +153,40 @@ def load(path: str = LIB_PATH) -> _Lib:
     if _LIB is None or _LIB.path != path:
         _LIB = _Lib(path)
     return _LIB
+
+
+class _DiagLib:
+    """liblonghorn_diag.so: the matrix-core rate probes (include/longhorn_diag.h)."""
+
+    def __init__(self, path: str):
+        if not os.path.exists(path):
+            raise FileNotFoundError(
+                f"{path} is not built: run `python -c 'import __graft_entry__ as g; g.build()'`")
+        self.cdll = C.CDLL(path)
+        self.path = path
+        for name, args in DIAG_SIGNATURES.items():
+            fn = getattr(self.cdll, name)
+            fn.argtypes = args
+            fn.restype = C.c_char_p if name == "lhd_last_error" else _i
+
+    def last_error(self) -> str:
+        return self.cdll.lhd_last_error().decode()
+
+    def call(self, name: str, *args) -> int:
+        st = getattr(self.cdll, name)(*args)
+        if st != LHQ_OK:
+            raise LhqError(name, st, self.last_error())
+        return st
+
+    def status(self, name: str, *args) -> int:
+        return getattr(self.cdll, name)(*args)
+
+
+_DIAG = None
+
+
+def load_diag(path: str = DIAG_PATH) -> _DiagLib:
+    global _DIAG
+    if _DIAG is None or _DIAG.path != path:
+        _DIAG = _DiagLib(path)
+    return _DIAG

@@ -1217,8 +1217,11 @@ int launch_gemm8(const uint8_t* A, const uint8_t* Bt, const float* As, const flo
             gemm8_skinny_kernel<EPI><<<ceil_div(N, 16), 64 * SK_WAVES, 0, as_stream(stream)>>>(p);
             return check_launch(who);
         }
+#ifdef LHQ_TUNING_KNOBS
+        // sweep build only: the 32x32x32 tile (LHQ_GEMM8_M16=0, 3 or 4
+        // stages) and the register-staged kernel (LHQ_GEMM8_DMA=0); the
+        // product library compiles only the 16x16x64 tile for int8
         if (use_dma) {
-            // the 16x16x64 tile (LHQ_GEMM8_M16=0: the 32x32x32 one)
             static const int m16 = env_int("LHQ_GEMM8_M16", 1);
             static const int stages = env_int("LHQ_GEMM8_STAGES", DS_STAGES);
             if (m16) return launch_dma<EPI, 4, true>(p, tiles, stream, who);
@@ -1227,9 +1230,19 @@ int launch_gemm8(const uint8_t* A, const uint8_t* Bt, const float* As, const flo
                 default: return launch_dma<EPI, 4, false>(p, tiles, stream, who);
             }
         }
+#else
+        (void)use_dma;
+        return launch_dma<EPI, 4, true>(p, tiles, stream, who);
+#endif
     }
-    gemm8_kernel<OP, EPI><<<tiles, NTHREADS, 0, as_stream(stream)>>>(p);
-    return check_launch(who);
+#ifndef LHQ_TUNING_KNOBS
+    if constexpr (OP == OP_FP8) {
+#endif
+        gemm8_kernel<OP, EPI><<<tiles, NTHREADS, 0, as_stream(stream)>>>(p);
+        return check_launch(who);
+#ifndef LHQ_TUNING_KNOBS
+    }
+#endif
 }
 
 }  // namespace

@@ -1258,7 +1258,9 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
     for (int c = 0; c < MM_CT; ++c) dnt[c] = min(nt0 + c, p.Nt - 1) - nt0;
     const int nt_left = p.Nt - nt0;
     // extents in bytes, at most 2^32 - 1 (offsets within them are 32-bit)
-    auto extent = [](int64_t bytes) { return static_cast<int>(static_cast<uint32_t>(min(bytes, int64_t{0xFFFFFFFF}))); };
+    auto extent = [](int64_t bytes) {
+        return static_cast<int>(static_cast<uint32_t>(bytes < int64_t{0xFFFFFFFF} ? bytes : int64_t{0xFFFFFFFF}));
+    };
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t*>(qw) + static_cast<int64_t>(nt0) * p.Kt * kW4TileBytes, 0,
         extent(static_cast<int64_t>(nt_left) * p.Kt * kW4TileBytes), kBufWord3);
@@ -2304,7 +2306,9 @@ std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
 
 // The current device's scratch address, looked up on the first call made on
-// that device and kept.
+// that device and kept.  hipGetSymbolAddress is no stream operation, so that
+// first call may also be made under HIP graph capture (tested in a fresh
+// process whose first call is captured).
 int scratch_for_current_device(const char* who, void** out) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -2369,15 +2373,15 @@ int lhq_gemm_w4a16_bf16_noalloc(const uint16_t* A, const uint8_t* qweight, const
                                 const uint32_t* zeros, uint16_t* C, int M, int N, int K, int G, void* stream) {
     const char* who = "gemm_w4a16_bf16_noalloc";
     if (int st = check_w4_shape(who, M, N, K, G)) return st;
+    // the workspace entry point's plan with a workspace of min(need, the
+    // scratch): a shape whose plan asks for more runs fewer splits, as
+    // lhq_gemm_w4a16_bf16_ws does with a 32 MiB workspace
     const int64_t need = lhq_gemm_w4a16_bf16_workspace_bytes(M, N, K, G);
-    LHQ_SUPPORTED(need <= kNoAllocScratchBytes,
-                  "%s: M=%d N=%d K=%d needs %lld bytes of split-K scratch, the static scratch holds %lld "
-                  "(use lhq_gemm_w4a16_bf16_ws with a larger workspace)",
-                  who, M, N, K, static_cast<long long>(need), static_cast<long long>(kNoAllocScratchBytes));
+    const int64_t cap = need < kNoAllocScratchBytes ? need : kNoAllocScratchBytes;
     void* ws = nullptr;
-    if (need > 0)
+    if (cap > 0)
         if (int st = scratch_for_current_device(who, &ws)) return st;
-    return gemm_w4a16_bf16_plan(who, A, qweight, scales, zeros, C, M, N, K, G, ws, need, stream);
+    return gemm_w4a16_bf16_plan(who, A, qweight, scales, zeros, C, M, N, K, G, ws, cap, stream);
 }
 
 int lhq_gemm_w4a16_bf16_batched(const uint16_t* A, const uint8_t* qweight, const uint16_t* scales,

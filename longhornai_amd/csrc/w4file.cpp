@@ -324,6 +324,10 @@ uint64_t fnv1a64(const uint8_t* p, size_t n) {
 
 int w4_dims(const char* who, int K, int N, int G, int fp16_scales, W4Dims& d, std::string& err) {
     W4_REQUIRE(w4_dims_ok(K, N, G), "%s: bad dims K=%d N=%d G=%d", who, K, N, G);
+    // the group sizes every W4A16 GEMM entry point takes: a file holding
+    // another would load and then fail at its first use
+    W4_SUPPORTED(G == 32 || G == 64 || G % 128 == 0, "%s: group_size %d: the W4A16 GEMMs take 32, 64 or a multiple of 128",
+                 who, G);
     d.K = K;
     d.N = N;
     d.G = G;

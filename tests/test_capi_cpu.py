@@ -21,6 +21,20 @@ def test_exports_every_declared_symbol(L):
     assert set(declared) == set(capi.SIGNATURES), "ctypes table out of sync with the header"
 
 
+def test_diag_library_exports_its_header_and_product_has_no_probes(L):
+    """The matrix-core probes live in liblonghorn_diag.so (longhorn_diag.h),
+    not in the product library, and their argument checks run on the host."""
+    D = capi.load_diag()
+    declared = capi.header_symbols(capi.DIAG_HEADER, "lhd_")
+    assert set(declared) == set(capi.DIAG_SIGNATURES), declared
+    assert not [s for s in declared if not hasattr(D.cdll, s)]
+    assert not [s for s in ("lhq_probe_mfma_rate", "lhq_probe_mfma_operands") if hasattr(L.cdll, s)]
+    sink = (C.c_int * 4)()
+    assert D.status("lhd_probe_mfma_rate", 8, 1, 1, C.addressof(sink), None) == 1
+    assert "kind" in D.last_error()
+    assert D.status("lhd_probe_mfma_operands", 0, None, 1, 1, C.addressof(sink), None, None) == 1
+
+
 def test_status_strings(L):
     assert L.lhq_status_string(0) == b"ok"
     assert L.lhq_status_string(capi.LHQ_ERR_UNSUPPORTED) == b"unsupported configuration"

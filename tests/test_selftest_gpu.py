@@ -11,6 +11,13 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(scope="module")
+def diag(lib):
+    """The diagnostics library (include/longhorn_diag.h) holding the probes."""
+    from longhornai_amd import capi
+    return capi.load_diag()
+
+
 def test_bf16_convert_matches_reference_rule_exhaustively(lib):
     import torch
     from longhornai_amd import ops
@@ -21,20 +28,21 @@ def test_bf16_convert_matches_reference_rule_exhaustively(lib):
     assert non_nan == 0 and nan == 0, f"mismatches: {non_nan} non-NaN, {nan} NaN"
 
 
-def test_mfma_rate_probe_runs_and_rejects_bad_arguments(lib):
-    """The matrix-core rate probe (bench.py's ceiling leg): a small launch of
+def test_mfma_rate_probe_runs_and_rejects_bad_arguments(diag):
+    """The matrix-core rate probe of the diagnostics library (bench.py's
+    ceiling leg): a small launch of
     each kind completes and writes one value per workgroup; an unknown kind
     is refused before any launch."""
     import torch
     from longhornai_amd import ops
     sink = torch.full((16,), -1, dtype=torch.int32, device="cuda")
     for kind in range(8):
-        lib.call("lhq_probe_mfma_rate", kind, 16, 8, sink.data_ptr(), ops.stream())
+        diag.call("lhd_probe_mfma_rate", kind, 16, 8, sink.data_ptr(), ops.stream())
     torch.cuda.synchronize()
-    assert lib.status("lhq_probe_mfma_rate", 8, 16, 8, sink.data_ptr(), ops.stream()) != 0
+    assert diag.status("lhd_probe_mfma_rate", 8, 16, 8, sink.data_ptr(), ops.stream()) != 0
 
 
-def test_mfma_operand_probe_runs_and_rejects_bad_arguments(lib):
+def test_mfma_operand_probe_runs_and_rejects_bad_arguments(diag):
     """The matrix-core rate probe on operands from memory (bench.py's
     same-operands figures): every kind completes and writes one value per
     workgroup and two clock counts; the int8 kind's accumulators grow
@@ -49,14 +57,14 @@ def test_mfma_operand_probe_runs_and_rejects_bad_arguments(lib):
     sink = torch.full((16,), -1, dtype=torch.int32, device="cuda")
     clocks = torch.zeros(32, dtype=torch.int64, device="cuda")
     for kind in range(8):
-        lib.call("lhq_probe_mfma_operands", kind, src.data_ptr(), 16, 4, sink.data_ptr(), clocks.data_ptr(),
+        diag.call("lhd_probe_mfma_operands", kind, src.data_ptr(), 16, 4, sink.data_ptr(), clocks.data_ptr(),
                  ops.stream())
         torch.cuda.synchronize()
         c = clocks.view(16, 2).cpu()
         assert bool((c[:, 1] > 0).all()) and bool((c[:, 0] > c[:, 1]).all()), c
     sums = []
     for iters in (1, 3):
-        lib.call("lhq_probe_mfma_operands", 0, src.data_ptr(), 16, iters, sink.data_ptr(), 0, ops.stream())
+        diag.call("lhd_probe_mfma_operands", 0, src.data_ptr(), 16, iters, sink.data_ptr(), 0, ops.stream())
         torch.cuda.synchronize()
         sums.append(sink.cpu().tolist())
     assert len(set(sums[0])) == 1 and sums[0][0] != 0
@@ -64,8 +72,8 @@ def test_mfma_operand_probe_runs_and_rejects_bad_arguments(lib):
     # the k-chain kinds issue the same products per round (kind 3) or twice
     # them (kind 4): integer sums equal to kind 0's, or double
     for kind, mult in ((3, 1), (4, 2)):
-        lib.call("lhq_probe_mfma_operands", kind, src.data_ptr(), 16, 3, sink.data_ptr(), 0, ops.stream())
+        diag.call("lhd_probe_mfma_operands", kind, src.data_ptr(), 16, 3, sink.data_ptr(), 0, ops.stream())
         torch.cuda.synchronize()
         assert all((mult * b - c) % 2**32 == 0 for b, c in zip(sums[1], sink.cpu().tolist())), kind
-    assert lib.status("lhq_probe_mfma_operands", 8, src.data_ptr(), 16, 4, sink.data_ptr(), 0, ops.stream()) != 0
-    assert lib.status("lhq_probe_mfma_operands", 0, 0, 16, 4, sink.data_ptr(), 0, ops.stream()) != 0
+    assert diag.status("lhd_probe_mfma_operands", 8, src.data_ptr(), 16, 4, sink.data_ptr(), 0, ops.stream()) != 0
+    assert diag.status("lhd_probe_mfma_operands", 0, 0, 16, 4, sink.data_ptr(), 0, ops.stream()) != 0

@@ -88,6 +88,8 @@ BAD = [
     ("K_text", lambda t, m: m.update(K="25x"), capi.LHQ_ERR_INVALID),
     ("K_mismatch", lambda t, m: m.update(K="512"), capi.LHQ_ERR_INVALID),
     ("G_not_dividing", lambda t, m: m.update(group_size="100"), capi.LHQ_ERR_INVALID),
+    # divides K, but no W4A16 GEMM takes it (32, 64 or a multiple of 128)
+    ("G_unsupported", lambda t, m: m.update(group_size="16"), capi.LHQ_ERR_UNSUPPORTED),
     ("scales_dtype", lambda t, m: t.update(scales=t["scales"].astype(np.float32)), capi.LHQ_ERR_INVALID),
     ("qweight_short", lambda t, m: t.update(qweight=t["qweight"][:-16]), capi.LHQ_ERR_INVALID),
     ("missing_zeros", lambda t, m: t.pop("zeros"), capi.LHQ_ERR_INVALID),

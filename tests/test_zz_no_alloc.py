@@ -86,3 +86,47 @@ def test_noalloc_in_a_captured_hip_graph(oracle, ops):
         torch.cuda.synchronize()
         print(f"graph replay {rep}", flush=True)
         assert np.array_equal(ops.host(C, np.uint16), want), f"replay {rep}"
+
+
+def test_noalloc_first_call_under_graph_capture():
+    """The first call in a process, where the scratch address is looked up,
+    may itself be under graph capture: a fresh process captures its very
+    first no-alloc call and replays the graph against the workspace entry
+    point (tests/noalloc_capture_first.py)."""
+    import os
+    import subprocess
+    import sys
+    script = os.path.join(os.path.dirname(os.path.abspath(__file__)), "noalloc_capture_first.py")
+    r = subprocess.run([sys.executable, "-u", script], capture_output=True, text=True, timeout=300)
+    print(r.stdout, r.stderr[-2000:], flush=True)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stderr[-2000:]
+
+
+def test_noalloc_caps_a_plan_above_the_scratch(ops):
+    """A shape whose split plan asks for more than the 32 MiB scratch (16 rows
+    at K = 131072) runs the workspace entry point's plan with a 32 MiB
+    workspace: fewer splits, bit-identical results."""
+    import torch
+    cap = 32 << 20
+    M, K, N, G = 16, 131072, 16384, 128
+    need = ops.lib().lhq_gemm_w4a16_bf16_workspace_bytes(M, N, K, G)
+    print(f"noalloc M={M} K={K} N={N}: plan asks {need} bytes, scratch {cap}", flush=True)
+    assert need > cap
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(31)
+    q, s, z = ops.w4_buffers(K, N, G, True)
+    q.copy_(torch.randint(0, 256, q.shape, dtype=torch.uint8, device="cuda", generator=gen))
+    s.copy_((torch.rand(s.shape, device="cuda", generator=gen) * 0.001).half().view(torch.int16))
+    z.copy_(torch.randint(-2**31, 2**31 - 1, z.shape, dtype=torch.int32, device="cuda", generator=gen))
+    w = ops.W4Weights(q, s, z, K, N, G, True)
+    A = torch.randn((M, K), device="cuda", generator=gen).to(torch.bfloat16).view(torch.int16)
+    ws = ops.empty((cap,), np.uint8)
+    ref = ops.host(ops.gemm_w4a16_bf16_ws(A, w, ws), np.uint16)
+    full = ops.host(ops.gemm_w4a16_bf16_ws(A, w, ops.empty((need,), np.uint8)), np.uint16)
+    for rep in range(2):
+        got = ops.host(ops.gemm_w4a16_bf16_noalloc(A, w, ops.empty((M, N), np.int16)), np.uint16)
+        assert np.array_equal(got, ref), rep
+    # the capped plan is a different split of the same sums: within the bf16 bar of the full one
+    assert rel_frobenius(D.bf16_bits_to_f32(got), D.bf16_bits_to_f32(full)) <= 1e-2
+    del q, s, z, w, ws
+    torch.cuda.empty_cache()
