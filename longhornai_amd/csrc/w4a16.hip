@@ -1176,7 +1176,8 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
     static_assert(RB == 4 || (RB <= 2 && L != 0 && !GR), "16- and 32-row blocks on plain launches, not 128 x 128");
     static_assert(!SK || (!GR && !SWI), "split-K on plain launches only");
     static_assert(L != 4 || SK, "the 8-wave 64 x 256 layout on split-K launches only");
-    static_assert(!F32 || (!GR && !SWI && !SK && L == 1 && RB == 4), "the fp32 interface: plain 64 x 256 tiles");
+    static_assert(!F32 || (!GR && !SWI && !SK && L != 0 && L != 4 && (RB == 4 ? L == 1 : true)),
+                  "the fp32 interface: plain launches, 64 x 256 tiles or 16- / 32-row blocks");
     constexpr int SEGS = 4 / BPS;
     constexpr int NW = (L >= 3) ? 8 : 4;                                  // waves
     constexpr int NK = (L == 2 || L == 4) ? 2 : (L == 3) ? 4 : 1;        // K parts
@@ -1234,7 +1235,8 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
     // array captured by the lambdas below, makes hipcc's host pass drop the
     // kernel's launch stub without a diagnostic; entries past DMA are unused)
     static_assert(DMA >= 1 && DMA <= 8, "activation DMAs per wave");
-    static_assert(NK == 1 || (RR % (DMA * 4) == 0 && RR / (DMA * 4) == NW / NK),
+    constexpr int DROWS = 64 * DMA / CPR;  // LDS rows one wave's DMAs fill
+    static_assert(NK == 1 || (RR % DROWS == 0 && RR / DROWS == NW / NK),
                   "each wave's DMA rows lie in its own K part's region");
     uint32_t a_voff[8];  // byte offsets from the workgroup's first row
 #pragma unroll
@@ -1321,17 +1323,27 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
     const bool live = m0 + 64 * wm < m_end;
     auto compute = [&](const uint8_t* buf, const Regs& R, int kt_in) {
         const int kt = kt_in + kofs;
-        if (!live || kt >= ke) return;  // the last K part may be short
+        // the last K part may be short; the fp32 form has a barrier inside,
+        // which every wave of the workgroup reaches with or without work
+        const bool active = live && kt < ke;
+        if (!F32 && !active) return;
         if constexpr (F32) {
             // Symmetric codes: 16 - 8 in every byte.  The VALU phase decodes
-            // the weights and splits this wave's own row block (wave w: rows
-            // 16w ..) into bf16 hi + lo in place: each lane overwrites the two
-            // fp32 chunks it read with their hi and lo halves, so no lane
-            // writes what another still reads.  It also computes that block's
-            // sums xs into LDS.  After a barrier the matrix phase, at raised
-            // priority, reads every row block's hi / lo fragments and sums.
-            static_assert(RB == NW, "one row block per wave");
-            f32x4_t* const xs_l = reinterpret_cast<f32x4_t*>(mm_lds + 2 * A_BYTES);
+            // the weights and splits the K part's activation rows into bf16
+            // hi + lo in place: the RB x 4 (row block, 32-k block) units of
+            // the region are dealt out in order to its WPR waves, UPW each,
+            // and each lane overwrites the two fp32 chunks it read with their
+            // hi and lo halves, so no lane writes what another still reads.
+            // Each wave also adds its units' activation sums into partial xs
+            // per row block in LDS (one partial per row block where a wave
+            // holds whole row blocks, PS per row block otherwise).  After a
+            // barrier the matrix phase, at raised priority, reads every row
+            // block's hi / lo fragments and adds its partial sums.
+            constexpr int WPR = NW / NK;               // waves sharing the region
+            constexpr int UPW = 4 * RB / WPR;          // units per wave
+            constexpr int PS = UPW >= 4 ? 1 : 4 / UPW; // partial sums per row block
+            static_assert(UPW * WPR == 4 * RB && (UPW % 4 == 0 || 4 % UPW == 0), "units per wave");
+            f32x4_t* const xs_l = reinterpret_cast<f32x4_t*>(mm_lds + 2 * A_BYTES) + wr * RB * PS * 64;
             u32x4_t b[MM_CT][4];
             float scv[MM_CT];
 #pragma unroll
@@ -1346,29 +1358,32 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
                 const int c0 = 8 * j + 2 * (lane >> 4) + h;
                 return const_cast<uint8_t*>(buf) + a_frag + i * 16 * RBYTES + ((c0 ^ col) * 16);
             };
-            {
-                u32x4_t ah[4], al[4];
+            if (active) {
+                f32x4_t xs = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const f32x4_t x0 = *reinterpret_cast<const f32x4_t*>(chunk(wave, j, 0));
-                    const f32x4_t x1 = *reinterpret_cast<const f32x4_t*>(chunk(wave, j, 1));
+                for (int q = 0; q < UPW; ++q) {
+                    const int u = wn * UPW + q, i = u / 4, j = u % 4;
+                    const f32x4_t x0 = *reinterpret_cast<const f32x4_t*>(chunk(i, j, 0));
+                    const f32x4_t x1 = *reinterpret_cast<const f32x4_t*>(chunk(i, j, 1));
                     const float v[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+                    u32x4_t ah, al;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const uint16_t h0 = f32_to_bf16(v[2 * e]), h1 = f32_to_bf16(v[2 * e + 1]);
-                        ah[j][e] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
-                        al[j][e] = pack_bf16x2(v[2 * e] - bf16_to_f32(h0), v[2 * e + 1] - bf16_to_f32(h1));
+                        ah[e] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
+                        al[e] = pack_bf16x2(v[2 * e] - bf16_to_f32(h0), v[2 * e + 1] - bf16_to_f32(h1));
                     }
-                    *reinterpret_cast<u32x4_t*>(chunk(wave, j, 0)) = ah[j];
-                    *reinterpret_cast<u32x4_t*>(chunk(wave, j, 1)) = al[j];
+                    *reinterpret_cast<u32x4_t*>(chunk(i, j, 0)) = ah;
+                    *reinterpret_cast<u32x4_t*>(chunk(i, j, 1)) = al;
+                    xs = mfma_bf16_16x16x32(ah, m144, xs);
+                    xs = mfma_bf16_16x16x32(al, m144, xs);
+                    if (j == 3 || q == UPW - 1) {
+                        // row block i's sum over this wave's units: partial
+                        // (u % 4) / UPW of PS (0 when the wave holds the block)
+                        xs_l[(i * PS + (PS > 1 ? (u % 4) / UPW : 0)) * 64 + lane] = xs;
+                        xs = f32x4_t{0.f, 0.f, 0.f, 0.f};
+                    }
                 }
-                f32x4_t xs = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    xs = mfma_bf16_16x16x32(ah[j], m144, xs);
-                    xs = mfma_bf16_16x16x32(al[j], m144, xs);
-                }
-                xs_l[wave * 64 + lane] = xs;
             }
             // every wave's splits and sums are in LDS (lgkmcnt(0); the next
             // tile's loads stay in flight); the empty asm statements keep the
@@ -1377,6 +1392,7 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
             asm volatile("" ::: "memory");
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
+            if (!active) return;
             __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int i = 0; i < RB; ++i) {
@@ -1386,7 +1402,13 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
                     ah[j] = *reinterpret_cast<const u32x4_t*>(chunk(i, j, 0));
                     al[j] = *reinterpret_cast<const u32x4_t*>(chunk(i, j, 1));
                 }
-                const f32x4_t xs = xs_l[i * 64 + lane];
+                f32x4_t xs = xs_l[i * PS * 64 + lane];
+#pragma unroll
+                for (int q = 1; q < PS; ++q) {
+                    const f32x4_t x2 = xs_l[(i * PS + q) * 64 + lane];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) xs[r] += x2[r];
+                }
 #pragma unroll
                 for (int c = 0; c < MM_CT; ++c) {
                     f32x4_t t = xs;
@@ -1834,25 +1856,55 @@ int launch_mma(const W4Args& a, int64_t rows, int groups, int batch, hipStream_t
 }
 
 // The fp32 interface on the tile kernel (64 x 256 tiles, plain launches).
-int launch_mma_f32(const W4Args& a, hipStream_t s, const char* who) {
-    const int64_t tiles = ceil_div64(a.M, 64);
+// The fp32 interface on the tile kernel: L = 1 with 64-row blocks (64 x 256
+// tiles), or 16- / 32-row blocks (RB = 1, 2) with K split across the waves
+// of the workgroup (L = 2: two K halves, 16/32 x 128 tiles, 4 waves; L = 3:
+// four K quarters, 8 waves) for launches of up to 32 rows, which have few
+// output tiles and take no workspace for a K split across workgroups.
+template <int L, int RB>
+int launch_mma_f32_rb(const W4Args& a, hipStream_t s, const char* who) {
+    constexpr int NW = L >= 3 ? 8 : 4, NK = L == 2 ? 2 : L == 3 ? 4 : 1, WN = L == 1 ? 4 : 2;
+    constexpr size_t a_bytes = static_cast<size_t>(NK) * 16 * RB * kW4TileK * 4;
+    constexpr int UPW = 4 * RB / (NW / NK), PS = UPW >= 4 ? 1 : 4 / UPW;
+    constexpr size_t lds = 2 * a_bytes + static_cast<size_t>(NK) * RB * PS * 64 * 16;  // tiles, partial sums
+    const int64_t tiles = ceil_div64(a.M, 16 * RB);
     LHQ_SUPPORTED(tiles <= 65535, "%s: %lld row tiles exceed the grid limit", who, static_cast<long long>(tiles));
-    constexpr size_t lds = 2 * 64 * kW4TileK * 4 + 4 * 64 * 16;  // two fp32 tiles and the row blocks' sums
-    const dim3 grid(ceil_div(a.Nt, 4 * MM_CT), static_cast<unsigned>(tiles), 1);
+    const dim3 grid(ceil_div(a.Nt, WN * MM_CT), static_cast<unsigned>(tiles), 1);
     if (a.gmul) {
-        allow_cu_lds<&w4_mma_kernel<4, true, false, false, 1, false, 4, true>>();
-        w4_mma_kernel<4, true, false, false, 1, false, 4, true><<<grid, 256, lds, s>>>(a);
+        allow_cu_lds<&w4_mma_kernel<4, true, false, false, L, false, RB, true>>();
+        w4_mma_kernel<4, true, false, false, L, false, RB, true><<<grid, 64 * NW, lds, s>>>(a);
     } else {
-        allow_cu_lds<&w4_mma_kernel<4, false, false, false, 1, false, 4, true>>();
-        w4_mma_kernel<4, false, false, false, 1, false, 4, true><<<grid, 256, lds, s>>>(a);
+        allow_cu_lds<&w4_mma_kernel<4, false, false, false, L, false, RB, true>>();
+        w4_mma_kernel<4, false, false, false, L, false, RB, true><<<grid, 64 * NW, lds, s>>>(a);
     }
     return check_launch(who);
 }
+int launch_mma_f32(const W4Args& a, hipStream_t s, const char* who) { return launch_mma_f32_rb<1, 4>(a, s, who); }
 
-// The prefill tile kernel serves the bf16 entry points when there are rows
-// enough to reuse each decoded weight tile (LHQ_W4_MMA=0 / 1 forces it off /
-// on where it applies): G >= 128, K % 128 == 0 (no activation padding in
-// LDS) and 32-bit element offsets for the activations.
+// fp32 interface at 2..47 rows: 0 = the ordinary choice (the 64-row tile
+// where mma_applies, else the 16-row kernel), L = 2, 3 = the tile kernel
+// with 16-row blocks (M <= 16) or 32-row blocks (ceil(M/32) row tiles),
+// K split in halves / quarters across the waves of the workgroup.  Measured
+// on MI355X at K = 8192 (us; ordinary / L = 2 / L = 3):
+//   M = 4..16, N = 28672: 55-75 / 50 / 44-48; N <= 11008: the ordinary
+//     kernel wins (M = 16, N = 8192: 27 / 46 / 40);
+//   M = 24, 32: N = 57344 180 / 110 / 127-134; N = 28672 176 / 74 / 68-71;
+//     N = 14336 (K = 4096) 38-43 / 37-38 / 32-34; N = 10240 48-53 / 67 / 58-61;
+//   M = 40, 47: N = 57344 184-185 / 191 / 233; N = 28672 178-179 / 103-105 /
+//     122-123; N = 14336 59-64 / 38-39 / 34; N = 10240 75-76 / 70 / 61-62.
+// The 64-row tile at 17..47 rows and N >= 16384 walks all of K in one row
+// tile of 112 workgroups (N = 28672), which the K-split layouts quadruple.
+int f32_thin_layout(const W4Args& a, int M) {
+    static const int env = tuning_knob("LHQ_W4_F32_THIN", -1);
+    if (M < 2 || M > 47 || a.G < kW4TileK || a.K % kW4TileK != 0) return 0;
+    if (env >= 0) return env;
+    const int N = a.N;
+    if (M <= 3) return 0;
+    if (M <= 16) return N >= 16384 ? 3 : 0;
+    if (M <= 32) return N >= 40000 ? 2 : N >= 12288 ? 3 : 0;
+    return N >= 40000 ? 0 : N >= 16384 ? 2 : N >= 10240 ? 3 : 0;
+}
+
 bool mma_applies(const W4Args& a, int64_t rows, double rows_per_block) {
     static const int env = tuning_knob("LHQ_W4_MMA", -1);
     if (env == 0) return false;
@@ -2340,7 +2392,15 @@ int lhq_gemm_w4a16(const float* A, const uint8_t* qweight, const float* scales, 
     LHQ_REQUIRE(qweight && scales && C && (A || M == 0), "gemm_w4a16: null pointer");
     if (M == 0) return LHQ_OK;
     W4Args a = make_args(A, qweight, scales, nullptr, C, M, N, K, G, alpha, beta);
-    if (mma_applies(a, M, M)) return launch_mma_f32(a, as_stream(stream), "w4a16 prefill (fp32)");
+    const char* who = "w4a16 prefill (fp32)";
+    const int thin = f32_thin_layout(a, M);
+    if (!thin && mma_applies(a, M, M)) return launch_mma_f32(a, as_stream(stream), who);
+    if (thin == 2) return M <= 16 ? launch_mma_f32_rb<2, 1>(a, as_stream(stream), who)
+                                  : launch_mma_f32_rb<2, 2>(a, as_stream(stream), who);
+    if (thin == 3) return M <= 16 ? launch_mma_f32_rb<3, 1>(a, as_stream(stream), who)
+                                  : launch_mma_f32_rb<3, 2>(a, as_stream(stream), who);
+    if (thin == 1) return M <= 16 ? launch_mma_f32_rb<1, 1>(a, as_stream(stream), who)
+                                  : launch_mma_f32_rb<1, 2>(a, as_stream(stream), who);
     return launch_w4<true, false, true>(a, 1, as_stream(stream));
 }
 

@@ -76,6 +76,31 @@ def test_w4a16_f32_beta0_ignores_nan_in_c(oracle, ops):
     assert rel_frobenius(got, want) <= TOL_F32
 
 
+# The fp32 interface at 2..32 rows on the tile kernel's 16- and 32-row blocks
+# with K split across the waves of a workgroup (where the launch picks it;
+# every layout is also run by forcing it in the sweep build): ragged K
+# (K parts of unequal length, and an empty last part at Kt = 9 in quarters),
+# partial column groups, G = 256, alpha / beta.
+@pytest.mark.parametrize("M,K,N,G,alpha,beta", [
+    (2, 1024, 96, 128, 1.0, 0.0),
+    (5, 1152, 200, 128, 0.5, 2.0),
+    (16, 4096, 4096, 128, 1.0, 0.0),
+    (16, 8192, 1040, 256, -1.0, 1.0),
+    (17, 2304, 272, 128, 1.0, 0.0),
+    (24, 1152, 4096, 128, 2.0, -0.5),
+    (32, 8192, 2048, 128, 1.0, 0.0),
+    # shapes the launch itself sends to the K-split layouts
+    (16, 1024, 16384, 128, 1.0, 0.0),      # 16-row blocks, K quarters
+    (24, 1152, 16384, 128, 0.5, 1.0),      # 32-row blocks, K quarters, an empty last quarter
+    (40, 1024, 20480, 128, 1.0, 0.0),      # two 32-row tiles, K halves
+    (20, 2048, 49152, 256, 1.0, 0.0),      # 32-row blocks, K halves, G = 256
+])
+def test_w4a16_f32_thin_tile(oracle, ops, M, K, N, G, alpha, beta):
+    got, want = _sym_case(oracle, ops, M, K, N, G, seed=1700 + M + K // 128, alpha=alpha, beta=beta)
+    err = rel_frobenius(got, want)
+    assert err <= TOL_F32, f"rel Frobenius {err:.3e}"
+
+
 # The fp32 interface on the prefill tile kernel (48+ rows, G >= 128, K a
 # multiple of 128): fp32 activations split into bf16 hi + lo operands.
 @pytest.mark.parametrize("M,K,N,G,alpha,beta", [
