@@ -969,7 +969,8 @@ def main() -> int:
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a 1 GiB device copy (PMC calibration kernel)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the W4A16 prefill and MoE legs")
-    ap.add_argument("--only", choices=["w4a16", "w8a8", "prefill", "moe", "fp8", "configs", "mfma", "f32", "w8gemv"],
+    ap.add_argument("--only", choices=["w4a16", "w8a8", "prefill", "moe", "fp8", "configs", "mfma", "f32", "w8gemv",
+                                      "thin", "grouped"],
                     default=None,
                     help="run one leg only (profiling); prints that leg's summary, not the bench line")
     ap.add_argument("--moe-tokens", type=int, default=512,
@@ -1003,6 +1004,24 @@ def main() -> int:
                 f"{r['sustained_same_operands']['value']:.0f} TOPS the MFMAs sustain on these values at "
                 f"{r['sustained_same_operands']['ghz']:.2f} GHz); zero operands {r['us_zero_operands']:.1f} us")
             print(json.dumps({"leg": "w8a8_prefill", **r}), flush=True)
+        return 0
+    if args.only == "thin":
+        # the thin-grid W4A16 launches (split K across workgroups through the
+        # workspace entry point): config 5 at M=64, config 2 at M=16
+        for m, kns in ((64, CONFIG5[1]), (16, CONFIG2[1])):
+            for k, n in kns:
+                r = bench_w4a16(ops, m, k, n, G, 200, 20, workspace=True)
+                log(f"w4a16 thin M={m} K={k} N={n}: {r['us_per_call']:.1f} us  {r['gbs']:.0f} GB/s "
+                    f"({100 * r['hbm_frac']:.1f}% HBM), workspace {r['workspace_bytes']} B")
+                print(json.dumps({"leg": "w4a16_thin", "M": m, "K": k, "N": n, "us_per_call": round(r["us_per_call"], 2),
+                                  "gbs": round(r["gbs"], 1), "hbm_frac": round(r["hbm_frac"], 4),
+                                  "workspace_bytes": r["workspace_bytes"]}), flush=True)
+        return 0
+    if args.only == "grouped":
+        r = bench_moe(ops, 200, 20)
+        log(f"moe grouped W4A16 (config 4): {r['us_per_call']:.1f} us  {r['tflops']:.0f} TFLOPS "
+            f"({100 * r['mfma_frac']:.1f}% of bf16 peak)")
+        print(json.dumps({"leg": "moe_grouped_w4a16", **r}), flush=True)
         return 0
     if args.only == "w8gemv":
         r = bench_w8_gemv(ops, 500, 50)
