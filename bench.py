@@ -323,24 +323,38 @@ def bench_moe(ops, steps, warmup, seed=0, T=512, E=8, topk=2, K=4096, N=14336, G
     qptr = torch.tensor([w.qweight.data_ptr() for w in sets], dtype=torch.int64, device="cuda")
     sptr = torch.tensor([w.scales.data_ptr() for w in sets], dtype=torch.int64, device="cuda")
     zptr = torch.tensor([w.zeros.data_ptr() for w in sets], dtype=torch.int64, device="cuda")
-    fn = ops.lib().cdll.lhq_gemm_w4a16_bf16_grouped
+    L = ops.lib().cdll
+    # the persistent launch (its workspace, as the query sizes it) and the
+    # one-workgroup-per-tile grid without one
+    ws_bytes = L.lhq_gemm_w4a16_bf16_grouped_workspace_bytes(E, rows, N, K, G)
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device="cuda")
 
-    def launch(_i):
-        st = fn(A.data_ptr(), offd.data_ptr(), qptr.data_ptr(), sptr.data_ptr(), zptr.data_ptr(), C.data_ptr(),
-                E, rows, N, K, G, ops.stream())
-        if st:
-            raise RuntimeError(f"lhq_gemm_w4a16_bf16_grouped: {ops.lib().last_error()}")
+    def launcher(persistent):
+        def launch(_i):
+            if persistent:
+                st = L.lhq_gemm_w4a16_bf16_grouped_ws(A.data_ptr(), offd.data_ptr(), qptr.data_ptr(), sptr.data_ptr(),
+                                                      zptr.data_ptr(), C.data_ptr(), E, rows, N, K, G, ws.data_ptr(),
+                                                      ws_bytes, ops.stream())
+            else:
+                st = L.lhq_gemm_w4a16_bf16_grouped(A.data_ptr(), offd.data_ptr(), qptr.data_ptr(), sptr.data_ptr(),
+                                                   zptr.data_ptr(), C.data_ptr(), E, rows, N, K, G, ops.stream())
+            if st:
+                raise RuntimeError(f"grouped W4A16: {ops.lib().last_error()}")
+        return launch
 
-    ms, _ = GraphTimer(launch, 1, chunk=16).time(steps, warmup)
+    ms_grid, _ = GraphTimer(launcher(False), 1, chunk=16).time(steps, warmup)
+    ms, _ = GraphTimer(launcher(True), 1, chunk=16).time(steps, warmup)
     us = ms * 1e3 / steps
     flops = 2 * rows * K * N
     byts = E * (K * N // 2 + (K // G) * N * 2 + (K // G) * N // 2) + rows * K * 2 + rows * N * 2
     res = {"tokens": T, "experts": E, "top_k": topk, "rows": rows, "rows_per_expert": counts.tolist(),
            "K": K, "N": N, "G": G, "us_per_call": us, "tflops": flops / (us * 1e-6) / 1e12,
-           "gbs": byts / (us * 1e-6) / 1e9, "flops": flops, "bytes": byts}
+           "gbs": byts / (us * 1e-6) / 1e9, "flops": flops, "bytes": byts,
+           "launch": "persistent, left-over tiles split along K (lhq_gemm_w4a16_bf16_grouped_ws)",
+           "workspace_bytes": ws_bytes, "us_per_call_grid": ms_grid * 1e3 / steps}
     res["mfma_frac"] = res["tflops"] / BF16_PEAK_TFLOPS
     res["hbm_frac"] = res["gbs"] / HBM_PEAK_GBS
-    del sets, A, C
+    del sets, A, C, ws
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     return res
@@ -431,6 +445,10 @@ def bench_moe_layer(ops, steps, warmup, seed=0, T=512, E=8, topk=2, H=4096, I=14
     out = ops.empty((T, H), np.int16)
     L = ops.lib()
     st = ops.stream
+    # one workspace for both grouped launches (they run in order on the stream)
+    ws_bytes = max(L.cdll.lhq_gemm_w4a16_bf16_grouped_swiglu_workspace_bytes(E, S, I, H, G),
+                   L.cdll.lhq_gemm_w4a16_bf16_grouped_workspace_bytes(E, S, H, I, G))
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device="cuda")
 
     def chk(name, status):
         if status:
@@ -442,13 +460,14 @@ def bench_moe_layer(ops, steps, warmup, seed=0, T=512, E=8, topk=2, H=4096, I=14
                                                      st()))
 
     def gate_up(_i):
-        chk("gate_up", L.cdll.lhq_gemm_w4a16_bf16_grouped_swiglu(xs.data_ptr(), off.data_ptr(), guq.data_ptr(),
-                                                                 gus.data_ptr(), guz.data_ptr(), act.data_ptr(), E,
-                                                                 S, I, H, G, st()))
+        chk("gate_up", L.cdll.lhq_gemm_w4a16_bf16_grouped_swiglu_ws(xs.data_ptr(), off.data_ptr(), guq.data_ptr(),
+                                                                    gus.data_ptr(), guz.data_ptr(), act.data_ptr(), E,
+                                                                    S, I, H, G, ws.data_ptr(), ws_bytes, st()))
 
     def down_proj(_i):
-        chk("down", L.cdll.lhq_gemm_w4a16_bf16_grouped(act.data_ptr(), off.data_ptr(), dq.data_ptr(), ds.data_ptr(),
-                                                       dz.data_ptr(), y.data_ptr(), E, S, H, I, G, st()))
+        chk("down", L.cdll.lhq_gemm_w4a16_bf16_grouped_ws(act.data_ptr(), off.data_ptr(), dq.data_ptr(), ds.data_ptr(),
+                                                          dz.data_ptr(), y.data_ptr(), E, S, H, I, G, ws.data_ptr(),
+                                                          ws_bytes, st()))
 
     def combine(_i):
         chk("combine", L.cdll.lhq_moe_combine_bf16(y.data_ptr(), pos.data_ptr(), gates.data_ptr(), out.data_ptr(),
@@ -473,7 +492,8 @@ def bench_moe_layer(ops, steps, warmup, seed=0, T=512, E=8, topk=2, H=4096, I=14
         "combine": (combine, 0, S * H * 2 + T * H * 2 + T * topk * 8),
     }
     res = {"tokens": T, "experts": E, "top_k": topk, "hidden": H, "intermediate": I, "G": G,
-           "rows_per_expert": rows, "stages": {}}
+           "rows_per_expert": rows, "grouped_launches": "persistent (the _ws entry points)",
+           "workspace_bytes": ws_bytes, "stages": {}}
     total_flops = total_bytes = 0
     for name, (fn, flops, byts) in stages.items():
         n = steps if flops else 4 * steps
@@ -492,7 +512,7 @@ def bench_moe_layer(ops, steps, warmup, seed=0, T=512, E=8, topk=2, H=4096, I=14
     res.update({"layer_us": round(us, 2), "tokens_per_s": round(T / (us * 1e-6), 1),
                 "layer_tflops": round(total_flops / (us * 1e-6) / 1e12, 1),
                 "layer_gbs": round(total_bytes / (us * 1e-6) / 1e9, 1)})
-    del gu, down, x, xs, act, y, out
+    del gu, down, x, xs, act, y, out, ws
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     return res

@@ -222,6 +222,41 @@ int lhq_gemm_w4a16_bf16_grouped_swiglu(const uint16_t* A, const int32_t* offsets
                                        int num_groups, int row_capacity, int I, int K,
                                        int group_size, void* stream);
 
+/* The two grouped launches above with a caller workspace (no reference
+ * counterpart: the reference's per-expert CPU loops need no partial sums).
+ * Where the tile kernel runs (enough rows per group), one persistent launch
+ * of two workgroups per CU walks the (group, 64-row tile, 256-column group)
+ * tiles counted from the device-side offsets table, one tile at a time per
+ * workgroup; where the tiles fill less than three quarters of one round,
+ * they are split along K evenly over all workgroups (stream-K), each K
+ * segment's fp32 partial sums going to `workspace`, and a second kernel on
+ * the stream adds each split tile's segments in K order (deterministic) and
+ * writes it.  Results match the calls without a workspace within fp32
+ * reassociation (bit for bit where nothing is split).
+ * lhq_gemm_w4a16_bf16_grouped[_swiglu]_workspace_bytes gives the bytes the
+ * split can use for a table of num_groups groups over row_capacity rows (0:
+ * the shape runs no tile kernel).  A smaller workspace (at least 64 KiB)
+ * still takes the persistent launch and splits only when the segments fit;
+ * NULL or less runs the launch without one.
+ * workspace: device memory, 16-byte aligned, any contents, not shared with
+ * a call running concurrently (calls in order on one stream may share it). */
+int64_t lhq_gemm_w4a16_bf16_grouped_workspace_bytes(int num_groups, int row_capacity, int N, int K,
+                                                    int group_size);
+int64_t lhq_gemm_w4a16_bf16_grouped_swiglu_workspace_bytes(int num_groups, int row_capacity, int I,
+                                                           int K, int group_size);
+int lhq_gemm_w4a16_bf16_grouped_ws(const uint16_t* A, const int32_t* offsets,
+                                   const uint8_t* const* qweights, const uint16_t* const* scales,
+                                   const uint32_t* const* zeros, uint16_t* C, int num_groups,
+                                   int row_capacity, int N, int K, int group_size, void* workspace,
+                                   int64_t workspace_bytes, void* stream);
+int lhq_gemm_w4a16_bf16_grouped_swiglu_ws(const uint16_t* A, const int32_t* offsets,
+                                          const uint8_t* const* qweights,
+                                          const uint16_t* const* scales,
+                                          const uint32_t* const* zeros, uint16_t* act,
+                                          int num_groups, int row_capacity, int I, int K,
+                                          int group_size, void* workspace, int64_t workspace_bytes,
+                                          void* stream);
+
 /* ---- MoE routing: moe.hpp:63-102 / moe.cpp:102-221 ---------------------- */
 /* moe_dispatch (moe.hpp:75-78, moe.cpp:102-140): expert_ids [T, top_k] ->
  * expert_offsets [E+1], token_idx / slot_idx [T*top_k] (stable: slot order
@@ -277,6 +312,22 @@ int lhq_moe_expert_mlp_w4a16_bf16(const uint16_t* expert_inputs, const int32_t* 
                                   uint16_t* expert_outputs, int n_experts, int row_capacity,
                                   int hidden_dim, int intermediate_dim, int group_size,
                                   void* stream);
+/* The same with the grouped launches' workspace (lhq_gemm_w4a16_bf16_grouped_ws;
+ * the two launches run in order on `stream` and share it): the larger of
+ * lhq_gemm_w4a16_bf16_grouped_swiglu_workspace_bytes(n_experts, row_capacity,
+ * intermediate_dim, hidden_dim, group_size) and
+ * lhq_gemm_w4a16_bf16_grouped_workspace_bytes(n_experts, row_capacity,
+ * hidden_dim, intermediate_dim, group_size) lets both split fully. */
+int lhq_moe_expert_mlp_w4a16_bf16_ws(const uint16_t* expert_inputs, const int32_t* expert_offsets,
+                                     const uint8_t* const* gate_up_qweights,
+                                     const uint16_t* const* gate_up_scales,
+                                     const uint32_t* const* gate_up_zeros,
+                                     const uint8_t* const* down_qweights,
+                                     const uint16_t* const* down_scales,
+                                     const uint32_t* const* down_zeros, uint16_t* act,
+                                     uint16_t* expert_outputs, int n_experts, int row_capacity,
+                                     int hidden_dim, int intermediate_dim, int group_size,
+                                     void* workspace, int64_t workspace_bytes, void* stream);
 
 /* ---- W8A8 GEMM: gemm_quant.hpp:34-45 / gemm_quant.cpp:29-49 ------------ */
 /* Reference semantics, bit-exact: Aq int8 [M,K]; Bt = lhq_b8_prepack(Bq);

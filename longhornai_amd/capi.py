@@ -60,6 +60,10 @@ SIGNATURES = {
     "lhq_gemm_w4a16_bf16_batched": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p],
     "lhq_gemm_w4a16_bf16_grouped": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p],
     "lhq_gemm_w4a16_bf16_grouped_swiglu": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p],
+    "lhq_gemm_w4a16_bf16_grouped_workspace_bytes": [_i, _i, _i, _i, _i],
+    "lhq_gemm_w4a16_bf16_grouped_swiglu_workspace_bytes": [_i, _i, _i, _i, _i],
+    "lhq_gemm_w4a16_bf16_grouped_ws": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i64, _p],
+    "lhq_gemm_w4a16_bf16_grouped_swiglu_ws": [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i64, _p],
     "lhq_w4_save": [C.c_char_p, _p, _p, _p, _i, _i, _i, _i, _p],
     "lhq_w4_file_info": [C.c_char_p, _p, _p, _p, _p],
     "lhq_w4_load": [C.c_char_p, _p, _p, _p, _i, _i, _i, _i, _p],
@@ -72,6 +76,8 @@ SIGNATURES = {
     "lhq_moe_combine_q8_f32": [_p, _p, _p, _p, _p, _i, _i, _i, _p],
     "lhq_moe_combine_q8_bf16": [_p, _p, _p, _p, _p, _i, _i, _i, _p],
     "lhq_moe_expert_mlp_w4a16_bf16": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p],
+    "lhq_moe_expert_mlp_w4a16_bf16_ws": [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _p, _i64,
+                                         _p],
     "lhq_gemm_w8a8": [_p, _p, _p, _p, _p, _i, _i, _i, _f, _f, _p],
     "lhq_gemm_w8a8_bf16": [_p, _p, _p, _p, _p, _i, _i, _i, _p],
     "lhq_gemm_w8a8_i32": [_p, _p, _p, _i, _i, _i, _p],
@@ -97,6 +103,8 @@ _RESTYPES = {
     "lhq_w4_zeros_bytes": _i64,
     "lhq_b8_prepacked_bytes": _i64,
     "lhq_gemm_w4a16_bf16_workspace_bytes": _i64,
+    "lhq_gemm_w4a16_bf16_grouped_workspace_bytes": _i64,
+    "lhq_gemm_w4a16_bf16_grouped_swiglu_workspace_bytes": _i64,
 }
 
 

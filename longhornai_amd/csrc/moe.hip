@@ -416,4 +416,21 @@ int lhq_moe_expert_mlp_w4a16_bf16(const uint16_t* expert_inputs, const int32_t* 
                                        n_experts, row_capacity, hidden_dim, intermediate_dim, group_size, stream);
 }
 
+int lhq_moe_expert_mlp_w4a16_bf16_ws(const uint16_t* expert_inputs, const int32_t* expert_offsets,
+                                     const uint8_t* const* gate_up_qweights, const uint16_t* const* gate_up_scales,
+                                     const uint32_t* const* gate_up_zeros, const uint8_t* const* down_qweights,
+                                     const uint16_t* const* down_scales, const uint32_t* const* down_zeros,
+                                     uint16_t* act, uint16_t* expert_outputs, int n_experts, int row_capacity,
+                                     int hidden_dim, int intermediate_dim, int group_size, void* workspace,
+                                     int64_t workspace_bytes, void* stream) {
+    if (int st = lhq_gemm_w4a16_bf16_grouped_swiglu_ws(expert_inputs, expert_offsets, gate_up_qweights,
+                                                       gate_up_scales, gate_up_zeros, act, n_experts, row_capacity,
+                                                       intermediate_dim, hidden_dim, group_size, workspace,
+                                                       workspace_bytes, stream))
+        return st;
+    return lhq_gemm_w4a16_bf16_grouped_ws(act, expert_offsets, down_qweights, down_scales, down_zeros,
+                                          expert_outputs, n_experts, row_capacity, hidden_dim, intermediate_dim,
+                                          group_size, workspace, workspace_bytes, stream);
+}
+
 }  // extern "C"

@@ -63,6 +63,10 @@ struct W4Args {
     // [s * kps, (s + 1) * kps) and writes fp32 partial sums ws[s][M][N]
     float* ws;
     int kps;
+    // persistent grouped launches: the workspace's 64 KiB partial-sum slots
+    // (at ws) and the launch's worker count
+    int64_t pk_slots;
+    int pk_workers;
 };
 
 // Scale group of segment s of K tile kt; a segment is BPS 32-wide k blocks
@@ -1171,10 +1175,107 @@ constexpr int kBufWord3 = 0x00020000;
 // bytes per row) and each fragment is split into bf16 hi + lo operands as it
 // is read, so every product runs twice on the bf16 MFMA (product error near
 // 2^-17 relative, as in the 16-row kernel's fp32 form); 64 x 256 tiles only.
-template <int BPS, bool GBIG, bool GR, bool SWI, int L, bool SK = false, int RB = 4, bool F32 = false>
-__global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_kernel(W4Args p) {
+
+// Persistent grouped launches (PK): one 64 x 256 tile's fp32 partial sums,
+// in f32x4 (one workspace slot, 64 KiB)
+constexpr int kPkTileVecs = 4 * 4 * MM_CT * 64;
+constexpr int64_t kPkSlotBytes = int64_t{kPkTileVecs} * 16;
+constexpr int kPkMinSegKt = 4;  // K tiles per stream-K part at least
+
+// Row blocks of rb rows over a grouped launch's table, counted as
+// resolve_group_rows lays them out (the same clamps); uniform.
+__device__ __forceinline__ int count_row_blocks(const W4Args& p, int rb) {
+    const int lane = threadIdx.x & 63;
+    int total = 0;
+    for (int e0 = 0; e0 < p.num_groups; e0 += 64) {
+        const int g = e0 + lane;
+        int nb = 0;
+        if (g < p.num_groups) {
+            const int r0 = min(max(p.offsets[g], 0), p.row_capacity);
+            const int r1 = min(max(p.offsets[g + 1], r0), p.row_capacity);
+            nb = (r1 - r0 + rb - 1) / rb;
+        }
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) nb += __shfl_xor(nb, d, 64);
+        total += nb;
+    }
+    return __builtin_amdgcn_readfirstlane(total);
+}
+
+// The work split of a persistent grouped launch over P workers (the tile
+// kernel and the fixup kernel derive the same plan from the same table).
+struct PkPlan {
+    int X;             // column groups of 256
+    int64_t dp_tiles;  // tiles dealt out whole
+    int64_t R;         // tiles past the last whole round
+    bool sk;           // the R tiles spread along K (only when R = T < P)
+    int64_t I;         // their K tiles, R * Kt
+    int Ps;            // workers sharing them
+};
+__device__ __forceinline__ PkPlan pk_plan(const W4Args& p, int P) {
+    PkPlan pl;
+    pl.X = (p.Nt + 4 * MM_CT - 1) / (4 * MM_CT);
+    const int64_t T = static_cast<int64_t>(pl.X) * count_row_blocks(p, 64);
+    const int64_t q = T / P;
+    pl.R = T - q * P;
+    pl.I = pl.R * p.Kt;
+    pl.Ps = static_cast<int>(min<int64_t>(P, max<int64_t>(1, pl.I / kPkMinSegKt)));
+    pl.sk = p.ws && q == 0 && 4 * pl.R <= 3 * static_cast<int64_t>(P) && pl.R > 0 && pl.Ps + pl.R - 1 <= p.pk_slots;
+    pl.dp_tiles = pl.sk ? q * P : T;
+    return pl;
+}
+// The worker whose part of the stream-K range holds K tile x of it: parts
+// are [floor(w I / Ps), floor((w + 1) I / Ps)), so w = ceil((x + 1) Ps / I) - 1.
+__device__ __forceinline__ int pk_worker_of(int64_t x, const PkPlan& pl) {
+    return static_cast<int>(((x + 1) * pl.Ps + pl.I - 1) / pl.I - 1);
+}
+
+// The bf16 epilogue of one wave's 16 RB x 16 MM_CT block: accumulator
+// (i, c) element r is row r0 + 16 i + 4 (lane >> 4) + r, column lane & 15 of
+// column tile nt0 + c.  SWI: blocks (c, c + 1) hold a gate tile and its up
+// tile (nt0 even), stored as act column tile (nt0 + c) / 2.
+template <bool SWI, int RB>
+__device__ __forceinline__ void store_bf16_block(const W4Args& p, uint16_t* C, const f32x4_t (&acc)[RB][MM_CT],
+                                                 int nt0, int r0, int m_end, int lane) {
+    const int col = lane & 15;
+#pragma unroll
+    for (int c = 0; c < MM_CT; c += SWI ? 2 : 1) {
+        const int nt = nt0 + c;
+        const int cn = (SWI ? (nt >> 1) : nt) * kW4TileN + col;
+        if (nt >= p.Nt || cn >= p.N) continue;
+#pragma unroll
+        for (int i = 0; i < RB; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = r0 + i * 16 + 4 * (lane >> 4) + r;
+                if (row >= m_end) continue;
+                if constexpr (SWI)
+                    C[static_cast<int64_t>(row) * p.N + cn] = f32_to_bf16(swiglu(acc[i][c][r], acc[i][c + 1][r]));
+                else C[static_cast<int64_t>(row) * p.N + cn] = f32_to_bf16(acc[i][c][r]);
+            }
+    }
+}
+
+// A pointer that is the same in every lane, moved to scalar registers.
+template <typename T>
+__device__ __forceinline__ T* uniform_ptr(T* q) {
+    const uint64_t v = reinterpret_cast<uint64_t>(q);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+    return reinterpret_cast<T*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// One output tile of w4_mma_kernel: column group bx, row tile by, batch or
+// split bz, K tiles [kb, ke) (a split-K launch takes its range from bz).
+// pk_slot >= 0 (persistent grouped launches): [kb, ke) is one K segment of
+// a tile split across workgroups, whose fp32 partial sums go to workspace
+// slot pk_slot in register order; w4_pk_fixup_kernel adds the segments.
+template <int BPS, bool GBIG, bool GR, bool SWI, int L, bool SK, int RB, bool F32, bool PK>
+__device__ __forceinline__ void mma_tile(const W4Args& p, uint8_t* mm_lds, int bx, int by, int bz, int kb_in,
+                                         int ke_in, int pk_slot) {
     static_assert(RB == 4 || (RB <= 2 && L != 0 && !GR), "16- and 32-row blocks on plain launches, not 128 x 128");
     static_assert(!SK || (!GR && !SWI), "split-K on plain launches only");
+    static_assert(!PK || (GR && L == 1 && RB == 4 && !SK && !F32), "persistent launches: grouped 64 x 256 tiles");
     static_assert(L != 4 || SK, "the 8-wave 64 x 256 layout on split-K launches only");
     static_assert(!F32 || (!GR && !SWI && !SK && L != 0 && L != 4 && (RB == 4 ? L == 1 : true)),
                   "the fp32 interface: plain launches, 64 x 256 tiles or 16- / 32-row blocks");
@@ -1188,7 +1289,7 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
     constexpr int CPR = RBYTES / 16;                                     // 16-byte chunks per row
     constexpr int A_BYTES = ((L == 0) ? 128 : NK * RR) * RBYTES;
     constexpr int DMA = A_BYTES / 1024 / NW;  // activation DMAs per wave per K tile
-    extern __shared__ __attribute__((aligned(1024))) uint8_t mm_lds[];  // 2 x A_BYTES
+    // mm_lds: 2 x A_BYTES (+ the fp32 form's partial sums)
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // this wave's LDS activation region (row group or K part), row group,
@@ -1199,23 +1300,31 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
     const int wn = (L == 1) ? wave : (L == 4) ? (wave & 3) : (wave & 1);
     // K tiles [kb, ke) of this workgroup (its split, or all of K), in NK
     // parts of kh tiles; this wave's part starts at kofs
-    const int kb = SK ? static_cast<int>(blockIdx.z) * p.kps : 0;
-    const int ke = SK ? min(p.Kt, kb + p.kps) : p.Kt;
+    const int kb = SK ? bz * p.kps : kb_in;
+    const int ke = SK ? min(p.Kt, kb + p.kps) : ke_in;
     const int kh = (ke - kb + NK - 1) / NK;
     const int kofs = kb + ks * kh;
-    const int z = SK ? 0 : blockIdx.z;
+    const int z = SK ? 0 : bz;
     int m0, m_end;
     const uint8_t* qw;
     const uint16_t* sc;
     const uint32_t* zs;
     if constexpr (GR) {
         int e;
-        if (!resolve_group<BM>(p, blockIdx.y, e, m0, m_end)) return;  // uniform per workgroup
+        if (!resolve_group<BM>(p, by, e, m0, m_end)) return;  // uniform per workgroup
         qw = p.qws[e];
         sc = static_cast<const uint16_t*>(p.scs[e]);
         zs = p.zss[e];
+        if constexpr (PK) {
+            // after an earlier tile's stores these table loads are vector
+            // loads; their (uniform) results go back to scalar registers,
+            // where the buffer descriptors need them
+            qw = uniform_ptr(qw);
+            sc = uniform_ptr(sc);
+            zs = uniform_ptr(zs);
+        }
     } else {
-        m0 = blockIdx.y * BM;
+        m0 = by * BM;
         m_end = p.M;
         qw = p.qw + z * p.qw_bs;
         sc = static_cast<const uint16_t*>(p.scales) + z * p.s_bs;
@@ -1254,7 +1363,7 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
     // a tile's loads take no vector address arithmetic (and a read past a
     // resource's extent returns zero instead of faulting).
     constexpr int ES = F32 ? 4 : 2;  // scale bytes
-    const int nt0 = min(static_cast<int>(blockIdx.x) * WN * MM_CT + wn * MM_CT, p.Nt - 1);
+    const int nt0 = min(bx * WN * MM_CT + wn * MM_CT, p.Nt - 1);
     int dnt[MM_CT];
 #pragma unroll
     for (int c = 0; c < MM_CT; ++c) dnt[c] = min(nt0 + c, p.Nt - 1) - nt0;
@@ -1599,12 +1708,25 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
     }
 
     // D element r of block (i, c): row 64*wm + 16*i + 4*(lane >> 4) + r,
-    // column of tile (blockIdx.x*8 + 4*wn + c), lane & 15
+    // column of tile (bx*WN*MM_CT + MM_CT*wn + c), lane & 15
+    if constexpr (PK) {
+        if (pk_slot >= 0) {
+            // a K segment of a split tile: its partial sums in register
+            // order (coalesced), every row of the tile
+            f32x4_t* const W = reinterpret_cast<f32x4_t*>(p.ws) + static_cast<int64_t>(pk_slot) * kPkTileVecs +
+                               wn * RB * MM_CT * 64 + lane;
+#pragma unroll
+            for (int i = 0; i < RB; ++i)
+#pragma unroll
+                for (int c = 0; c < MM_CT; ++c) W[(i * MM_CT + c) * 64] = acc[i][c];
+            return;
+        }
+    }
     if constexpr (SK) {
-        float* const W = p.ws + static_cast<int64_t>(blockIdx.z) * p.M * p.N;
+        float* const W = p.ws + static_cast<int64_t>(bz) * p.M * p.N;
 #pragma unroll
         for (int c = 0; c < MM_CT; ++c) {
-            const int nt = static_cast<int>(blockIdx.x) * WN * MM_CT + wn * MM_CT + c;
+            const int nt = bx * WN * MM_CT + wn * MM_CT + c;
             const int cn = nt * kW4TileN + col;
             if (nt >= p.Nt || cn >= p.N) continue;
 #pragma unroll
@@ -1617,28 +1739,14 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
         }
         return;
     }
-    uint16_t* C = static_cast<uint16_t*>(p.C) + (GR ? 0 : z * p.c_bs);
-    if constexpr (SWI) {
-        // blocks (c, c + 1) hold a gate tile and its up tile (nt even)
-#pragma unroll
-        for (int c = 0; c < MM_CT; c += 2) {
-            const int nt = static_cast<int>(blockIdx.x) * WN * MM_CT + wn * MM_CT + c;
-            const int cn = (nt >> 1) * kW4TileN + col;
-            if (nt >= p.Nt || cn >= p.N) continue;
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int row = m0 + wm * 64 + i * 16 + 4 * (lane >> 4) + r;
-                    if (row < m_end)
-                        C[static_cast<int64_t>(row) * p.N + cn] = f32_to_bf16(swiglu(acc[i][c][r], acc[i][c + 1][r]));
-                }
-        }
+    if constexpr (!F32) {
+        store_bf16_block<SWI, RB>(p, static_cast<uint16_t*>(p.C) + (GR ? 0 : z * p.c_bs), acc,
+                                  bx * WN * MM_CT + wn * MM_CT, m0 + wm * 64, m_end, lane);
         return;
     }
 #pragma unroll
     for (int c = 0; c < MM_CT; ++c) {
-        const int nt = static_cast<int>(blockIdx.x) * WN * MM_CT + wn * MM_CT + c;
+        const int nt = bx * WN * MM_CT + wn * MM_CT + c;
         const int cn = nt * kW4TileN + col;
         if (nt >= p.Nt || cn >= p.N) continue;
 #pragma unroll
@@ -1646,11 +1754,136 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = m0 + wm * 64 + i * 16 + 4 * (lane >> 4) + r;
-                if (row >= m_end) continue;
-                // F32: the reference's alpha / beta epilogue on fp32 C
-                if constexpr (F32) w4_store<true>(p, z * p.c_bs + static_cast<int64_t>(row) * p.N + cn, acc[i][c][r]);
-                else C[static_cast<int64_t>(row) * p.N + cn] = f32_to_bf16(acc[i][c][r]);
+                // the reference's alpha / beta epilogue on fp32 C
+                if (row < m_end) w4_store<true>(p, z * p.c_bs + static_cast<int64_t>(row) * p.N + cn, acc[i][c][r]);
             }
+    }
+}
+
+// The tile kernel: one output tile per workgroup (grid: column groups x row
+// tiles x batch or K splits), or with PK a persistent grouped launch.
+//
+// PK: gridDim.x workers (two per CU, all resident) share the T = X * Y
+// tiles of a ragged grouped launch, X column groups of 256 and Y row tiles
+// of 64 (counted from the device-side group table), tile t to worker t % P.
+// Where the tiles do not fill one round (T < P) and leave at least a quarter
+// of the workers idle, they are spread evenly along K instead (stream-K):
+// their T * Kt K tiles form one range cut into Ps equal parts (at least 4 K
+// tiles each), and each worker runs its part tile by tile -- a whole tile
+// writes its output, a K segment of a tile writes fp32 partial sums to
+// workspace slot (worker + tile), and w4_pk_fixup_kernel, next on the
+// stream, adds each split tile's segments in K order (deterministic) and
+// writes the output.  Measured on MI355X (us; one-workgroup-per-tile grid /
+// persistent, whole tiles / persistent, split): config 4's grouped GEMM
+// (1,120 tiles, K = 4096) 197.7 / 183.2 / 182.4, its SwiGLU gate / up launch
+// (2,240 tiles) 349.9 / 342.2 / 347.8, its down projection (320 tiles, K =
+// 14336) 199.9 / 195.8 / 185.4: with whole rounds to run, the split's
+// partial sums and fixup cost what balancing the last round saves.
+template <int BPS, bool GBIG, bool GR, bool SWI, int L, bool SK = false, int RB = 4, bool F32 = false, bool PK = false>
+__global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_kernel(W4Args p) {
+    extern __shared__ __attribute__((aligned(1024))) uint8_t mm_lds[];
+    if constexpr (!PK) {
+        mma_tile<BPS, GBIG, GR, SWI, L, SK, RB, F32, false>(p, mm_lds, blockIdx.x, blockIdx.y, blockIdx.z, 0, p.Kt,
+                                                             -1);
+    } else {
+        const PkPlan pl = pk_plan(p, gridDim.x);
+        const int w = blockIdx.x;
+        // Tile coordinates pass through readfirstlane: they are uniform, and
+        // the buffer descriptors built from them must sit in scalar
+        // registers (a value the compiler cannot prove uniform puts every
+        // buffer load of the K loop in a waterfall loop).
+        auto uni = [](int64_t v) { return __builtin_amdgcn_readfirstlane(static_cast<int>(v)); };
+        bool first = true;
+        // a barrier between tiles: the next tile's first DMA overwrites LDS
+        // that other waves may still read for the last one
+        for (int64_t t = w; t < pl.dp_tiles; t += gridDim.x) {
+            if (!first) __syncthreads();
+            first = false;
+            mma_tile<BPS, GBIG, GR, SWI, L, SK, RB, F32, true>(p, mm_lds, uni(t % pl.X), uni(t / pl.X), 0, 0, p.Kt,
+                                                                -1);
+        }
+        if (!pl.sk || w >= pl.Ps) return;
+        int64_t lo = w * pl.I / pl.Ps;
+        const int64_t hi = (w + 1) * pl.I / pl.Ps;
+        while (lo < hi) {
+            const int64_t tr = lo / p.Kt;  // split tile, counted from the first one
+            const int k0 = uni(lo - tr * p.Kt);
+            const int k1 = uni(min<int64_t>(p.Kt, k0 + (hi - lo)));
+            const int64_t t = pl.dp_tiles + tr;
+            if (!first) __syncthreads();
+            first = false;
+            mma_tile<BPS, GBIG, GR, SWI, L, SK, RB, F32, true>(p, mm_lds, uni(t % pl.X), uni(t / pl.X), 0, k0, k1,
+                                                                uni((k0 == 0 && k1 == p.Kt) ? -1 : w + tr));
+            lo += k1 - k0;
+        }
+    }
+}
+
+// The split tiles of a persistent grouped launch (w4_mma_kernel with PK,
+// same W4Args, p.pk_workers = its grid): split tile tr's K segments are
+// the partial sums of workers wa..wb in slots wa + tr .. wb + tr, added in
+// that (K) order and written as the tile kernel writes a tile.  Workgroup
+// 4 tr + qn takes column quarter qn of the tile (the 16 KiB a slot holds for
+// wave qn): thread t holds lane t & 63 of column tile t >> 6 at row blocks
+// 0..3, or with SWI the gate / up pair (2 (t >> 6 & 1), + 1) at row blocks
+// 2 (t >> 7) and + 1; each segment's loads are issued four segments at a
+// time before they are added.
+template <bool SWI>
+__global__ __launch_bounds__(256) void w4_pk_fixup_kernel(W4Args p) {
+    const PkPlan pl = pk_plan(p, p.pk_workers);
+    const int64_t tr = blockIdx.x >> 2;
+    const int qn = blockIdx.x & 3;
+    if (!pl.sk || tr >= pl.R) return;
+    const int wa = pk_worker_of(tr * p.Kt, pl), wb = pk_worker_of((tr + 1) * p.Kt - 1, pl);
+    if (wa == wb) return;  // one worker ran the whole tile
+    const int64_t t = pl.dp_tiles + tr;
+    int e, m0, m_end;
+    if (!resolve_group<64>(p, static_cast<int>(t / pl.X), e, m0, m_end)) return;
+    const int lane = threadIdx.x & 63, cp = threadIdx.x >> 6;
+    // this thread's four (row block, column tile) accumulators
+    int ib[4], cb[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        ib[k] = SWI ? 2 * (cp >> 1) + (k >> 1) : k;
+        cb[k] = SWI ? 2 * (cp & 1) + (k & 1) : cp;
+    }
+    const f32x4_t* const W = reinterpret_cast<const f32x4_t*>(p.ws) + qn * 4 * MM_CT * 64 + lane;
+    f32x4_t acc[4];
+    for (int w0 = wa; w0 <= wb; w0 += 4) {
+        f32x4_t v[4][4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const f32x4_t* const S = W + (min(w0 + u, wb) + tr) * kPkTileVecs;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[u][k] = S[(ib[k] * MM_CT + cb[k]) * 64];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            if (w0 + u > wb) break;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if (w0 + u == wa) acc[k] = v[u][k];
+                else
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[k][r] += v[u][k][r];
+            }
+        }
+    }
+    uint16_t* const C = static_cast<uint16_t*>(p.C);
+    const int nt0 = static_cast<int>(t % pl.X) * 4 * MM_CT + qn * MM_CT;
+    const int col = lane & 15;
+#pragma unroll
+    for (int k = 0; k < 4; k += SWI ? 2 : 1) {
+        const int nt = nt0 + cb[k];
+        const int cn = (SWI ? (nt >> 1) : nt) * kW4TileN + col;
+        if (nt >= p.Nt || cn >= p.N) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int row = m0 + ib[k] * 16 + 4 * (lane >> 4) + r;
+            if (row >= m_end) continue;
+            if constexpr (SWI) C[static_cast<int64_t>(row) * p.N + cn] = f32_to_bf16(swiglu(acc[k][r], acc[k + 1][r]));
+            else C[static_cast<int64_t>(row) * p.N + cn] = f32_to_bf16(acc[k][r]);
+        }
     }
 }
 
@@ -2117,17 +2350,41 @@ W4Args make_args(const void* A, const uint8_t* qw, const void* sc, const uint32_
     return a;
 }
 
-// Ragged grouped launch (device-side group table).  SWI: N is the
-// intermediate width I, the weights hold 2 ceil(I/16) interleaved gate / up
-// column tiles, and C is act [rows, I].
+// Workers of a persistent grouped launch: two 64 x 256 tile workgroups per
+// CU (the tile kernel's occupancy), all resident at once.
+int pk_workers() { return 2 * std::max(device_cus(), 1); }
+
+// Tiles a persistent grouped launch can leave over: R < min(P, T), with T
+// at most X (ceil(rows / 64) + live groups).
+int64_t pk_max_left(const W4Args& a, int64_t P) {
+    const int64_t X = ceil_div(a.Nt, 4 * MM_CT);
+    const int64_t t_max = X * (ceil_div64(a.row_capacity, 64) + std::min(a.num_groups, a.row_capacity));
+    return std::min(t_max, P - 1);
+}
+
+// The persistent grouped launch (w4_mma_kernel with PK) and its fixup, with
+// ws_slots 64 KiB partial-sum slots at ws.
 template <bool SWI>
-int grouped_w4(const char* who, const uint16_t* A, const int32_t* offsets, const uint8_t* const* qweights,
-               const uint16_t* const* scales, const uint32_t* const* zeros, uint16_t* C, int num_groups,
-               int row_capacity, int N, int K, int G, void* stream) {
-    if (int st = check_w4_shape(who, row_capacity, N, K, G)) return st;
-    LHQ_REQUIRE(num_groups >= 0, "%s: negative num_groups", who);
-    LHQ_REQUIRE(offsets && qweights && scales && zeros && C && (A || row_capacity == 0), "%s: null pointer", who);
-    if (num_groups == 0 || row_capacity == 0) return LHQ_OK;
+int launch_mma_pk(W4Args a, void* ws, int64_t ws_slots, hipStream_t s, const char* who) {
+    constexpr size_t lds = 2 * 64 * kW4TileK * 2;
+    const int P = pk_workers();
+    a.ws = static_cast<float*>(ws);
+    a.pk_slots = ws_slots;
+    a.pk_workers = P;
+    if (a.gmul) w4_mma_kernel<4, true, true, SWI, 1, false, 4, false, true><<<P, 256, lds, s>>>(a);
+    else w4_mma_kernel<4, false, true, SWI, 1, false, 4, false, true><<<P, 256, lds, s>>>(a);
+    if (int st = check_launch(who)) return st;
+    // at most min(P - 1, T) tiles are left over, four workgroups each
+    w4_pk_fixup_kernel<SWI><<<static_cast<unsigned>(4 * std::max<int64_t>(1, pk_max_left(a, P))), 256, 0, s>>>(a);
+    return check_launch(who);
+}
+
+// The grouped launch's arguments (SWI: N is the intermediate width I, the
+// weights hold 2 ceil(I/16) interleaved gate / up column tiles).
+template <bool SWI>
+W4Args grouped_args(const uint16_t* A, const int32_t* offsets, const uint8_t* const* qweights,
+                    const uint16_t* const* scales, const uint32_t* const* zeros, uint16_t* C, int num_groups,
+                    int row_capacity, int N, int K, int G) {
     W4Args a = make_args(A, nullptr, nullptr, nullptr, C, row_capacity, N, K, G, 1.0f, 0.0f);
     if constexpr (SWI) a.Nt = 2 * ceil_div(N, kW4TileN);
     a.offsets = offsets;
@@ -2136,11 +2393,43 @@ int grouped_w4(const char* who, const uint16_t* A, const int32_t* offsets, const
     a.zss = zeros;
     a.num_groups = num_groups;
     a.row_capacity = row_capacity;
+    return a;
+}
+bool grouped_uses_tiles(const W4Args& a) {
+    return mma_applies(a, a.row_capacity, static_cast<double>(a.row_capacity) / a.num_groups);
+}
+
+// Partial-sum slots a persistent grouped launch can use: the stream-K part
+// of Ps <= P workers over R < min(P, T) tiles touches slots up to
+// (Ps - 1) + (R - 1), with T at most X (ceil(rows / 64) + live groups).
+int64_t grouped_pk_slots(const W4Args& a) {
+    const int64_t P = pk_workers();
+    return P + pk_max_left(a, P) - 1;
+}
+
+// Ragged grouped launch (device-side group table); ws / ws_bytes: the
+// persistent launch's workspace (none: one workgroup per tile).
+template <bool SWI>
+int grouped_w4(const char* who, const uint16_t* A, const int32_t* offsets, const uint8_t* const* qweights,
+               const uint16_t* const* scales, const uint32_t* const* zeros, uint16_t* C, int num_groups,
+               int row_capacity, int N, int K, int G, void* ws, int64_t ws_bytes, void* stream) {
+    if (int st = check_w4_shape(who, row_capacity, N, K, G)) return st;
+    LHQ_REQUIRE(num_groups >= 0, "%s: negative num_groups", who);
+    LHQ_REQUIRE(offsets && qweights && scales && zeros && C && (A || row_capacity == 0), "%s: null pointer", who);
+    LHQ_REQUIRE(ws_bytes >= 0, "%s: negative workspace_bytes", who);
+    if (num_groups == 0 || row_capacity == 0) return LHQ_OK;
+    const W4Args a =
+        grouped_args<SWI>(A, offsets, qweights, scales, zeros, C, num_groups, row_capacity, N, K, G);
     // at most min(num_groups, row_capacity) groups hold rows, so
     // sum_e ceil(rows_e / B) <= ceil(row_capacity / B) + live_groups for row blocks of B
     const int live_groups = std::min(num_groups, row_capacity);
-    if (mma_applies(a, row_capacity, static_cast<double>(row_capacity) / num_groups))
+    if (grouped_uses_tiles(a)) {
+        if (ws && ws_bytes >= kPkSlotBytes) {
+            LHQ_REQUIRE((reinterpret_cast<uintptr_t>(ws) & 15) == 0, "%s: workspace not 16-byte aligned", who);
+            return launch_mma_pk<SWI>(a, ws, ws_bytes / kPkSlotBytes, as_stream(stream), who);
+        }
         return launch_mma<true, SWI>(a, row_capacity, live_groups, 1, as_stream(stream), who);
+    }
     const int64_t mblocks = ceil_div64(row_capacity, 16) + live_groups;
     LHQ_SUPPORTED(mblocks <= 65535, "%s: %lld row blocks exceed the grid limit", who, static_cast<long long>(mblocks));
     return launch_w4<false, true, false, true, SWI>(a, 1, as_stream(stream), static_cast<int>(mblocks));
@@ -2465,14 +2754,49 @@ int lhq_gemm_w4a16_bf16_grouped(const uint16_t* A, const int32_t* offsets, const
                                 const uint16_t* const* scales, const uint32_t* const* zeros, uint16_t* C,
                                 int num_groups, int row_capacity, int N, int K, int G, void* stream) {
     return grouped_w4<false>("gemm_w4a16_bf16_grouped", A, offsets, qweights, scales, zeros, C, num_groups,
-                             row_capacity, N, K, G, stream);
+                             row_capacity, N, K, G, nullptr, 0, stream);
 }
 
 int lhq_gemm_w4a16_bf16_grouped_swiglu(const uint16_t* A, const int32_t* offsets, const uint8_t* const* qweights,
                                        const uint16_t* const* scales, const uint32_t* const* zeros, uint16_t* act,
                                        int num_groups, int row_capacity, int I, int K, int G, void* stream) {
     return grouped_w4<true>("gemm_w4a16_bf16_grouped_swiglu", A, offsets, qweights, scales, zeros, act,
-                            num_groups, row_capacity, I, K, G, stream);
+                            num_groups, row_capacity, I, K, G, nullptr, 0, stream);
+}
+
+int64_t lhq_gemm_w4a16_bf16_grouped_workspace_bytes(int num_groups, int row_capacity, int N, int K, int G) {
+    if (check_w4_shape("gemm_w4a16_bf16_grouped_workspace_bytes", row_capacity, N, K, G) || num_groups <= 0 ||
+        row_capacity == 0)
+        return 0;
+    const W4Args a = grouped_args<false>(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, num_groups,
+                                         row_capacity, N, K, G);
+    return grouped_uses_tiles(a) ? grouped_pk_slots(a) * kPkSlotBytes : 0;
+}
+
+int64_t lhq_gemm_w4a16_bf16_grouped_swiglu_workspace_bytes(int num_groups, int row_capacity, int I, int K, int G) {
+    if (check_w4_shape("gemm_w4a16_bf16_grouped_swiglu_workspace_bytes", row_capacity, I, K, G) ||
+        num_groups <= 0 || row_capacity == 0)
+        return 0;
+    const W4Args a = grouped_args<true>(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, num_groups,
+                                        row_capacity, I, K, G);
+    return grouped_uses_tiles(a) ? grouped_pk_slots(a) * kPkSlotBytes : 0;
+}
+
+int lhq_gemm_w4a16_bf16_grouped_ws(const uint16_t* A, const int32_t* offsets, const uint8_t* const* qweights,
+                                   const uint16_t* const* scales, const uint32_t* const* zeros, uint16_t* C,
+                                   int num_groups, int row_capacity, int N, int K, int G, void* workspace,
+                                   int64_t workspace_bytes, void* stream) {
+    return grouped_w4<false>("gemm_w4a16_bf16_grouped_ws", A, offsets, qweights, scales, zeros, C, num_groups,
+                             row_capacity, N, K, G, workspace, workspace ? workspace_bytes : 0, stream);
+}
+
+int lhq_gemm_w4a16_bf16_grouped_swiglu_ws(const uint16_t* A, const int32_t* offsets,
+                                          const uint8_t* const* qweights, const uint16_t* const* scales,
+                                          const uint32_t* const* zeros, uint16_t* act, int num_groups,
+                                          int row_capacity, int I, int K, int G, void* workspace,
+                                          int64_t workspace_bytes, void* stream) {
+    return grouped_w4<true>("gemm_w4a16_bf16_grouped_swiglu_ws", A, offsets, qweights, scales, zeros, act,
+                            num_groups, row_capacity, I, K, G, workspace, workspace ? workspace_bytes : 0, stream);
 }
 
 }  // extern "C"

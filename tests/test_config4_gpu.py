@@ -9,7 +9,9 @@ launches of the quantized expert MLP around it (moe.cpp:150-196):
   by column tile, act = bf16(silu(A Wg) * (A Wu)));
 * the down projection, K = 14336, N = 4096.
 
-The GPU computes every output element.  The weights are random codes, fp16
+The grouped launches run both ways: without a workspace (one workgroup per
+tile) and with one (the persistent launch that splits its left-over tiles
+along K).  The GPU computes every output element.  The weights are random codes, fp16
 scales and zero points (a GEMM does not care how they were made).  A sample
 of rows x columns is checked against the oracle run on the same codes
 sliced to those columns (the int4 format is per column, so the slice is
@@ -69,9 +71,17 @@ def _check(oracle, got, want):
     assert (np.abs(got - want_b) <= np.abs(want_b) * 2.0 ** -7 + 1e-30).mean() > 0.99
 
 
-def _grouped_launch(oracle, ops, K, N, seed):
-    """One grouped launch of lhq_gemm_w4a16_bf16_grouped over config 4's
-    routing; returns (A, off, per-expert codes, full output)."""
+def _workspace(ops, name, *dims):
+    import torch
+    n = getattr(ops.lib().cdll, name)(*dims)
+    assert n > 0
+    return torch.empty(n, dtype=torch.uint8, device="cuda"), n
+
+
+def _grouped_launch(oracle, ops, K, N, seed, ws=False):
+    """One grouped launch of lhq_gemm_w4a16_bf16_grouped (ws: the persistent
+    lhq_gemm_w4a16_bf16_grouped_ws) over config 4's routing; returns (A,
+    off, per-expert codes, full output)."""
     import torch
     g = D.rng(seed)
     off, tok = _routing(oracle, seed)
@@ -82,17 +92,22 @@ def _grouped_launch(oracle, ops, K, N, seed):
     q, s, z = ops.pointer_tables(Ws)
     rows = A.shape[0]
     C = ops.zeros((rows, N), np.int16)
-    print(f"config 4 grouped launch K={K} N={N} rows={rows}", flush=True)
-    ops.run("lhq_gemm_w4a16_bf16_grouped", A, off, q, s, z, C, E, rows, N, K, G)
+    print(f"config 4 grouped launch K={K} N={N} rows={rows} ws={ws}", flush=True)
+    if ws:
+        buf, n = _workspace(ops, "lhq_gemm_w4a16_bf16_grouped_workspace_bytes", E, rows, N, K, G)
+        ops.run("lhq_gemm_w4a16_bf16_grouped_ws", A, off, q, s, z, C, E, rows, N, K, G, buf, n)
+    else:
+        ops.run("lhq_gemm_w4a16_bf16_grouped", A, off, q, s, z, C, E, rows, N, K, G)
     out = ops.host(C, np.uint16)
     del Ws, q, s, z, C
     torch.cuda.empty_cache()
     return g, A, off, codes, out
 
 
+@pytest.mark.parametrize("ws", [False, True], ids=["grid", "persistent"])
 @pytest.mark.parametrize("K,N", [(4096, 14336), (14336, 4096)], ids=["gate_shape", "down_shape"])
-def test_config4_grouped_full_size(oracle, ops, K, N):
-    g, A, off, codes, out = _grouped_launch(oracle, ops, K, N, seed=40 + K // 4096)
+def test_config4_grouped_full_size(oracle, ops, K, N, ws):
+    g, A, off, codes, out = _grouped_launch(oracle, ops, K, N, seed=40 + K // 4096, ws=ws)
     rows, cols = _sample(g, off, N)
     got, want = [], []
     for r in rows:
@@ -104,7 +119,8 @@ def test_config4_grouped_full_size(oracle, ops, K, N):
     _check(oracle, np.array(got), np.array(want))
 
 
-def test_config4_swiglu_gate_up_full_size(oracle, ops):
+@pytest.mark.parametrize("ws", [False, True], ids=["grid", "persistent"])
+def test_config4_swiglu_gate_up_full_size(oracle, ops, ws):
     import torch
     H, I = 4096, 14336
     g = D.rng(47)
@@ -122,8 +138,12 @@ def test_config4_swiglu_gate_up_full_size(oracle, ops):
     q, s, z = ops.pointer_tables(gu)
     rows = A.shape[0]
     act = ops.zeros((rows, I), np.int16)
-    print(f"config 4 SwiGLU gate/up launch H={H} I={I} rows={rows}", flush=True)
-    ops.run("lhq_gemm_w4a16_bf16_grouped_swiglu", A, off, q, s, z, act, E, rows, I, H, G)
+    print(f"config 4 SwiGLU gate/up launch H={H} I={I} rows={rows} ws={ws}", flush=True)
+    if ws:
+        buf, n = _workspace(ops, "lhq_gemm_w4a16_bf16_grouped_swiglu_workspace_bytes", E, rows, I, H, G)
+        ops.run("lhq_gemm_w4a16_bf16_grouped_swiglu_ws", A, off, q, s, z, act, E, rows, I, H, G, buf, n)
+    else:
+        ops.run("lhq_gemm_w4a16_bf16_grouped_swiglu", A, off, q, s, z, act, E, rows, I, H, G)
     out = ops.host(act, np.uint16)
     del gu, q, s, z, act
     torch.cuda.empty_cache()
