@@ -234,10 +234,12 @@ int lhq_gemm_w4a16_bf16_grouped_swiglu(const uint16_t* A, const int32_t* offsets
  * writes it.  Results match the calls without a workspace within fp32
  * reassociation (bit for bit where nothing is split).
  * lhq_gemm_w4a16_bf16_grouped[_swiglu]_workspace_bytes gives the bytes the
- * split can use for a table of num_groups groups over row_capacity rows (0:
- * the shape runs no tile kernel).  A smaller workspace (at least 64 KiB)
- * still takes the persistent launch and splits only when the segments fit;
- * NULL or less runs the launch without one.
+ * call can use for a table of num_groups groups over row_capacity rows: 0
+ * where the shape runs no tile kernel, 64 KiB where the tile count's bound
+ * from row_capacity rules the split out, up to ~56 MiB on MI355X otherwise.
+ * A smaller workspace (at least 64 KiB) still takes the persistent launch
+ * and splits only when the segments fit; NULL or less runs the launch
+ * without one.
  * workspace: device memory, 16-byte aligned, any contents, not shared with
  * a call running concurrently (calls in order on one stream may share it). */
 int64_t lhq_gemm_w4a16_bf16_grouped_workspace_bytes(int num_groups, int row_capacity, int N, int K,

@@ -2354,12 +2354,10 @@ W4Args make_args(const void* A, const uint8_t* qw, const void* sc, const uint32_
 // CU (the tile kernel's occupancy), all resident at once.
 int pk_workers() { return 2 * std::max(device_cus(), 1); }
 
-// Tiles a persistent grouped launch can leave over: R < min(P, T), with T
-// at most X (ceil(rows / 64) + live groups).
-int64_t pk_max_left(const W4Args& a, int64_t P) {
+// Tiles of a grouped launch at most: X (ceil(rows / 64) + live groups).
+int64_t pk_max_tiles(const W4Args& a) {
     const int64_t X = ceil_div(a.Nt, 4 * MM_CT);
-    const int64_t t_max = X * (ceil_div64(a.row_capacity, 64) + std::min(a.num_groups, a.row_capacity));
-    return std::min(t_max, P - 1);
+    return X * (ceil_div64(a.row_capacity, 64) + std::min(a.num_groups, a.row_capacity));
 }
 
 // The persistent grouped launch (w4_mma_kernel with PK) and its fixup, with
@@ -2368,14 +2366,20 @@ template <bool SWI>
 int launch_mma_pk(W4Args a, void* ws, int64_t ws_slots, hipStream_t s, const char* who) {
     constexpr size_t lds = 2 * 64 * kW4TileK * 2;
     const int P = pk_workers();
+    // The split needs T <= 3P/4; T is counted on the device, but its bound
+    // from row_capacity tells when no table can give a split, and then no
+    // slot is offered and the fixup kernel (~4 us for nothing) not launched.
+    const int64_t t_max = pk_max_tiles(a);
+    const bool may_split = 4 * t_max <= 3 * static_cast<int64_t>(P);
     a.ws = static_cast<float*>(ws);
-    a.pk_slots = ws_slots;
+    a.pk_slots = may_split ? ws_slots : 0;
     a.pk_workers = P;
     if (a.gmul) w4_mma_kernel<4, true, true, SWI, 1, false, 4, false, true><<<P, 256, lds, s>>>(a);
     else w4_mma_kernel<4, false, true, SWI, 1, false, 4, false, true><<<P, 256, lds, s>>>(a);
     if (int st = check_launch(who)) return st;
-    // at most min(P - 1, T) tiles are left over, four workgroups each
-    w4_pk_fixup_kernel<SWI><<<static_cast<unsigned>(4 * std::max<int64_t>(1, pk_max_left(a, P))), 256, 0, s>>>(a);
+    if (!may_split) return LHQ_OK;
+    // four workgroups per split tile (every tile when the split runs)
+    w4_pk_fixup_kernel<SWI><<<static_cast<unsigned>(4 * std::max<int64_t>(1, t_max)), 256, 0, s>>>(a);
     return check_launch(who);
 }
 
@@ -2399,12 +2403,12 @@ bool grouped_uses_tiles(const W4Args& a) {
     return mma_applies(a, a.row_capacity, static_cast<double>(a.row_capacity) / a.num_groups);
 }
 
-// Partial-sum slots a persistent grouped launch can use: the stream-K part
-// of Ps <= P workers over R < min(P, T) tiles touches slots up to
-// (Ps - 1) + (R - 1), with T at most X (ceil(rows / 64) + live groups).
+// Partial-sum slots a persistent grouped launch can use: a split of R = T
+// <= 3P/4 tiles over Ps <= P workers touches slots up to (Ps - 1) + (R - 1);
+// none where the tile bound rules the split out.
 int64_t grouped_pk_slots(const W4Args& a) {
-    const int64_t P = pk_workers();
-    return P + pk_max_left(a, P) - 1;
+    const int64_t P = pk_workers(), t_max = pk_max_tiles(a);
+    return 4 * t_max <= 3 * P ? P + t_max - 1 : 0;
 }
 
 // Ragged grouped launch (device-side group table); ws / ws_bytes: the
@@ -2770,7 +2774,7 @@ int64_t lhq_gemm_w4a16_bf16_grouped_workspace_bytes(int num_groups, int row_capa
         return 0;
     const W4Args a = grouped_args<false>(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, num_groups,
                                          row_capacity, N, K, G);
-    return grouped_uses_tiles(a) ? grouped_pk_slots(a) * kPkSlotBytes : 0;
+    return grouped_uses_tiles(a) ? std::max<int64_t>(1, grouped_pk_slots(a)) * kPkSlotBytes : 0;
 }
 
 int64_t lhq_gemm_w4a16_bf16_grouped_swiglu_workspace_bytes(int num_groups, int row_capacity, int I, int K, int G) {
@@ -2779,7 +2783,7 @@ int64_t lhq_gemm_w4a16_bf16_grouped_swiglu_workspace_bytes(int num_groups, int r
         return 0;
     const W4Args a = grouped_args<true>(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, num_groups,
                                         row_capacity, I, K, G);
-    return grouped_uses_tiles(a) ? grouped_pk_slots(a) * kPkSlotBytes : 0;
+    return grouped_uses_tiles(a) ? std::max<int64_t>(1, grouped_pk_slots(a)) * kPkSlotBytes : 0;
 }
 
 int lhq_gemm_w4a16_bf16_grouped_ws(const uint16_t* A, const int32_t* offsets, const uint8_t* const* qweights,

@@ -47,7 +47,7 @@ def _plan(rows_per_group, Nt, Kt, slots):
     T = X * sum(-(-r // 64) for r in rows_per_group)
     q, R = divmod(T, P)
     Ps = min(P, max(1, R * Kt // 4))
-    sk = q == 0 and R > 0 and 4 * R <= 3 * P and Ps + R - 1 <= slots
+    sk = q == 0 and R > 0 and 4 * R <= 3 * P and Ps + R - 1 <= slots  # slots: 1 where T_max rules it out
     return T, q, R, sk
 
 
@@ -228,9 +228,13 @@ def test_grouped_workspace_bytes(ops):
     L = ops.lib().cdll
     # a few rows per group: the 16-row kernel, no workspace
     assert L.lhq_gemm_w4a16_bf16_grouped_workspace_bytes(8, 16, 4096, 4096, 128) == 0
-    # the tile kernel: P + min(T_max, P - 1) - 1 slots, T_max = X (ceil(rows / 64) + live groups)
+    # the tile kernel: P + T_max - 1 slots, T_max = X (ceil(rows / 64) + live groups), where
+    # T_max <= 3P/4 allows a split; one slot (the persistent launch alone) otherwise
     assert L.lhq_gemm_w4a16_bf16_grouped_workspace_bytes(8, 1024, 256, 4096, 128) == (P + 24 - 1) * SLOT
-    assert L.lhq_gemm_w4a16_bf16_grouped_workspace_bytes(8, 1024, 14336, 4096, 128) == (2 * P - 2) * SLOT
+    assert L.lhq_gemm_w4a16_bf16_grouped_workspace_bytes(8, 1024, 14336, 4096, 128) == SLOT
+    # config 4's down projection: T_max = 16 x 24 = 384 = 3P/4 at P = 512
+    if P == 512:
+        assert L.lhq_gemm_w4a16_bf16_grouped_workspace_bytes(8, 1024, 4096, 14336, 128) == (P + 384 - 1) * SLOT
     # the SwiGLU form counts 2 ceil(I / 16) column tiles
     assert (L.lhq_gemm_w4a16_bf16_grouped_swiglu_workspace_bytes(8, 1024, 200, 4096, 128)
             == (P + 2 * 24 - 1) * SLOT)
