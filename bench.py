@@ -350,7 +350,7 @@ def bench_moe(ops, steps, warmup, seed=0, T=512, E=8, topk=2, K=4096, N=14336, G
     res = {"tokens": T, "experts": E, "top_k": topk, "rows": rows, "rows_per_expert": counts.tolist(),
            "K": K, "N": N, "G": G, "us_per_call": us, "tflops": flops / (us * 1e-6) / 1e12,
            "gbs": byts / (us * 1e-6) / 1e9, "flops": flops, "bytes": byts,
-           "launch": "persistent, left-over tiles split along K (lhq_gemm_w4a16_bf16_grouped_ws)",
+           "launch": "persistent tile scheduler (lhq_gemm_w4a16_bf16_grouped_ws; split along K below one round)",
            "workspace_bytes": ws_bytes, "us_per_call_grid": ms_grid * 1e3 / steps}
     res["mfma_frac"] = res["tflops"] / BF16_PEAK_TFLOPS
     res["hbm_frac"] = res["gbs"] / HBM_PEAK_GBS
