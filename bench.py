@@ -211,10 +211,13 @@ def make_w4_sets(ops, K: int, N: int, G: int, nsets: int, seed: int):
     return sets
 
 
-def bench_w4a16_f32(ops, M, K, N, G, steps, warmup, seed=0, min_rotate_bytes=2 * INFINITY_CACHE_BYTES + (1 << 26)):
+def bench_w4a16_f32(ops, M, K, N, G, steps, warmup, seed=0, min_rotate_bytes=2 * INFINITY_CACHE_BYTES + (1 << 26),
+                    workspace=False):
     """The reference interface (lhq_gemm_w4a16, gemm_quant.cpp:54-82): fp32
     activations and output, symmetric int4 weights with fp32 group scales,
     alpha = 1, beta = 0; timed over rotating weight sets like the bf16 legs.
+    workspace: through lhq_gemm_w4a16_ws with the workspace the shape asks
+    for (K split across workgroups at thin grids; the lh:: drop-in's route).
     Bytes: K*N/2 codes + (K/G)*N*4 scales + M*K*4 + M*N*4."""
     import numpy as np
     import torch
@@ -230,24 +233,31 @@ def bench_w4a16_f32(ops, M, K, N, G, steps, warmup, seed=0, min_rotate_bytes=2 *
         del packed, sc
     A = [torch.randn((M, K), generator=gen, device="cuda") for _ in range(nsets)]
     C = [torch.zeros((M, N), device="cuda") for _ in range(nsets)]
-    fn = ops.lib().cdll.lhq_gemm_w4a16
+    L = ops.lib().cdll
+    ws_bytes = L.lhq_gemm_w4a16_workspace_bytes(M, N, K, G) if workspace else 0
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device="cuda")
 
     def launch(i):
         j = i % nsets
-        st = fn(A[j].data_ptr(), sets[j].qweight.data_ptr(), sets[j].scales.data_ptr(), C[j].data_ptr(),
-                M, N, K, G, 1.0, 0.0, ops.stream())
+        if workspace:
+            st = L.lhq_gemm_w4a16_ws(A[j].data_ptr(), sets[j].qweight.data_ptr(), sets[j].scales.data_ptr(),
+                                     C[j].data_ptr(), M, N, K, G, 1.0, 0.0, ws.data_ptr(), ws_bytes, ops.stream())
+        else:
+            st = L.lhq_gemm_w4a16(A[j].data_ptr(), sets[j].qweight.data_ptr(), sets[j].scales.data_ptr(),
+                                  C[j].data_ptr(), M, N, K, G, 1.0, 0.0, ops.stream())
         if st:
             raise RuntimeError(f"lhq_gemm_w4a16: {ops.lib().last_error()}")
 
     timer = GraphTimer(launch, nsets, chunk=nsets * max(1, 64 // nsets))
     ms, _ = timer.time(steps, warmup)
     us = ms * 1e3 / steps
-    res = {"leg": "w4a16_f32_interface", "M": M, "K": K, "N": N, "G": G, "entry": "lhq_gemm_w4a16",
+    res = {"leg": "w4a16_f32_interface", "M": M, "K": K, "N": N, "G": G,
+           "entry": "lhq_gemm_w4a16_ws" if workspace else "lhq_gemm_w4a16", "workspace_bytes": ws_bytes,
            "us_per_call": round(us, 2), "gbs": round(per / (us * 1e-6) / 1e9, 1),
            "hbm_frac": round(per / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
            "tflops": round(2.0 * M * K * N / (us * 1e-6) / 1e12, 1),
            "mfma_frac": round(2.0 * M * K * N / (us * 1e-6) / 1e12 / BF16_PEAK_TFLOPS, 4)}
-    del timer, sets, A, C
+    del timer, sets, A, C, ws
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     return res
@@ -1063,12 +1073,18 @@ def main() -> int:
         return 0
     if args.only == "f32":
         # the reference interface: decode shapes on the integer decode and
-        # 16-row kernels, prefill shapes on the tile kernel
-        for m, k, n, st in ((1, 8192, 28672, 500), (16, 8192, 28672, 200), (256, 8192, 8192, 100),
-                            (1024, 8192, 8192, 40), (4096, 8192, 8192, 20)):
-            r = bench_w4a16_f32(ops, m, k, n, G, st, max(3, st // 10))
-            log(f"w4a16 fp32 interface M={m} K={k} N={n}: {r['us_per_call']:.1f} us  {r['gbs']:.0f} GB/s "
-                f"({100 * r['hbm_frac']:.1f}% HBM)  {r['tflops']:.0f} TFLOPS ({100 * r['mfma_frac']:.1f}% bf16)")
+        # 16-row kernels, prefill shapes on the tile kernel; thin shapes also
+        # through the workspace entry point (K split across workgroups, the
+        # lh:: drop-in's route)
+        for m, k, n, st, ws in ((1, 8192, 28672, 500, False), (16, 8192, 28672, 200, False),
+                                (16, 8192, 28672, 200, True), (4, 8192, 28672, 200, True),
+                                (64, 8192, 8192, 200, True), (64, 8192, 8192, 100, False),
+                                (256, 8192, 8192, 100, False), (1024, 8192, 8192, 40, False),
+                                (4096, 8192, 8192, 20, False)):
+            r = bench_w4a16_f32(ops, m, k, n, G, st, max(3, st // 10), workspace=ws)
+            log(f"w4a16 fp32 interface M={m} K={k} N={n} ({r['entry']}): {r['us_per_call']:.1f} us  "
+                f"{r['gbs']:.0f} GB/s ({100 * r['hbm_frac']:.1f}% HBM)  {r['tflops']:.0f} TFLOPS "
+                f"({100 * r['mfma_frac']:.1f}% bf16)")
             print(json.dumps(r), flush=True)
         return 0
     if args.only == "configs":

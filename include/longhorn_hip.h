@@ -157,6 +157,22 @@ int lhq_b8_prepack(const uint8_t* B, int K, int N, uint8_t* Bt, void* stream);
 int lhq_gemm_w4a16(const float* A, const uint8_t* qweight, const float* scales,
                    float* C, int M, int N, int K, int group_size, float alpha, float beta,
                    void* stream);
+/* lhq_gemm_w4a16 with a caller workspace (no reference counterpart: the
+ * reference's CPU loop needs no partial sums; the lh:: drop-in of
+ * gemm_w4a16_groupwise passes one).  At 2..64 rows (group_size a multiple
+ * of 128, K % 128 == 0) K is split across workgroups: each split writes fp32
+ * partial sums to `workspace`, and a second kernel adds them in split order
+ * and applies alpha / beta as lhq_gemm_w4a16 does (deterministic).  The
+ * split count is the most the workspace allows, up to
+ * lhq_gemm_w4a16_workspace_bytes for the shape (0: no split); with a NULL or
+ * smaller workspace the call runs with fewer splits or as lhq_gemm_w4a16.
+ * workspace: device memory, 16-byte aligned, any contents, not shared with a
+ * call running concurrently.  Results match lhq_gemm_w4a16 within fp32
+ * reassociation. */
+int64_t lhq_gemm_w4a16_workspace_bytes(int M, int N, int K, int group_size);
+int lhq_gemm_w4a16_ws(const float* A, const uint8_t* qweight, const float* scales, float* C,
+                      int M, int N, int K, int group_size, float alpha, float beta,
+                      void* workspace, int64_t workspace_bytes, void* stream);
 /* Benchmark configs 2/5: bf16 A [M,K]; asymmetric W4 (fp16 scales, u4
  * zeros) prepacked by lhq_w4_prepack_asym; bf16 C [M,N] = A@W, fp32 accumulate. */
 int lhq_gemm_w4a16_bf16(const uint16_t* A, const uint8_t* qweight, const uint16_t* scales,

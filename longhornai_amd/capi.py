@@ -54,6 +54,8 @@ SIGNATURES = {
     "lhq_b8_prepack": [_p, _i, _i, _p, _p],
     "lhq_gemm_w4a16": [_p, _p, _p, _p, _i, _i, _i, _i, _f, _f, _p],
     "lhq_gemm_w4a16_bf16": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
+    "lhq_gemm_w4a16_workspace_bytes": [_i, _i, _i, _i],
+    "lhq_gemm_w4a16_ws": [_p, _p, _p, _p, _i, _i, _i, _i, _f, _f, _p, _i64, _p],
     "lhq_gemm_w4a16_bf16_workspace_bytes": [_i, _i, _i, _i],
     "lhq_gemm_w4a16_bf16_ws": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p, _i64, _p],
     "lhq_gemm_w4a16_bf16_noalloc": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _p],
@@ -102,6 +104,7 @@ _RESTYPES = {
     "lhq_w4_scales_bytes": _i64,
     "lhq_w4_zeros_bytes": _i64,
     "lhq_b8_prepacked_bytes": _i64,
+    "lhq_gemm_w4a16_workspace_bytes": _i64,
     "lhq_gemm_w4a16_bf16_workspace_bytes": _i64,
     "lhq_gemm_w4a16_bf16_grouped_workspace_bytes": _i64,
     "lhq_gemm_w4a16_bf16_grouped_swiglu_workspace_bytes": _i64,

@@ -110,8 +110,11 @@ void gemm_w4a16_groupwise(const float* A, const uint8_t* B_packed, const float* 
         dev::check(lhq_w4_prepack_sym(dP.as<uint8_t>(), dS.as<float>(), K, N, G, qw.as<uint8_t>(), qs.as<float>(),
                                       dev::stream()),
                    "gemm_w4a16_groupwise (prepack)");
-        dev::check(lhq_gemm_w4a16(dA.as<float>(), qw.as<uint8_t>(), qs.as<float>(), dC.as<float>(), M, N, K, G, alpha,
-                                  beta, dev::stream()),
+        // thin grids split K across workgroups over a workspace
+        const int64_t ws_bytes = lhq_gemm_w4a16_workspace_bytes(M, N, K, G);
+        Buffer ws(ws_bytes > 0 ? static_cast<size_t>(ws_bytes) : 16);
+        dev::check(lhq_gemm_w4a16_ws(dA.as<float>(), qw.as<uint8_t>(), qs.as<float>(), dC.as<float>(), M, N, K, G,
+                                     alpha, beta, ws.as<void>(), ws_bytes > 0 ? ws_bytes : 0, dev::stream()),
                    "gemm_w4a16_groupwise");
     } else {
         // group sizes the MFMA segmentation cannot express (not 32, 64 or a

@@ -1277,7 +1277,7 @@ __device__ __forceinline__ void mma_tile(const W4Args& p, uint8_t* mm_lds, int b
     static_assert(!SK || (!GR && !SWI), "split-K on plain launches only");
     static_assert(!PK || (GR && L == 1 && RB == 4 && !SK && !F32), "persistent launches: grouped 64 x 256 tiles");
     static_assert(L != 4 || SK, "the 8-wave 64 x 256 layout on split-K launches only");
-    static_assert(!F32 || (!GR && !SWI && !SK && L != 0 && L != 4 && (RB == 4 ? L == 1 : true)),
+    static_assert(!F32 || (!GR && !SWI && L != 0 && L != 4 && (RB == 4 ? L == 1 : true)),
                   "the fp32 interface: plain launches, 64 x 256 tiles or 16- / 32-row blocks");
     constexpr int SEGS = 4 / BPS;
     constexpr int NW = (L >= 3) ? 8 : 4;                                  // waves
@@ -1913,6 +1913,35 @@ __global__ void w4_splitk_reduce_kernel(const float* __restrict__ ws, uint16_t* 
     }
     if constexpr (VEC) *reinterpret_cast<u32x2_t*>(C + i) = u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
     else C[i] = f32_to_bf16(v);
+}
+
+// The fp32 interface's split-K sum: C[i] = alpha * (sum over s < S of
+// ws[s][i], in split order), then the reference's beta (beta == 0 never
+// reads C, gemm_quant.cpp:12-21), as w4_store<true> does for an unsplit
+// tile.  Four consecutive elements per thread where 4 | MN.
+template <bool VEC>
+__global__ void w4_splitk_reduce_f32_kernel(const float* __restrict__ ws, float* __restrict__ C, int64_t mn, int S,
+                                            float alpha, float beta) {
+    constexpr int U = 8;
+    using V = std::conditional_t<VEC, f32x4_t, float>;
+    const int64_t i = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) * (VEC ? 4 : 1);
+    if (i >= mn) return;
+    V v{};
+    for (int s0 = 0; s0 < S; s0 += U) {
+        V w[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u)  // splits past S re-read the last one (not added)
+            w[u] = *reinterpret_cast<const V*>(ws + static_cast<int64_t>(min(s0 + u, S - 1)) * mn + i);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (s0 + u >= S) break;
+            if (s0 + u == 0) v = w[u];
+            else v += w[u];
+        }
+    }
+    V out = alpha * v;
+    if (beta != 0.0f) out = beta * *reinterpret_cast<const V*>(C + i) + out;
+    *reinterpret_cast<V*>(C + i) = out;
 }
 
 // ---------------------------------------------------------------------------
@@ -2613,6 +2642,123 @@ int launch_split(W4Args a, const TilePlan& t, void* ws, hipStream_t s, const cha
     return check_launch(who);
 }
 
+// ---------------------------------------------------------------------------
+// The fp32 interface (gemm_quant.hpp:47-57) at thin grids: K split across
+// workgroups over a caller workspace (lhq_gemm_w4a16_ws).  The tile kernel's
+// fp32 form with 16-, 32- or 64-row blocks writes each split's fp32 partial
+// sums to ws[s][M][N], and w4_splitk_reduce_f32_kernel adds them in split
+// order and applies the reference's alpha / beta (deterministic).
+// ---------------------------------------------------------------------------
+template <int L, int RB>
+void launch_split_f32_rb(const W4Args& a, unsigned splits, hipStream_t s) {
+    constexpr int NW = L >= 3 ? 8 : 4, NK = L == 2 ? 2 : L == 3 ? 4 : 1, WN = L == 1 ? 4 : 2;
+    constexpr size_t a_bytes = static_cast<size_t>(NK) * 16 * RB * kW4TileK * 4;
+    constexpr int UPW = 4 * RB / (NW / NK), PS = UPW >= 4 ? 1 : 4 / UPW;
+    constexpr size_t lds = 2 * a_bytes + static_cast<size_t>(NK) * RB * PS * 64 * 16;  // tiles, partial sums
+    const dim3 grid(ceil_div(a.Nt, WN * MM_CT), ceil_div(a.M, 16 * RB), splits);
+    if (a.gmul) {
+        allow_cu_lds<&w4_mma_kernel<4, true, false, false, L, true, RB, true>>();
+        w4_mma_kernel<4, true, false, false, L, true, RB, true><<<grid, 64 * NW, lds, s>>>(a);
+    } else {
+        allow_cu_lds<&w4_mma_kernel<4, false, false, false, L, true, RB, true>>();
+        w4_mma_kernel<4, false, false, false, L, true, RB, true><<<grid, 64 * NW, lds, s>>>(a);
+    }
+}
+
+// ws_cap: the workspace bytes available (-1: as much as the plan wants).
+// 16-, 32- or 64-row blocks (RB = 1, 2, 4) on 256-column workgroups (L = 1)
+// and S splits that bring the grid to about two workgroups per CU, each
+// walking at least 4 K tiles.  Measured on MI355X (us, lhq_gemm_w4a16 /
+// this split): M = 16, K = 8192, N = 28672 48.6 / 36.4; M = 16, K = 28672,
+// N = 8192 88.7 / 40.8; M = 4, N = 28672 43.8 / 34.0; M = 32, N = 28672
+// 70.7 / 55.3; M = 64, K = N = 8192 181 / 35.3; M = 48, K = N = 4096 91.5 /
+// 22.8 (the unsplit 64-row tile leaves the chip nearly empty from 17 rows
+// on); M = 8, K = 4096, N = 11008 17.4 / 14.8.  K halves or quarters
+// inside the workgroup (L = 2, 3) with splits were within noise or slower
+// (M = 16, K = N = 8192: 17.6-18.8 against 18.6).  It is not used at 2..16
+// rows with K * N below 32 Mi, where the unsplit kernels win or tie (M = 2,
+// K = N = 4096: 5.5 / 12.1; M = 8: 11.7 / 12.5; M = 16: 13.0 / 12.9).
+TilePlan plan_thin_f32(const W4Args& a, int64_t ws_cap) {
+    TilePlan t;
+    // (read on every call in a tuning build, so one process can sweep them)
+    const int env_on = tuning_knob("LHQ_W4_F32_SPLIT", -1);  // 0: never split, 1: split wherever allowed
+    const int env_s = tuning_knob("LHQ_W4_F32_SPLIT_S", 0);  // force the split count
+    const int env_l = tuning_knob("LHQ_W4_F32_SPLIT_L", 0);  // force the layout (1..3)
+    if (env_on == 0 || a.M < 2 || a.M > 64) return t;
+    if (a.G < kW4TileK || a.K % kW4TileK != 0 || static_cast<int64_t>(a.M) * a.K >= (int64_t{1} << 31)) return t;
+    if (env_on != 1 && a.M <= 16 && static_cast<int64_t>(a.K) * a.N < (int64_t{32} << 20)) return t;
+    t.RB = a.M <= 16 ? 1 : a.M <= 32 ? 2 : 4;
+    t.L = 1;
+#ifdef LHQ_TUNING_KNOBS
+    if (env_l >= 1 && env_l <= 3 && (t.RB < 4 || env_l == 1)) t.L = env_l;
+#else
+    (void)env_l;
+#endif
+    const int WN = t.L == 1 ? 4 : 2, per_cu = t.L >= 3 ? 1 : 2;
+    const int64_t wgs = static_cast<int64_t>(ceil_div(a.Nt, WN * MM_CT)) * ceil_div(a.M, 16 * t.RB);
+    const int cus = std::max(device_cus(), 1);
+    // about one round of the resident workgroups, at least 4 K tiles each
+    int S = static_cast<int>(std::min<int64_t>(std::max<int64_t>(1, per_cu * cus / wgs), a.Kt / kSplitMinKt));
+    if (env_s >= 1) S = std::min(env_s, a.Kt);
+    const int64_t per_split = static_cast<int64_t>(a.M) * a.N * 4;
+    if (ws_cap >= 0) S = static_cast<int>(std::min<int64_t>(S, std::max<int64_t>(1, ws_cap / per_split)));
+    const int kps = ceil_div(a.Kt, std::max(S, 1));
+    S = ceil_div(a.Kt, kps);
+    if (S <= 1) return t;
+    t.split = true;
+    t.S = S;
+    t.kps = kps;
+    t.ws_bytes = S * per_split;
+    return t;
+}
+
+int launch_split_f32(W4Args a, const TilePlan& t, void* ws, hipStream_t s, const char* who) {
+    a.ws = static_cast<float*>(ws);
+    a.kps = t.kps;
+    const unsigned S = static_cast<unsigned>(t.S);
+#ifdef LHQ_TUNING_KNOBS
+    if (t.L == 3 && t.RB < 4) t.RB == 1 ? launch_split_f32_rb<3, 1>(a, S, s) : launch_split_f32_rb<3, 2>(a, S, s);
+    else if (t.L == 2 && t.RB < 4) t.RB == 1 ? launch_split_f32_rb<2, 1>(a, S, s) : launch_split_f32_rb<2, 2>(a, S, s);
+    else
+#endif
+    if (t.RB == 4) launch_split_f32_rb<1, 4>(a, S, s);
+    else t.RB == 1 ? launch_split_f32_rb<1, 1>(a, S, s) : launch_split_f32_rb<1, 2>(a, S, s);
+    if (int st = check_launch(who)) return st;
+    const int64_t mn = static_cast<int64_t>(a.M) * a.N;
+    const bool vec = mn % 4 == 0 && (reinterpret_cast<uintptr_t>(a.C) & 15) == 0;
+    const unsigned blocks = static_cast<unsigned>(ceil_div64(vec ? mn / 4 : mn, 256));
+    float* const C = static_cast<float*>(a.C);
+    if (vec) w4_splitk_reduce_f32_kernel<true><<<blocks, 256, 0, s>>>(a.ws, C, mn, t.S, a.alpha, a.beta);
+    else w4_splitk_reduce_f32_kernel<false><<<blocks, 256, 0, s>>>(a.ws, C, mn, t.S, a.alpha, a.beta);
+    return check_launch(who);
+}
+
+// lhq_gemm_w4a16 with a workspace of ws_cap bytes at ws (0: none).
+int gemm_w4a16_f32(const char* who, const float* A, const uint8_t* qweight, const float* scales, float* C, int M,
+                   int N, int K, int G, float alpha, float beta, void* ws, int64_t ws_cap, void* stream) {
+    if (int st = check_w4_shape(who, M, N, K, G)) return st;
+    LHQ_REQUIRE(qweight && scales && C && (A || M == 0), "%s: null pointer", who);
+    LHQ_REQUIRE(ws || ws_cap <= 0, "%s: null workspace with %lld bytes", who, static_cast<long long>(ws_cap));
+    if (M == 0) return LHQ_OK;
+    W4Args a = make_args(A, qweight, scales, nullptr, C, M, N, K, G, alpha, beta);
+    if (ws_cap > 0) {
+        const TilePlan t = plan_thin_f32(a, ws_cap);
+        if (t.split) {
+            LHQ_REQUIRE((reinterpret_cast<uintptr_t>(ws) & 15) == 0, "%s: workspace not 16-byte aligned", who);
+            return launch_split_f32(a, t, ws, as_stream(stream), who);
+        }
+    }
+    const int thin = f32_thin_layout(a, M);
+    if (!thin && mma_applies(a, M, M)) return launch_mma_f32(a, as_stream(stream), who);
+    if (thin == 2) return M <= 16 ? launch_mma_f32_rb<2, 1>(a, as_stream(stream), who)
+                                  : launch_mma_f32_rb<2, 2>(a, as_stream(stream), who);
+    if (thin == 3) return M <= 16 ? launch_mma_f32_rb<3, 1>(a, as_stream(stream), who)
+                                  : launch_mma_f32_rb<3, 2>(a, as_stream(stream), who);
+    if (thin == 1) return M <= 16 ? launch_mma_f32_rb<1, 1>(a, as_stream(stream), who)
+                                  : launch_mma_f32_rb<1, 2>(a, as_stream(stream), who);
+    return launch_w4<true, false, true>(a, 1, as_stream(stream));
+}
+
 // lhq_gemm_w4a16_bf16 with a workspace of ws_bytes at ws (ws_cap < 0: the
 // plan may use as much as it wants, the caller has checked that it fits).
 int gemm_w4a16_bf16_plan(const char* who, const uint16_t* A, const uint8_t* qweight, const uint16_t* scales,
@@ -2681,20 +2827,20 @@ extern "C" {
 
 int lhq_gemm_w4a16(const float* A, const uint8_t* qweight, const float* scales, float* C, int M,
                    int N, int K, int G, float alpha, float beta, void* stream) {
-    if (int st = check_w4_shape("gemm_w4a16", M, N, K, G)) return st;
-    LHQ_REQUIRE(qweight && scales && C && (A || M == 0), "gemm_w4a16: null pointer");
-    if (M == 0) return LHQ_OK;
-    W4Args a = make_args(A, qweight, scales, nullptr, C, M, N, K, G, alpha, beta);
-    const char* who = "w4a16 prefill (fp32)";
-    const int thin = f32_thin_layout(a, M);
-    if (!thin && mma_applies(a, M, M)) return launch_mma_f32(a, as_stream(stream), who);
-    if (thin == 2) return M <= 16 ? launch_mma_f32_rb<2, 1>(a, as_stream(stream), who)
-                                  : launch_mma_f32_rb<2, 2>(a, as_stream(stream), who);
-    if (thin == 3) return M <= 16 ? launch_mma_f32_rb<3, 1>(a, as_stream(stream), who)
-                                  : launch_mma_f32_rb<3, 2>(a, as_stream(stream), who);
-    if (thin == 1) return M <= 16 ? launch_mma_f32_rb<1, 1>(a, as_stream(stream), who)
-                                  : launch_mma_f32_rb<1, 2>(a, as_stream(stream), who);
-    return launch_w4<true, false, true>(a, 1, as_stream(stream));
+    return gemm_w4a16_f32("gemm_w4a16", A, qweight, scales, C, M, N, K, G, alpha, beta, nullptr, 0, stream);
+}
+
+int64_t lhq_gemm_w4a16_workspace_bytes(int M, int N, int K, int G) {
+    if (check_w4_shape("gemm_w4a16_workspace_bytes", M, N, K, G) || M == 0) return 0;
+    const W4Args a = make_args(nullptr, nullptr, nullptr, nullptr, nullptr, M, N, K, G, 1.0f, 0.0f);
+    return plan_thin_f32(a, -1).ws_bytes;
+}
+
+int lhq_gemm_w4a16_ws(const float* A, const uint8_t* qweight, const float* scales, float* C, int M, int N, int K,
+                      int G, float alpha, float beta, void* workspace, int64_t workspace_bytes, void* stream) {
+    LHQ_REQUIRE(workspace_bytes >= 0, "gemm_w4a16_ws: negative workspace_bytes");
+    return gemm_w4a16_f32("gemm_w4a16_ws", A, qweight, scales, C, M, N, K, G, alpha, beta, workspace,
+                          workspace ? workspace_bytes : 0, stream);
 }
 
 int lhq_gemm_w4a16_bf16(const uint16_t* A, const uint8_t* qweight, const uint16_t* scales,
