@@ -74,11 +74,42 @@ FAKE = C.c_void_p(0x1000)  # never dereferenced: validation fails first
     ("lhq_gemm_w4a16_bf16_batched", (FAKE, FAKE, FAKE, FAKE, FAKE, 70000, 1, 64, 128, 128, None),
      capi.LHQ_ERR_INVALID),
     ("lhq_gemm_f32", (FAKE, FAKE, FAKE, -1, 4, 4, 1.0, 0.0, None), capi.LHQ_ERR_INVALID),
+    # the workspace entry points check their arguments before anything is launched
+    ("lhq_gemm_w4a16_ws", (None, FAKE, FAKE, FAKE, 16, 64, 128, 128, 1.0, 0.0, FAKE, 1024, None),
+     capi.LHQ_ERR_INVALID),
+    ("lhq_gemm_w4a16_ws", (FAKE, FAKE, FAKE, FAKE, 16, 64, 128, 128, 1.0, 0.0, FAKE, -1, None),
+     capi.LHQ_ERR_INVALID),
+    ("lhq_gemm_w4a16_ws", (FAKE, FAKE, FAKE, FAKE, 16, 64, 96, 96, 1.0, 0.0, FAKE, 1024, None),
+     capi.LHQ_ERR_UNSUPPORTED),
+    ("lhq_gemm_w4a16_bf16_grouped_ws", (FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 8, 1024, 256, 4096, 128, FAKE, -1,
+                                        None), capi.LHQ_ERR_INVALID),
+    ("lhq_gemm_w4a16_bf16_grouped_ws", (FAKE, None, FAKE, FAKE, FAKE, FAKE, 8, 1024, 256, 4096, 128, FAKE, 65536,
+                                        None), capi.LHQ_ERR_INVALID),
+    ("lhq_gemm_w4a16_bf16_grouped_swiglu_ws", (FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, -2, 1024, 256, 4096, 128, FAKE,
+                                               65536, None), capi.LHQ_ERR_INVALID),
+    ("lhq_moe_expert_mlp_w4a16_bf16_ws", (FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 8, 1024, 4096,
+                                          14336, 128, FAKE, -1, None), capi.LHQ_ERR_INVALID),
 ])
 def test_host_validation(L, name, args, code):
     st = L.status(name, *args)
     assert st == code, (st, L.last_error())
     assert L.last_error()
+
+
+def test_workspace_queries_on_the_host(L):
+    """The workspace-size queries are host functions: shapes that never split
+    ask for nothing, whatever the device."""
+    f32 = L.cdll.lhq_gemm_w4a16_workspace_bytes
+    assert f32(1, 28672, 8192, 128) == 0       # one row
+    assert f32(65, 8192, 8192, 128) == 0       # beyond 64 rows
+    assert f32(16, 4096, 4096, 128) == 0       # 2..16 rows with K * N < 32 Mi
+    assert f32(32, 8192, 8192, 64) == 0        # G < 128
+    assert f32(16, 8192, 8192, 48) == 0        # a group size the GEMMs reject
+    g = L.cdll.lhq_gemm_w4a16_bf16_grouped_workspace_bytes
+    assert g(8, 16, 4096, 4096, 128) == 0      # two rows per group: no tile kernel
+    assert g(0, 1024, 4096, 4096, 128) == 0
+    assert g(8, 1024, 4096, 4096, 64) == 0     # G < 128
+    assert g(8, 1024, 4096, 4096, 128) % 65536 == 0
 
 
 def test_empty_problems_are_noops(L):
