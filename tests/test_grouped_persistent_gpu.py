@@ -294,3 +294,52 @@ def test_expert_mlp_ws_matches_oracle(oracle, ops):
     assert rel_frobenius(D.bf16_bits_to_f32(ops.host(y2, np.uint16)), y_h) <= TOL_BF16
     del dn, gu
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("rows,K,N", [
+    ([123, 115, 133, 136, 114, 147, 134, 122], 2048, 256),    # split along K: tile kernel + fixup
+    ([512] * 8, 256, 2048),                                   # one round of whole tiles
+])
+def test_grouped_persistent_in_a_captured_hip_graph(oracle, ops, rows, K, N):
+    """The persistent launch (and its fixup) allocates nothing and records no
+    memset, so it can be captured: a graph of one call is replayed three
+    times with new activations written into its input and the output
+    cleared eagerly between replays; each replay equals the eager call on
+    the same input bit for bit."""
+    import torch
+    c = Case(oracle, ops, rows, K, N, 128, seed=77)
+    n = c.workspace_bytes(ops)
+    ws = _workspace(ops, n)
+    A = ops.dev(c.A)
+    off = ops.dev(c.off)
+    q, s, z = c.tables
+    C = ops.zeros((c.rows, N), np.int16)
+    E = len(rows)
+    L = ops.lib().cdll
+
+    def call():
+        st = L.lhq_gemm_w4a16_bf16_grouped_ws(A.data_ptr(), off.data_ptr(), q.data_ptr(), s.data_ptr(),
+                                              z.data_ptr(), C.data_ptr(), E, c.rows, N, K, 128, ws.data_ptr(), n,
+                                              ops.stream())
+        assert st == 0, ops.lib().last_error()
+
+    call()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        with torch.cuda.graph(g, stream=st):
+            call()
+    torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        A.copy_(ops.dev(D.to_bf16_bits(oracle, D.rng(200 + rep).standard_normal((c.rows, K)).astype(np.float32))))
+        C.zero_()
+        call()
+        want = ops.host(C, np.uint16).copy()
+        C.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        print(f"grouped graph replay {rep}", flush=True)
+        assert np.array_equal(ops.host(C, np.uint16), want), f"replay {rep}"

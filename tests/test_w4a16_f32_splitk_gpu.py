@@ -118,3 +118,45 @@ def test_f32_splitk_workspace_bytes_rules(ops):
     if torch.cuda.get_device_properties(0).multi_processor_count == 256:
         assert f(16, 8192, 28672, 128) == 4 * 16 * 28672 * 4
         assert f(64, 8192, 8192, 128) == 16 * 64 * 8192 * 4   # 32 groups, 16 splits of 4 K tiles
+
+
+def test_f32_splitk_in_a_captured_hip_graph(oracle, ops):
+    """The split (tile kernel + reduce) allocates nothing and records no
+    memset: a captured call replayed three times with new activations, C
+    reset eagerly between replays (beta = 0.5 reads it), equals the eager
+    call bit for bit each time."""
+    import torch
+    M, K, N, G = 16, 8192, 4096, 128
+    A, w, C0, _ = _case(oracle, ops, M, K, N, G, seed=2500, alpha=1.5, beta=0.5)
+    n = _ws_bytes(ops, M, K, N, G)
+    assert n > 0
+    ws = torch.empty(n, dtype=torch.uint8, device="cuda")
+    C = ops.dev(C0)
+    C0d = ops.dev(C0)
+    L = ops.lib().cdll
+
+    def call():
+        st = L.lhq_gemm_w4a16_ws(A.data_ptr(), w.qweight.data_ptr(), w.scales.data_ptr(), C.data_ptr(), M, N, K,
+                                 G, 1.5, 0.5, ws.data_ptr(), n, ops.stream())
+        assert st == 0, ops.lib().last_error()
+
+    call()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        with torch.cuda.graph(g, stream=st):
+            call()
+    torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        A.copy_(ops.dev(D.uniform((M, K), -1, 1, 2600 + rep)))
+        C.copy_(C0d)
+        call()
+        want = ops.host(C).copy()
+        C.copy_(C0d)
+        g.replay()
+        torch.cuda.synchronize()
+        print(f"fp32 split graph replay {rep}", flush=True)
+        assert np.array_equal(ops.host(C).view(np.uint32), want.view(np.uint32)), f"replay {rep}"
