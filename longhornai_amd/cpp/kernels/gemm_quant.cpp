@@ -7,6 +7,7 @@
 // launches the kernel and copies C back.
 #include "kernels/gemm_quant.hpp"
 
+#include <algorithm>
 #include <cmath>
 
 #include "kernels/device.hpp"
@@ -111,10 +112,11 @@ void gemm_w4a16_groupwise(const float* A, const uint8_t* B_packed, const float* 
                                       dev::stream()),
                    "gemm_w4a16_groupwise (prepack)");
         // thin grids split K across workgroups over a workspace
-        const int64_t ws_bytes = lhq_gemm_w4a16_workspace_bytes(M, N, K, G);
-        Buffer ws(ws_bytes > 0 ? static_cast<size_t>(ws_bytes) : 16);
+        // (a zero-byte Buffer holds no allocation: the call then runs unsplit)
+        const int64_t ws_bytes = std::max<int64_t>(0, lhq_gemm_w4a16_workspace_bytes(M, N, K, G));
+        Buffer ws(static_cast<size_t>(ws_bytes));
         dev::check(lhq_gemm_w4a16_ws(dA.as<float>(), qw.as<uint8_t>(), qs.as<float>(), dC.as<float>(), M, N, K, G,
-                                     alpha, beta, ws.as<void>(), ws_bytes > 0 ? ws_bytes : 0, dev::stream()),
+                                     alpha, beta, ws.get(), ws_bytes, dev::stream()),
                    "gemm_w4a16_groupwise");
     } else {
         // group sizes the MFMA segmentation cannot express (not 32, 64 or a
