@@ -1760,6 +1760,303 @@ __device__ __forceinline__ void mma_tile(const W4Args& p, uint8_t* mm_lds, int b
     }
 }
 
+// ---------------------------------------------------------------------------
+// The 64 x 256 bf16 tile on the 32x32x16 MFMA (W32: layout 1, 64-row blocks,
+// bf16 activations and output; plain, batched, grouped, SwiGLU and the
+// persistent grouped launches).  Same loads, LDS layout and K loop as
+// mma_tile; what changes is the matrix work per K tile and wave (64 rows x
+// 64 columns x 128 k):
+//   - the products run as 32 MFMAs of 32x32x16 instead of 64 of 16x16x32.
+//     Each MFMA issue takes the SIMD's issue port for about 8 cycles
+//     whatever its size, so the 32-cycle form leaves room for ~6 VALU
+//     instructions (the weight decode and group corrections) per MFMA where
+//     the 16-cycle form leaves ~2: measured with register operands, two
+//     waves per SIMD, chains of MFMAs with n VALU instructions between them:
+//     16x16x32 17.6 / 27.1 / 35.2 cycles per MFMA at n = 0 / 4 / 6,
+//     32x32x16 32.5 / 33.6 / 35.2 / 44.6 at n = 0 / 4 / 6 / 8;
+//   - the activation sums xs = -144 * sum_k x seeding the chains are made
+//     once per workgroup, each wave the 16 rows 16 * wave.. on the
+//     16x16x32 MFMA (4 MFMAs against the -144 operand), and handed to every
+//     wave through 256 bytes of LDS (a barrier between the VALU phase and the
+//     matrix phase), where the 16x16 form has every wave sum all 64 rows;
+//   - the wave's four column tiles nt0 + c form two 32-column blocks: block
+//     cb holds tile cb in lanes with (lane >> 4) & 1 == 0 and tile cb + 2 in
+//     the others, so with SwiGLU's interleaved gate / up tiles block 0 holds
+//     the gates and block 1 the ups of the same two output tiles, in the
+//     same lanes;
+//   - MFMA q = (j, s) (k block j of 32, half s) takes in lane l the row /
+//     column l & 31 of the block and the 8 k at 32 j + 16 s + 8 (l >> 5):
+//     the weight dwords j of the prepacked tile's 16-byte chunk
+//     (l & 15) + 16 (l >> 5) + 32 s, and the activations of LDS chunk
+//     4 j + 2 s + (l >> 5) of row l & 31;
+//   - D element e of block (ib, cb) in lane l: row 32 ib + 8 (e >> 2) +
+//     4 (l >> 5) + (e & 3), column (lane & 15) of the lane's tile; the group
+//     correction acc += s * t uses one scale per lane and block.
+// Everything else (zero point folded into the codes, xs seeding each chain,
+// one correction per group, the two phases at raised priority for the
+// matrix phase, unconditional clamped loads) is as in mma_tile.
+template <bool GBIG, bool GR, bool SWI, bool PK>
+__device__ __forceinline__ void mma_tile32(const W4Args& p, uint8_t* mm_lds, int bx, int by, int bz, int kb, int ke,
+                                           int pk_slot) {
+    constexpr int BPS = 4;
+    constexpr int RBYTES = kW4TileK * 2;          // LDS bytes per activation row
+    constexpr int A_BYTES = 64 * RBYTES;          // one activation buffer
+    constexpr int DMA = A_BYTES / 1024 / 4;       // activation DMAs per wave per K tile
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = lane & 15, h = lane >> 5, u = (lane >> 4) & 1;
+    int m0, m_end;
+    const uint8_t* qw;
+    const uint16_t* sc;
+    const uint32_t* zs;
+    if constexpr (GR) {
+        int e;
+        if (!resolve_group<64>(p, by, e, m0, m_end)) return;  // uniform per workgroup
+        qw = p.qws[e];
+        sc = static_cast<const uint16_t*>(p.scs[e]);
+        zs = p.zss[e];
+        if constexpr (PK) {
+            qw = uniform_ptr(qw);
+            sc = uniform_ptr(sc);
+            zs = uniform_ptr(zs);
+        }
+    } else {
+        m0 = by * 64;
+        m_end = p.M;
+        qw = p.qw + bz * p.qw_bs;
+        sc = static_cast<const uint16_t*>(p.scales) + bz * p.s_bs;
+        zs = p.zeros + bz * p.z_bs;
+    }
+    const uint16_t* A = static_cast<const uint16_t*>(p.A) + (GR ? 0 : bz * p.a_bs);
+    uint32_t a_voff[DMA];  // as in mma_tile: LDS row idx >> 4, slot idx & 15
+#pragma unroll
+    for (int q = 0; q < DMA; ++q) {
+        const int idx = (DMA * wave + q) * 64 + lane;
+        const int r = idx / 16, slot = idx % 16;
+        const int row = min(m0 + r, m_end - 1);
+        a_voff[q] = (static_cast<uint32_t>(row - m0) * static_cast<uint32_t>(p.K) +
+                     static_cast<uint32_t>((slot ^ (r & 15)) * 8)) * 2;
+    }
+    const uint32_t s_half = 16u * (col & 1);
+    const int nt0 = min(bx * 4 * MM_CT + wave * MM_CT, p.Nt - 1);
+    const int nt_left = p.Nt - nt0;
+    auto extent = [](int64_t bytes) {
+        return static_cast<int>(static_cast<uint32_t>(bytes < int64_t{0xFFFFFFFF} ? bytes : int64_t{0xFFFFFFFF}));
+    };
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(qw) + static_cast<int64_t>(nt0) * p.Kt * kW4TileBytes, 0,
+        extent(static_cast<int64_t>(nt_left) * p.Kt * kW4TileBytes), kBufWord3);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(sc) + static_cast<int64_t>(nt0) * p.NG * 16, 0,
+        extent(static_cast<int64_t>(nt_left) * p.NG * 16 * 2), kBufWord3);
+    const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(zs) + static_cast<int64_t>(nt0) * p.NG8 * 16, 0,
+        extent(static_cast<int64_t>(nt_left) * p.NG8 * 16 * 4), kBufWord3);
+    const __amdgpu_buffer_rsrc_t ra_ = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(A) + static_cast<int64_t>(m0) * p.K, 0,
+        extent(static_cast<int64_t>(m_end - m0) * p.K * 2), kBufWord3);
+    // the lane's tile in block cb (tiles past Nt re-read the last one)
+    uint32_t w_voff[2], s_voff[2], z_voff[2];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+        const uint32_t dt = static_cast<uint32_t>(min(nt0 + cb + 2 * u, p.Nt - 1) - nt0);
+        w_voff[cb] = dt * static_cast<uint32_t>(p.Kt) * kW4TileBytes + col * 16 + 256 * h;
+        s_voff[cb] = (dt * static_cast<uint32_t>(p.NG) * 16 + (col & ~1)) * 2;
+        z_voff[cb] = (dt * static_cast<uint32_t>(p.NG8) * 16 + col) * 4;
+    }
+
+    struct Regs {
+        u32x4_t w[2][2];  // block cb, half s
+        uint32_t sw[2];
+        uint32_t zw[2];
+    };
+    auto issue = [&](uint8_t* buf, Regs& R, int kt_in) {
+        const int kt = min(kt_in + kb, p.Kt - 1);
+#pragma unroll
+        for (int q = 0; q < DMA; ++q)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra_, (LHQ_LDS_AS void*)(buf + (DMA * wave + q) * 1024), 16,
+                                                     a_voff[q], kt * kW4TileK * 2, 0, 0);
+        const int g = group_of_c<BPS, GBIG>(kt, 0, p.gmul);
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+            R.zw[cb] = __builtin_amdgcn_raw_buffer_load_b32(rz, z_voff[cb], (g >> 3) * 16 * 4, 0);
+            R.sw[cb] = __builtin_amdgcn_raw_buffer_load_b32(rs, s_voff[cb], g * 16 * 2, 0);
+#pragma unroll
+            for (int s = 0; s < 2; ++s)
+                R.w[cb][s] = __builtin_amdgcn_raw_buffer_load_b128(rw, w_voff[cb] + 512 * s, kt * kW4TileBytes, 0);
+        }
+    };
+
+    f32x16_t acc[2][2];
+#pragma unroll
+    for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[ib][cb][e] = 0.f;
+    const u32x4_t m144 = {kM144Bf16x2, kM144Bf16x2, kM144Bf16x2, kM144Bf16x2};
+    float* const xs_l = reinterpret_cast<float*>(mm_lds + 2 * A_BYTES);  // 64 rows' sums, two tiles
+    // rows past the end read the last row; a tile with no live row (m0 >=
+    // m_end) skips the arithmetic in every wave alike
+    const bool live = m0 < m_end;
+    // The activation sums of a K tile, made before the rendezvous that
+    // opens it: each wave's own DMAs carry its 16 rows (16 * wave..) of every
+    // tile, so once its loads have landed the wave sums them (4 MFMAs against
+    // the -144 operand, 16x16 D layout: rows 4 (lane >> 4) + r, every column
+    // alike) and column 0 writes them to the tile's half of xs_l; the
+    // rendezvous barrier then publishes them to every wave.  Two halves: a
+    // tile's sums are written while the waves may still read the previous
+    // tile's.
+    auto sums = [&](const uint8_t* buf, int kt_in) {
+        // vmcnt(0) (expcnt and lgkmcnt at their maxima), as a builtin so the
+        // compiler's wait counting knows the tile's loads are complete
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        asm volatile("" ::: "memory");
+        if (!live) return;
+        f32x4_t xs = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            xs = mfma_bf16_16x16x32(*reinterpret_cast<const u32x4_t*>(buf + (16 * wave + col) * RBYTES +
+                                                                      (((4 * j + (lane >> 4)) ^ col) * 16)),
+                                    m144, xs);
+        if (col == 0) *reinterpret_cast<f32x4_t*>(xs_l + 64 * (kt_in & 1) + 16 * wave + 4 * (lane >> 4)) = xs;
+    };
+    auto compute = [&](const uint8_t* buf, const Regs& R, int kt_in) {
+        if (!live) return;
+        const int g = group_of_c<BPS, GBIG>(kb + kt_in, 0, p.gmul);
+        const float* const xs_t = xs_l + 64 * (kt_in & 1);
+        uint32_t zb[2];
+        float scs[2];
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+            zb[cb] = __builtin_amdgcn_perm(0u, 16u - ((R.zw[cb] >> (4 * (g & 7))) & 15u), 0u);
+            scs[cb] = f16_to_f32(static_cast<uint16_t>(R.sw[cb] >> s_half));
+        }
+        // activation fragment of row block ib for k step q, read two k
+        // steps ahead of its use
+        auto frag32 = [&](int q, int ib) {
+            const int j = q >> 1, s = q & 1;
+            return *reinterpret_cast<const u32x4_t*>(buf + (32 * ib + (lane & 31)) * RBYTES +
+                                                     (((4 * j + 2 * s + h) ^ col) * 16));
+        };
+        u32x4_t af[3][2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+            for (int ib = 0; ib < 2; ++ib) af[q][ib] = frag32(q, ib);
+        // four chains (ib, cb) seeded with their row block's sums; per k
+        // step q the two weight operands are decoded just before their
+        // MFMAs (the VALU work runs under the 32-cycle MFMAs), and the two
+        // activation fragments serve both column blocks
+        f32x16_t t[2][2];
+#pragma unroll
+        for (int ib = 0; ib < 2; ++ib) {
+#pragma unroll
+            for (int i4 = 0; i4 < 4; ++i4) {
+                const f32x4_t x = *reinterpret_cast<const f32x4_t*>(xs_t + 32 * ib + 8 * i4 + 4 * h);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) t[ib][0][4 * i4 + r] = x[r];
+            }
+            t[ib][1] = t[ib][0];
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int j = q >> 1, s = q & 1;
+            if (q + 2 < 8)
+#pragma unroll
+                for (int ib = 0; ib < 2; ++ib) af[(q + 2) % 3][ib] = frag32(q + 2, ib);
+            u32x4_t bq[2];
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) bq[cb] = w4_operand_z(R.w[cb][s][j], zb[cb]);
+#pragma unroll
+            for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb) t[ib][cb] = mfma_bf16_32x32x16(af[q % 3][ib], bq[cb], t[ib][cb]);
+            // keeps each k step's fragment reads two steps ahead of their use
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[ib][cb][e] = __builtin_fmaf(scs[cb], t[ib][cb][e], acc[ib][cb][e]);
+    };
+    // every wave's loads of the tile have landed (waited in sums), its sums
+    // are in LDS, and every wave is done with the buffers the next loads
+    // overwrite.  0xC07F: lgkmcnt(0), vmcnt and expcnt at their maxima; the
+    // empty asm statements keep the compiler from moving LDS accesses across
+    // the barrier
+    auto rendezvous = [&]() {
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+
+    uint8_t* const buf0 = mm_lds;
+    uint8_t* const buf1 = mm_lds + A_BYTES;
+    const int kh = ke - kb;
+    Regs ra, rb;
+    issue(buf0, ra, 0);
+    sums(buf0, 0);
+    int kt = 0;
+    for (; kt + 2 <= kh; kt += 2) {
+        rendezvous();
+        issue(buf1, rb, kt + 1);
+        compute(buf0, ra, kt);
+        sums(buf1, kt + 1);
+        rendezvous();
+        issue(buf0, ra, kt + 2);  // clamped past the end: never used
+        compute(buf1, rb, kt + 1);
+        if (kt + 2 < kh) sums(buf0, kt + 2);
+    }
+    if (kt < kh) {
+        rendezvous();
+        compute(buf0, ra, kt);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    const int ntw = bx * 4 * MM_CT + wave * MM_CT;  // the wave's first column tile
+    if constexpr (PK) {
+        if (pk_slot >= 0) {
+            // a K segment of a split tile: its partial sums in register
+            // order (f32x4 (ib, cb, e >> 2) of each lane), every row
+            f32x4_t* const W = reinterpret_cast<f32x4_t*>(p.ws) + static_cast<int64_t>(pk_slot) * kPkTileVecs +
+                               wave * 16 * 64 + lane;
+#pragma unroll
+            for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                    for (int i4 = 0; i4 < 4; ++i4)
+                        W[((ib * 2 + cb) * 4 + i4) * 64] =
+                            f32x4_t{acc[ib][cb][4 * i4], acc[ib][cb][4 * i4 + 1], acc[ib][cb][4 * i4 + 2],
+                                    acc[ib][cb][4 * i4 + 3]};
+            return;
+        }
+    }
+    uint16_t* const C = static_cast<uint16_t*>(p.C) + (GR ? 0 : bz * p.c_bs);
+#pragma unroll
+    for (int cb = 0; cb < (SWI ? 1 : 2); ++cb) {
+        // SwiGLU: block 0 holds the gates, block 1 the ups of output tile
+        // ntw / 2 + u
+        const int nt = ntw + cb + 2 * u;
+        const int cn = (SWI ? (ntw >> 1) + u : nt) * kW4TileN + col;
+        if (nt >= p.Nt || cn >= p.N) continue;
+#pragma unroll
+        for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int row = m0 + 32 * ib + 8 * (e >> 2) + 4 * h + (e & 3);
+                if (row >= m_end) continue;
+                if constexpr (SWI)
+                    C[static_cast<int64_t>(row) * p.N + cn] = f32_to_bf16(swiglu(acc[ib][0][e], acc[ib][1][e]));
+                else C[static_cast<int64_t>(row) * p.N + cn] = f32_to_bf16(acc[ib][cb][e]);
+            }
+    }
+}
+
 // The tile kernel: one output tile per workgroup (grid: column groups x row
 // tiles x batch or K splits), or with PK a persistent grouped launch.
 //
@@ -1779,12 +2076,17 @@ __device__ __forceinline__ void mma_tile(const W4Args& p, uint8_t* mm_lds, int b
 // (2,240 tiles) 349.9 / 342.2 / 347.8, its down projection (320 tiles, K =
 // 14336) 199.9 / 195.8 / 185.4: with whole rounds to run, the split's
 // partial sums and fixup cost what balancing the last round saves.
-template <int BPS, bool GBIG, bool GR, bool SWI, int L, bool SK = false, int RB = 4, bool F32 = false, bool PK = false>
+template <int BPS, bool GBIG, bool GR, bool SWI, int L, bool SK = false, int RB = 4, bool F32 = false, bool PK = false,
+          bool W32 = false>
 __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_kernel(W4Args p) {
+    static_assert(!W32 || (BPS == 4 && L == 1 && RB == 4 && !SK && !F32), "the 32x32x16 tile: bf16 64 x 256 tiles");
     extern __shared__ __attribute__((aligned(1024))) uint8_t mm_lds[];
+    auto tile = [&](int bx, int by, int bz, int k0, int k1, int slot) {
+        if constexpr (W32) mma_tile32<GBIG, GR, SWI, PK>(p, mm_lds, bx, by, bz, k0, k1, slot);
+        else mma_tile<BPS, GBIG, GR, SWI, L, SK, RB, F32, PK>(p, mm_lds, bx, by, bz, k0, k1, slot);
+    };
     if constexpr (!PK) {
-        mma_tile<BPS, GBIG, GR, SWI, L, SK, RB, F32, false>(p, mm_lds, blockIdx.x, blockIdx.y, blockIdx.z, 0, p.Kt,
-                                                             -1);
+        tile(blockIdx.x, blockIdx.y, blockIdx.z, 0, p.Kt, -1);
     } else {
         const PkPlan pl = pk_plan(p, gridDim.x);
         const int w = blockIdx.x;
@@ -1793,28 +2095,39 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
         // registers (a value the compiler cannot prove uniform puts every
         // buffer load of the K loop in a waterfall loop).
         auto uni = [](int64_t v) { return __builtin_amdgcn_readfirstlane(static_cast<int>(v)); };
-        bool first = true;
-        // a barrier between tiles: the next tile's first DMA overwrites LDS
-        // that other waves may still read for the last one
-        for (int64_t t = w; t < pl.dp_tiles; t += gridDim.x) {
+        // one loop and one tile call site for both parts (whole tiles
+        // t = w, w + P, ..., then this worker's stream-K range [lo, hi)), so
+        // the tile is inlined once; a barrier between tiles: the next
+        // tile's first DMA overwrites LDS that other waves may still read
+        // for the last one
+        int64_t t = w, lo = 0, hi = 0;
+        bool split = false, first = true;
+        while (true) {
+            int64_t tt;
+            int k0 = 0, k1 = p.Kt, slot = -1;
+            if (!split) {
+                if (t < pl.dp_tiles) {
+                    tt = t;
+                    t += gridDim.x;
+                } else {
+                    if (!pl.sk || w >= pl.Ps) break;
+                    split = true;
+                    lo = w * pl.I / pl.Ps;
+                    hi = (w + 1) * pl.I / pl.Ps;
+                    continue;
+                }
+            } else {
+                if (lo >= hi) break;
+                const int64_t tr = lo / p.Kt;  // split tile, counted from the first one
+                k0 = static_cast<int>(lo - tr * p.Kt);
+                k1 = static_cast<int>(min<int64_t>(p.Kt, k0 + (hi - lo)));
+                tt = pl.dp_tiles + tr;
+                slot = (k0 == 0 && k1 == p.Kt) ? -1 : static_cast<int>(w + tr);
+                lo += k1 - k0;
+            }
             if (!first) __syncthreads();
             first = false;
-            mma_tile<BPS, GBIG, GR, SWI, L, SK, RB, F32, true>(p, mm_lds, uni(t % pl.X), uni(t / pl.X), 0, 0, p.Kt,
-                                                                -1);
-        }
-        if (!pl.sk || w >= pl.Ps) return;
-        int64_t lo = w * pl.I / pl.Ps;
-        const int64_t hi = (w + 1) * pl.I / pl.Ps;
-        while (lo < hi) {
-            const int64_t tr = lo / p.Kt;  // split tile, counted from the first one
-            const int k0 = uni(lo - tr * p.Kt);
-            const int k1 = uni(min<int64_t>(p.Kt, k0 + (hi - lo)));
-            const int64_t t = pl.dp_tiles + tr;
-            if (!first) __syncthreads();
-            first = false;
-            mma_tile<BPS, GBIG, GR, SWI, L, SK, RB, F32, true>(p, mm_lds, uni(t % pl.X), uni(t / pl.X), 0, k0, k1,
-                                                                uni((k0 == 0 && k1 == p.Kt) ? -1 : w + tr));
-            lo += k1 - k0;
+            tile(uni(tt % pl.X), uni(tt / pl.X), 0, uni(k0), uni(k1), uni(slot));
         }
     }
 }
@@ -1827,8 +2140,10 @@ __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_ker
 // wave qn): thread t holds lane t & 63 of column tile t >> 6 at row blocks
 // 0..3, or with SWI the gate / up pair (2 (t >> 6 & 1), + 1) at row blocks
 // 2 (t >> 7) and + 1; each segment's loads are issued four segments at a
-// time before they are added.
-template <bool SWI>
+// time before they are added.  W32 (slots written by mma_tile32): thread t
+// holds lane t & 63 of blocks (ib, cb) at the D rows 8 i4 .. of the (ib, i4)
+// pairs 2 (t >> 6) and + 1, cb = 0 and 1 of each (a gate / up pair with SWI).
+template <bool SWI, bool W32 = false>
 __global__ __launch_bounds__(256) void w4_pk_fixup_kernel(W4Args p) {
     const PkPlan pl = pk_plan(p, p.pk_workers);
     const int64_t tr = blockIdx.x >> 2;
@@ -1840,12 +2155,21 @@ __global__ __launch_bounds__(256) void w4_pk_fixup_kernel(W4Args p) {
     int e, m0, m_end;
     if (!resolve_group<64>(p, static_cast<int>(t / pl.X), e, m0, m_end)) return;
     const int lane = threadIdx.x & 63, cp = threadIdx.x >> 6;
-    // this thread's four (row block, column tile) accumulators
-    int ib[4], cb[4];
+    // this thread's four slot entries: (row block, column tile) of the
+    // 16x16 layout, or (ib, cb, i4) of the 32x32 one
+    int ib[4], cb[4], ent[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-        ib[k] = SWI ? 2 * (cp >> 1) + (k >> 1) : k;
-        cb[k] = SWI ? 2 * (cp & 1) + (k & 1) : cp;
+        if constexpr (W32) {
+            const int c = 2 * cp + (k >> 1);
+            ib[k] = c >> 2;  // 32-row block
+            cb[k] = k & 1;
+            ent[k] = (ib[k] * 2 + cb[k]) * 4 + (c & 3);
+        } else {
+            ib[k] = SWI ? 2 * (cp >> 1) + (k >> 1) : k;
+            cb[k] = SWI ? 2 * (cp & 1) + (k & 1) : cp;
+            ent[k] = ib[k] * MM_CT + cb[k];
+        }
     }
     const f32x4_t* const W = reinterpret_cast<const f32x4_t*>(p.ws) + qn * 4 * MM_CT * 64 + lane;
     f32x4_t acc[4];
@@ -1855,7 +2179,7 @@ __global__ __launch_bounds__(256) void w4_pk_fixup_kernel(W4Args p) {
         for (int u = 0; u < 4; ++u) {
             const f32x4_t* const S = W + (min(w0 + u, wb) + tr) * kPkTileVecs;
 #pragma unroll
-            for (int k = 0; k < 4; ++k) v[u][k] = S[(ib[k] * MM_CT + cb[k]) * 64];
+            for (int k = 0; k < 4; ++k) v[u][k] = S[ent[k] * 64];
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -1874,12 +2198,21 @@ __global__ __launch_bounds__(256) void w4_pk_fixup_kernel(W4Args p) {
     const int col = lane & 15;
 #pragma unroll
     for (int k = 0; k < 4; k += SWI ? 2 : 1) {
-        const int nt = nt0 + cb[k];
-        const int cn = (SWI ? (nt >> 1) : nt) * kW4TileN + col;
+        int nt, cn, row0;
+        if constexpr (W32) {
+            const int u = (lane >> 4) & 1;
+            nt = nt0 + cb[k] + 2 * u;
+            cn = (SWI ? (nt0 >> 1) + u : nt) * kW4TileN + col;
+            row0 = m0 + 32 * ib[k] + 8 * (ent[k] & 3) + 4 * (lane >> 5);
+        } else {
+            nt = nt0 + cb[k];
+            cn = (SWI ? (nt >> 1) : nt) * kW4TileN + col;
+            row0 = m0 + ib[k] * 16 + 4 * (lane >> 4);
+        }
         if (nt >= p.Nt || cn >= p.N) continue;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int row = m0 + ib[k] * 16 + 4 * (lane >> 4) + r;
+            const int row = row0 + r;
             if (row >= m_end) continue;
             if constexpr (SWI) C[static_cast<int64_t>(row) * p.N + cn] = f32_to_bf16(swiglu(acc[k][r], acc[k + 1][r]));
             else C[static_cast<int64_t>(row) * p.N + cn] = f32_to_bf16(acc[k][r]);
@@ -2059,11 +2392,31 @@ void launch_gemv_waves(const W4Args& a, dim3 grid, int W, int bps, hipStream_t s
 
 // G >= 128 only (one scale group per K tile segment); smaller groups would
 // need four times the activation-sum registers and spill.
+// LDS of the 32x32x16 tile: two activation buffers and two tiles' row sums
+constexpr size_t kMma32Lds = 2 * 64 * kW4TileK * 2 + 2 * 64 * 4;
+// the 32x32x16 form of the 64 x 256 bf16 tile (LHQ_W4_W32=0 in a tuning
+// build keeps the 16x16x32 form)
+bool use_w32() {
+    static const bool on = tuning_knob("LHQ_W4_W32", 1) != 0;
+    return on;
+}
+template <bool GBIG, bool GR, bool SWI, bool PK>
+void launch_mma32(const W4Args& a, dim3 grid, hipStream_t s) {
+    w4_mma_kernel<4, GBIG, GR, SWI, 1, false, 4, false, PK, true><<<grid, 256, kMma32Lds, s>>>(a);
+}
+
 template <bool GR, bool SWI, int L>
 void launch_mma_l(const W4Args& a, unsigned row_tiles, unsigned batch, hipStream_t s) {
     constexpr size_t lds = 2 * ((L == 1) ? 64 : (L == 3) ? 256 : 128) * kW4TileK * 2;
     constexpr int threads = (L == 3) ? 512 : 256;
     const dim3 grid(ceil_div(a.Nt, ((L == 1) ? 4 : 2) * MM_CT), row_tiles, batch);
+    if constexpr (L == 1) {
+        if (use_w32()) {
+            if (a.gmul) launch_mma32<true, GR, SWI, false>(a, grid, s);
+            else launch_mma32<false, GR, SWI, false>(a, grid, s);
+            return;
+        }
+    }
     if (a.gmul) {
         if constexpr (lds > 64 * 1024) allow_cu_lds<&w4_mma_kernel<4, true, GR, SWI, L>>();
         w4_mma_kernel<4, true, GR, SWI, L><<<grid, threads, lds, s>>>(a);
@@ -2405,12 +2758,21 @@ int launch_mma_pk(W4Args a, void* ws, int64_t ws_slots, hipStream_t s, const cha
     a.ws = static_cast<float*>(ws);
     a.pk_slots = may_split ? ws_slots : 0;
     a.pk_workers = P;
-    if (a.gmul) w4_mma_kernel<4, true, true, SWI, 1, false, 4, false, true><<<P, 256, lds, s>>>(a);
-    else w4_mma_kernel<4, false, true, SWI, 1, false, 4, false, true><<<P, 256, lds, s>>>(a);
+    const bool w32 = use_w32();
+    if (w32) {
+        if (a.gmul) launch_mma32<true, true, SWI, true>(a, dim3(P), s);
+        else launch_mma32<false, true, SWI, true>(a, dim3(P), s);
+    } else if (a.gmul) {
+        w4_mma_kernel<4, true, true, SWI, 1, false, 4, false, true><<<P, 256, lds, s>>>(a);
+    } else {
+        w4_mma_kernel<4, false, true, SWI, 1, false, 4, false, true><<<P, 256, lds, s>>>(a);
+    }
     if (int st = check_launch(who)) return st;
     if (!may_split) return LHQ_OK;
     // four workgroups per split tile (every tile when the split runs)
-    w4_pk_fixup_kernel<SWI><<<static_cast<unsigned>(4 * std::max<int64_t>(1, t_max)), 256, 0, s>>>(a);
+    const unsigned fix_wgs = static_cast<unsigned>(4 * std::max<int64_t>(1, t_max));
+    if (w32) w4_pk_fixup_kernel<SWI, true><<<fix_wgs, 256, 0, s>>>(a);
+    else w4_pk_fixup_kernel<SWI><<<fix_wgs, 256, 0, s>>>(a);
     return check_launch(who);
 }
 
