@@ -1795,9 +1795,10 @@ __device__ __forceinline__ void mma_tile(const W4Args& p, uint8_t* mm_lds, int b
 // Everything else (zero point folded into the codes, xs seeding each chain,
 // one correction per group, the two phases at raised priority for the
 // matrix phase, unconditional clamped loads) is as in mma_tile.
-template <bool GBIG, bool GR, bool SWI, bool PK>
-__device__ __forceinline__ void mma_tile32(const W4Args& p, uint8_t* mm_lds, int bx, int by, int bz, int kb, int ke,
-                                           int pk_slot) {
+template <bool GBIG, bool GR, bool SWI, bool PK, bool SK>
+__device__ __forceinline__ void mma_tile32(const W4Args& p, uint8_t* mm_lds, int bx, int by, int bz, int kb_in,
+                                           int ke_in, int pk_slot) {
+    static_assert(!SK || (!GR && !SWI && !PK), "split-K on plain launches only");
     constexpr int BPS = 4;
     constexpr int RBYTES = kW4TileK * 2;          // LDS bytes per activation row
     constexpr int A_BYTES = 64 * RBYTES;          // one activation buffer
@@ -1805,6 +1806,11 @@ __device__ __forceinline__ void mma_tile32(const W4Args& p, uint8_t* mm_lds, int
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int col = lane & 15, h = lane >> 5, u = (lane >> 4) & 1;
+    // K tiles [kb, ke): a split-K launch takes its split's range from bz,
+    // which is the batch index otherwise
+    const int kb = SK ? bz * p.kps : kb_in;
+    const int ke = SK ? min(p.Kt, kb + p.kps) : ke_in;
+    const int z = SK ? 0 : bz;
     int m0, m_end;
     const uint8_t* qw;
     const uint16_t* sc;
@@ -1823,11 +1829,11 @@ __device__ __forceinline__ void mma_tile32(const W4Args& p, uint8_t* mm_lds, int
     } else {
         m0 = by * 64;
         m_end = p.M;
-        qw = p.qw + bz * p.qw_bs;
-        sc = static_cast<const uint16_t*>(p.scales) + bz * p.s_bs;
-        zs = p.zeros + bz * p.z_bs;
+        qw = p.qw + z * p.qw_bs;
+        sc = static_cast<const uint16_t*>(p.scales) + z * p.s_bs;
+        zs = p.zeros + z * p.z_bs;
     }
-    const uint16_t* A = static_cast<const uint16_t*>(p.A) + (GR ? 0 : bz * p.a_bs);
+    const uint16_t* A = static_cast<const uint16_t*>(p.A) + (GR ? 0 : z * p.a_bs);
     uint32_t a_voff[DMA];  // as in mma_tile: LDS row idx >> 4, slot idx & 15
 #pragma unroll
     for (int q = 0; q < DMA; ++q) {
@@ -2036,7 +2042,25 @@ __device__ __forceinline__ void mma_tile32(const W4Args& p, uint8_t* mm_lds, int
             return;
         }
     }
-    uint16_t* const C = static_cast<uint16_t*>(p.C) + (GR ? 0 : bz * p.c_bs);
+    if constexpr (SK) {
+        // the split's fp32 partial sums, ws[split][M][N]
+        float* const W = p.ws + static_cast<int64_t>(bz) * p.M * p.N;
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+            const int nt = ntw + cb + 2 * u;
+            const int cn = nt * kW4TileN + col;
+            if (nt >= p.Nt || cn >= p.N) continue;
+#pragma unroll
+            for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int row = m0 + 32 * ib + 8 * (e >> 2) + 4 * h + (e & 3);
+                    if (row < m_end) W[static_cast<int64_t>(row) * p.N + cn] = acc[ib][cb][e];
+                }
+        }
+        return;
+    }
+    uint16_t* const C = static_cast<uint16_t*>(p.C) + (GR ? 0 : z * p.c_bs);
 #pragma unroll
     for (int cb = 0; cb < (SWI ? 1 : 2); ++cb) {
         // SwiGLU: block 0 holds the gates, block 1 the ups of output tile
@@ -2079,10 +2103,10 @@ __device__ __forceinline__ void mma_tile32(const W4Args& p, uint8_t* mm_lds, int
 template <int BPS, bool GBIG, bool GR, bool SWI, int L, bool SK = false, int RB = 4, bool F32 = false, bool PK = false,
           bool W32 = false>
 __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_kernel(W4Args p) {
-    static_assert(!W32 || (BPS == 4 && L == 1 && RB == 4 && !SK && !F32), "the 32x32x16 tile: bf16 64 x 256 tiles");
+    static_assert(!W32 || (BPS == 4 && L == 1 && RB == 4 && !F32), "the 32x32x16 tile: bf16 64 x 256 tiles");
     extern __shared__ __attribute__((aligned(1024))) uint8_t mm_lds[];
     auto tile = [&](int bx, int by, int bz, int k0, int k1, int slot) {
-        if constexpr (W32) mma_tile32<GBIG, GR, SWI, PK>(p, mm_lds, bx, by, bz, k0, k1, slot);
+        if constexpr (W32) mma_tile32<GBIG, GR, SWI, PK, SK>(p, mm_lds, bx, by, bz, k0, k1, slot);
         else mma_tile<BPS, GBIG, GR, SWI, L, SK, RB, F32, PK>(p, mm_lds, bx, by, bz, k0, k1, slot);
     };
     if constexpr (!PK) {
@@ -2959,6 +2983,13 @@ void launch_split_rb(const W4Args& a, unsigned splits, hipStream_t s) {
     constexpr size_t lds = 2 * NK * 16 * RB * kW4TileK * 2;
     constexpr int threads = (L >= 3) ? 512 : 256;
     const dim3 grid(ceil_div(a.Nt, ((L == 1 || L == 4) ? 4 : 2) * MM_CT), ceil_div(a.M, 16 * RB), splits);
+    if constexpr (L == 1 && RB == 4) {
+        if (use_w32()) {
+            if (a.gmul) w4_mma_kernel<4, true, false, false, 1, true, 4, false, false, true><<<grid, 256, kMma32Lds, s>>>(a);
+            else w4_mma_kernel<4, false, false, false, 1, true, 4, false, false, true><<<grid, 256, kMma32Lds, s>>>(a);
+            return;
+        }
+    }
     if (a.gmul) {
         if constexpr (lds > 64 * 1024) allow_cu_lds<&w4_mma_kernel<4, true, false, false, L, true, RB>>();
         w4_mma_kernel<4, true, false, false, L, true, RB><<<grid, threads, lds, s>>>(a);
