@@ -1762,8 +1762,8 @@ __device__ __forceinline__ void mma_tile(const W4Args& p, uint8_t* mm_lds, int b
 
 // ---------------------------------------------------------------------------
 // The 64 x 256 bf16 tile on the 32x32x16 MFMA (W32: layout 1, 64-row blocks,
-// bf16 activations and output; plain, batched, grouped, SwiGLU and the
-// persistent grouped launches).  Same loads, LDS layout and K loop as
+// bf16 activations and output; plain, batched, grouped, SwiGLU, persistent
+// grouped and split-K launches).  Same loads and LDS activation layout as
 // mma_tile; what changes is the matrix work per K tile and wave (64 rows x
 // 64 columns x 128 k):
 //   - the products run as 32 MFMAs of 32x32x16 instead of 64 of 16x16x32.
@@ -1773,12 +1773,15 @@ __device__ __forceinline__ void mma_tile(const W4Args& p, uint8_t* mm_lds, int b
 //     the 16-cycle form leaves ~2: measured with register operands, two
 //     waves per SIMD, chains of MFMAs with n VALU instructions between them:
 //     16x16x32 17.6 / 27.1 / 35.2 cycles per MFMA at n = 0 / 4 / 6,
-//     32x32x16 32.5 / 33.6 / 35.2 / 44.6 at n = 0 / 4 / 6 / 8;
+//     32x32x16 32.5 / 33.6 / 35.2 / 44.6 at n = 0 / 4 / 6 / 8.  So the
+//     weight decode is interleaved with the MFMAs (two operands per k step)
+//     instead of running as a phase of its own;
 //   - the activation sums xs = -144 * sum_k x seeding the chains are made
-//     once per workgroup, each wave the 16 rows 16 * wave.. on the
-//     16x16x32 MFMA (4 MFMAs against the -144 operand), and handed to every
-//     wave through 256 bytes of LDS (a barrier between the VALU phase and the
-//     matrix phase), where the 16x16 form has every wave sum all 64 rows;
+//     once per workgroup: each wave sums the 16 rows its own DMAs carry
+//     (16 * wave..; 4 MFMAs of 16x16x32 against the -144 operand) as soon as
+//     its loads land, before the K tile's rendezvous, whose barrier hands
+//     them to every wave through LDS; the 16x16 form has every wave sum all
+//     64 rows;
 //   - the wave's four column tiles nt0 + c form two 32-column blocks: block
 //     cb holds tile cb in lanes with (lane >> 4) & 1 == 0 and tile cb + 2 in
 //     the others, so with SwiGLU's interleaved gate / up tiles block 0 holds
@@ -1793,8 +1796,8 @@ __device__ __forceinline__ void mma_tile(const W4Args& p, uint8_t* mm_lds, int b
 //     4 (l >> 5) + (e & 3), column (lane & 15) of the lane's tile; the group
 //     correction acc += s * t uses one scale per lane and block.
 // Everything else (zero point folded into the codes, xs seeding each chain,
-// one correction per group, the two phases at raised priority for the
-// matrix phase, unconditional clamped loads) is as in mma_tile.
+// one correction per group, one K tile of loads in flight, unconditional
+// clamped loads) is as in mma_tile.
 template <bool GBIG, bool GR, bool SWI, bool PK, bool SK>
 __device__ __forceinline__ void mma_tile32(const W4Args& p, uint8_t* mm_lds, int bx, int by, int bz, int kb_in,
                                            int ke_in, int pk_slot) {
