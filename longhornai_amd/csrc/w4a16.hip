@@ -1761,11 +1761,12 @@ __device__ __forceinline__ void mma_tile(const W4Args& p, uint8_t* mm_lds, int b
 }
 
 // ---------------------------------------------------------------------------
-// The 64 x 256 bf16 tile on the 32x32x16 MFMA (W32: layout 1, 64-row blocks,
-// bf16 activations and output; plain, batched, grouped, SwiGLU, persistent
-// grouped and split-K launches).  Same loads and LDS activation layout as
-// mma_tile; what changes is the matrix work per K tile and wave (64 rows x
-// 64 columns x 128 k):
+// The 64 x 256 tile on the 32x32x16 MFMA (W32: layout 1, 64-row blocks;
+// bf16 activations and output on plain, batched, grouped, SwiGLU, persistent
+// grouped and split-K launches, and the fp32 interface (F32) on plain and
+// split-K launches).  Same loads and LDS activation layout as mma_tile; what
+// changes is the matrix work per K tile and wave (64 rows x 64 columns x
+// 128 k):
 //   - the products run as 32 MFMAs of 32x32x16 instead of 64 of 16x16x32.
 //     Each MFMA issue takes the SIMD's issue port for about 8 cycles
 //     whatever its size, so the 32-cycle form leaves room for ~6 VALU
@@ -1795,15 +1796,22 @@ __device__ __forceinline__ void mma_tile(const W4Args& p, uint8_t* mm_lds, int b
 //   - D element e of block (ib, cb) in lane l: row 32 ib + 8 (e >> 2) +
 //     4 (l >> 5) + (e & 3), column (lane & 15) of the lane's tile; the group
 //     correction acc += s * t uses one scale per lane and block.
+// F32: fp32 activations staged in LDS (512 bytes per row); each wave splits
+// its own 16 rows into bf16 hi + lo in place before the rendezvous (with
+// their sums), and every product runs twice, hi and lo, as in mma_tile's
+// fp32 form; symmetric codes, fp32 scales, the alpha / beta epilogue.
 // Everything else (zero point folded into the codes, xs seeding each chain,
 // one correction per group, one K tile of loads in flight, unconditional
 // clamped loads) is as in mma_tile.
-template <bool GBIG, bool GR, bool SWI, bool PK, bool SK>
+template <bool GBIG, bool GR, bool SWI, bool PK, bool SK, bool F32>
 __device__ __forceinline__ void mma_tile32(const W4Args& p, uint8_t* mm_lds, int bx, int by, int bz, int kb_in,
                                            int ke_in, int pk_slot) {
     static_assert(!SK || (!GR && !SWI && !PK), "split-K on plain launches only");
+    static_assert(!F32 || (!GR && !SWI && !PK), "the fp32 interface: plain launches");
     constexpr int BPS = 4;
-    constexpr int RBYTES = kW4TileK * 2;          // LDS bytes per activation row
+    constexpr int EA = F32 ? 4 : 2;               // activation bytes
+    constexpr int RBYTES = kW4TileK * EA;         // LDS bytes per activation row
+    constexpr int CPR = RBYTES / 16;              // 16-byte chunks per row
     constexpr int A_BYTES = 64 * RBYTES;          // one activation buffer
     constexpr int DMA = A_BYTES / 1024 / 4;       // activation DMAs per wave per K tile
     const int lane = threadIdx.x & 63;
@@ -1837,14 +1845,16 @@ __device__ __forceinline__ void mma_tile32(const W4Args& p, uint8_t* mm_lds, int
         zs = p.zeros + z * p.z_bs;
     }
     const uint16_t* A = static_cast<const uint16_t*>(p.A) + (GR ? 0 : z * p.a_bs);
-    uint32_t a_voff[DMA];  // as in mma_tile: LDS row idx >> 4, slot idx & 15
+    const float* Af = static_cast<const float*>(p.A) + z * p.a_bs;
+    const float* scf = static_cast<const float*>(p.scales) + z * p.s_bs;
+    uint32_t a_voff[DMA];  // as in mma_tile: LDS row idx / CPR, slot idx % CPR
 #pragma unroll
     for (int q = 0; q < DMA; ++q) {
         const int idx = (DMA * wave + q) * 64 + lane;
-        const int r = idx / 16, slot = idx % 16;
+        const int r = idx / CPR, slot = idx % CPR;
         const int row = min(m0 + r, m_end - 1);
         a_voff[q] = (static_cast<uint32_t>(row - m0) * static_cast<uint32_t>(p.K) +
-                     static_cast<uint32_t>((slot ^ (r & 15)) * 8)) * 2;
+                     static_cast<uint32_t>((slot ^ (r & 15)) * (16 / EA))) * EA;
     }
     const uint32_t s_half = 16u * (col & 1);
     const int nt0 = min(bx * 4 * MM_CT + wave * MM_CT, p.Nt - 1);
@@ -1852,25 +1862,28 @@ __device__ __forceinline__ void mma_tile32(const W4Args& p, uint8_t* mm_lds, int
     auto extent = [](int64_t bytes) {
         return static_cast<int>(static_cast<uint32_t>(bytes < int64_t{0xFFFFFFFF} ? bytes : int64_t{0xFFFFFFFF}));
     };
+    constexpr int ES = F32 ? 4 : 2;  // scale bytes
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t*>(qw) + static_cast<int64_t>(nt0) * p.Kt * kW4TileBytes, 0,
         extent(static_cast<int64_t>(nt_left) * p.Kt * kW4TileBytes), kBufWord3);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(sc) + static_cast<int64_t>(nt0) * p.NG * 16, 0,
-        extent(static_cast<int64_t>(nt_left) * p.NG * 16 * 2), kBufWord3);
+        F32 ? static_cast<void*>(const_cast<float*>(scf) + static_cast<int64_t>(nt0) * p.NG * 16)
+            : static_cast<void*>(const_cast<uint16_t*>(sc) + static_cast<int64_t>(nt0) * p.NG * 16),
+        0, extent(static_cast<int64_t>(nt_left) * p.NG * 16 * ES), kBufWord3);
     const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint32_t*>(zs) + static_cast<int64_t>(nt0) * p.NG8 * 16, 0,
-        extent(static_cast<int64_t>(nt_left) * p.NG8 * 16 * 4), kBufWord3);
+        extent(F32 ? 0 : static_cast<int64_t>(nt_left) * p.NG8 * 16 * 4), kBufWord3);
     const __amdgpu_buffer_rsrc_t ra_ = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(A) + static_cast<int64_t>(m0) * p.K, 0,
-        extent(static_cast<int64_t>(m_end - m0) * p.K * 2), kBufWord3);
+        F32 ? static_cast<void*>(const_cast<float*>(Af) + static_cast<int64_t>(m0) * p.K)
+            : static_cast<void*>(const_cast<uint16_t*>(A) + static_cast<int64_t>(m0) * p.K),
+        0, extent(static_cast<int64_t>(m_end - m0) * p.K * EA), kBufWord3);
     // the lane's tile in block cb (tiles past Nt re-read the last one)
     uint32_t w_voff[2], s_voff[2], z_voff[2];
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
         const uint32_t dt = static_cast<uint32_t>(min(nt0 + cb + 2 * u, p.Nt - 1) - nt0);
         w_voff[cb] = dt * static_cast<uint32_t>(p.Kt) * kW4TileBytes + col * 16 + 256 * h;
-        s_voff[cb] = (dt * static_cast<uint32_t>(p.NG) * 16 + (col & ~1)) * 2;
+        s_voff[cb] = (dt * static_cast<uint32_t>(p.NG) * 16 + (F32 ? col : (col & ~1))) * ES;
         z_voff[cb] = (dt * static_cast<uint32_t>(p.NG8) * 16 + col) * 4;
     }
 
@@ -1884,12 +1897,12 @@ __device__ __forceinline__ void mma_tile32(const W4Args& p, uint8_t* mm_lds, int
 #pragma unroll
         for (int q = 0; q < DMA; ++q)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ra_, (LHQ_LDS_AS void*)(buf + (DMA * wave + q) * 1024), 16,
-                                                     a_voff[q], kt * kW4TileK * 2, 0, 0);
+                                                     a_voff[q], kt * kW4TileK * EA, 0, 0);
         const int g = group_of_c<BPS, GBIG>(kt, 0, p.gmul);
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
-            R.zw[cb] = __builtin_amdgcn_raw_buffer_load_b32(rz, z_voff[cb], (g >> 3) * 16 * 4, 0);
-            R.sw[cb] = __builtin_amdgcn_raw_buffer_load_b32(rs, s_voff[cb], g * 16 * 2, 0);
+            if constexpr (!F32) R.zw[cb] = __builtin_amdgcn_raw_buffer_load_b32(rz, z_voff[cb], (g >> 3) * 16 * 4, 0);
+            R.sw[cb] = __builtin_amdgcn_raw_buffer_load_b32(rs, s_voff[cb], g * 16 * ES, 0);
 #pragma unroll
             for (int s = 0; s < 2; ++s)
                 R.w[cb][s] = __builtin_amdgcn_raw_buffer_load_b128(rw, w_voff[cb] + 512 * s, kt * kW4TileBytes, 0);
@@ -1908,6 +1921,12 @@ __device__ __forceinline__ void mma_tile32(const W4Args& p, uint8_t* mm_lds, int
     // rows past the end read the last row; a tile with no live row (m0 >=
     // m_end) skips the arithmetic in every wave alike
     const bool live = m0 < m_end;
+    // activation chunk of row `row` of the tile (LDS slot chunk ^ (row & 15));
+    // fp32 rows after the split: chunk 8 j + 2 g holds the bf16 hi halves and
+    // chunk 8 j + 2 g + 1 the lo halves of k = 32 j + 8 g .. + 7
+    auto chunk_at = [&](const uint8_t* buf, int row, int c) {
+        return const_cast<uint8_t*>(buf) + row * RBYTES + ((c ^ (row & 15)) * 16);
+    };
     // The activation sums of a K tile, made before the rendezvous that
     // opens it: each wave's own DMAs carry its 16 rows (16 * wave..) of every
     // tile, so once its loads have landed the wave sums them (4 MFMAs against
@@ -1915,19 +1934,41 @@ __device__ __forceinline__ void mma_tile32(const W4Args& p, uint8_t* mm_lds, int
     // alike) and column 0 writes them to the tile's half of xs_l; the
     // rendezvous barrier then publishes them to every wave.  Two halves: a
     // tile's sums are written while the waves may still read the previous
-    // tile's.
+    // tile's.  F32: the wave first splits its rows' fp32 activations into
+    // bf16 hi + lo in place (each lane rewrites the two chunks it read) and
+    // sums both halves (8 MFMAs).
     auto sums = [&](const uint8_t* buf, int kt_in) {
         // vmcnt(0) (expcnt and lgkmcnt at their maxima), as a builtin so the
         // compiler's wait counting knows the tile's loads are complete
         __builtin_amdgcn_s_waitcnt(0x0F70);
         asm volatile("" ::: "memory");
         if (!live) return;
+        const int row = 16 * wave + col;
         f32x4_t xs = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            xs = mfma_bf16_16x16x32(*reinterpret_cast<const u32x4_t*>(buf + (16 * wave + col) * RBYTES +
-                                                                      (((4 * j + (lane >> 4)) ^ col) * 16)),
-                                    m144, xs);
+        for (int j = 0; j < 4; ++j) {
+            if constexpr (F32) {
+                uint8_t* const c_hi = chunk_at(buf, row, 8 * j + 2 * (lane >> 4));
+                uint8_t* const c_lo = chunk_at(buf, row, 8 * j + 2 * (lane >> 4) + 1);
+                const f32x4_t x0 = *reinterpret_cast<const f32x4_t*>(c_hi);
+                const f32x4_t x1 = *reinterpret_cast<const f32x4_t*>(c_lo);
+                const float v[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+                u32x4_t ah, al;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint16_t h0 = f32_to_bf16(v[2 * e]), h1 = f32_to_bf16(v[2 * e + 1]);
+                    ah[e] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
+                    al[e] = pack_bf16x2(v[2 * e] - bf16_to_f32(h0), v[2 * e + 1] - bf16_to_f32(h1));
+                }
+                *reinterpret_cast<u32x4_t*>(c_hi) = ah;
+                *reinterpret_cast<u32x4_t*>(c_lo) = al;
+                xs = mfma_bf16_16x16x32(ah, m144, xs);
+                xs = mfma_bf16_16x16x32(al, m144, xs);
+            } else {
+                xs = mfma_bf16_16x16x32(
+                    *reinterpret_cast<const u32x4_t*>(chunk_at(buf, row, 4 * j + (lane >> 4))), m144, xs);
+            }
+        }
         if (col == 0) *reinterpret_cast<f32x4_t*>(xs_l + 64 * (kt_in & 1) + 16 * wave + 4 * (lane >> 4)) = xs;
     };
     auto compute = [&](const uint8_t* buf, const Regs& R, int kt_in) {
@@ -1938,24 +1979,33 @@ __device__ __forceinline__ void mma_tile32(const W4Args& p, uint8_t* mm_lds, int
         float scs[2];
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
-            zb[cb] = __builtin_amdgcn_perm(0u, 16u - ((R.zw[cb] >> (4 * (g & 7))) & 15u), 0u);
-            scs[cb] = f16_to_f32(static_cast<uint16_t>(R.sw[cb] >> s_half));
+            if constexpr (F32) {
+                zb[cb] = 0x08080808u;  // symmetric codes: 16 - 8 in every byte
+                scs[cb] = __uint_as_float(R.sw[cb]);
+            } else {
+                zb[cb] = __builtin_amdgcn_perm(0u, 16u - ((R.zw[cb] >> (4 * (g & 7))) & 15u), 0u);
+                scs[cb] = f16_to_f32(static_cast<uint16_t>(R.sw[cb] >> s_half));
+            }
         }
-        // activation fragment of row block ib for k step q, read two k
-        // steps ahead of its use
-        auto frag32 = [&](int q, int ib) {
+        // activation fragment(s) of row block ib for k step q (F32: the hi
+        // and the lo halves), read ahead of their use
+        constexpr int NH = F32 ? 2 : 1;  // fragments per row block and k step
+        constexpr int RING = F32 ? 2 : 3;
+        auto frag32 = [&](int q, int ib, int hh) {
             const int j = q >> 1, s = q & 1;
-            return *reinterpret_cast<const u32x4_t*>(buf + (32 * ib + (lane & 31)) * RBYTES +
-                                                     (((4 * j + 2 * s + h) ^ col) * 16));
+            const int c = F32 ? 8 * j + 2 * (2 * s + h) + hh : 4 * j + 2 * s + h;
+            return *reinterpret_cast<const u32x4_t*>(chunk_at(buf, 32 * ib + (lane & 31), c));
         };
-        u32x4_t af[3][2];
+        u32x4_t af[RING][2][NH];
 #pragma unroll
-        for (int q = 0; q < 2; ++q)
+        for (int q = 0; q < RING - 1; ++q)
 #pragma unroll
-            for (int ib = 0; ib < 2; ++ib) af[q][ib] = frag32(q, ib);
+            for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+                for (int hh = 0; hh < NH; ++hh) af[q][ib][hh] = frag32(q, ib, hh);
         // four chains (ib, cb) seeded with their row block's sums; per k
         // step q the two weight operands are decoded just before their
-        // MFMAs (the VALU work runs under the 32-cycle MFMAs), and the two
+        // MFMAs (the VALU work runs under the 32-cycle MFMAs), and the
         // activation fragments serve both column blocks
         f32x16_t t[2][2];
 #pragma unroll
@@ -1971,17 +2021,22 @@ __device__ __forceinline__ void mma_tile32(const W4Args& p, uint8_t* mm_lds, int
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
             const int j = q >> 1, s = q & 1;
-            if (q + 2 < 8)
+            if (q + RING - 1 < 8)
 #pragma unroll
-                for (int ib = 0; ib < 2; ++ib) af[(q + 2) % 3][ib] = frag32(q + 2, ib);
+                for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+                    for (int hh = 0; hh < NH; ++hh) af[(q + RING - 1) % RING][ib][hh] = frag32(q + RING - 1, ib, hh);
             u32x4_t bq[2];
 #pragma unroll
             for (int cb = 0; cb < 2; ++cb) bq[cb] = w4_operand_z(R.w[cb][s][j], zb[cb]);
 #pragma unroll
             for (int ib = 0; ib < 2; ++ib)
 #pragma unroll
-                for (int cb = 0; cb < 2; ++cb) t[ib][cb] = mfma_bf16_32x32x16(af[q % 3][ib], bq[cb], t[ib][cb]);
-            // keeps each k step's fragment reads two steps ahead of their use
+                for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                    for (int hh = 0; hh < NH; ++hh)
+                        t[ib][cb] = mfma_bf16_32x32x16(af[q % RING][ib][hh], bq[cb], t[ib][cb]);
+            // keeps each k step's fragment reads ahead of their use
             __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
@@ -2063,24 +2118,42 @@ __device__ __forceinline__ void mma_tile32(const W4Args& p, uint8_t* mm_lds, int
         }
         return;
     }
-    uint16_t* const C = static_cast<uint16_t*>(p.C) + (GR ? 0 : z * p.c_bs);
+    if constexpr (F32) {
+        // the reference's alpha / beta epilogue on fp32 C
 #pragma unroll
-    for (int cb = 0; cb < (SWI ? 1 : 2); ++cb) {
-        // SwiGLU: block 0 holds the gates, block 1 the ups of output tile
-        // ntw / 2 + u
-        const int nt = ntw + cb + 2 * u;
-        const int cn = (SWI ? (ntw >> 1) + u : nt) * kW4TileN + col;
-        if (nt >= p.Nt || cn >= p.N) continue;
+        for (int cb = 0; cb < 2; ++cb) {
+            const int nt = ntw + cb + 2 * u;
+            const int cn = nt * kW4TileN + col;
+            if (nt >= p.Nt || cn >= p.N) continue;
 #pragma unroll
-        for (int ib = 0; ib < 2; ++ib)
+            for (int ib = 0; ib < 2; ++ib)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int row = m0 + 32 * ib + 8 * (e >> 2) + 4 * h + (e & 3);
-                if (row >= m_end) continue;
-                if constexpr (SWI)
-                    C[static_cast<int64_t>(row) * p.N + cn] = f32_to_bf16(swiglu(acc[ib][0][e], acc[ib][1][e]));
-                else C[static_cast<int64_t>(row) * p.N + cn] = f32_to_bf16(acc[ib][cb][e]);
-            }
+                for (int e = 0; e < 16; ++e) {
+                    const int row = m0 + 32 * ib + 8 * (e >> 2) + 4 * h + (e & 3);
+                    if (row < m_end)
+                        w4_store<true>(p, z * p.c_bs + static_cast<int64_t>(row) * p.N + cn, acc[ib][cb][e]);
+                }
+        }
+    } else {
+        uint16_t* const C = static_cast<uint16_t*>(p.C) + (GR ? 0 : z * p.c_bs);
+#pragma unroll
+        for (int cb = 0; cb < (SWI ? 1 : 2); ++cb) {
+            // SwiGLU: block 0 holds the gates, block 1 the ups of output tile
+            // ntw / 2 + u
+            const int nt = ntw + cb + 2 * u;
+            const int cn = (SWI ? (ntw >> 1) + u : nt) * kW4TileN + col;
+            if (nt >= p.Nt || cn >= p.N) continue;
+#pragma unroll
+            for (int ib = 0; ib < 2; ++ib)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int row = m0 + 32 * ib + 8 * (e >> 2) + 4 * h + (e & 3);
+                    if (row >= m_end) continue;
+                    if constexpr (SWI)
+                        C[static_cast<int64_t>(row) * p.N + cn] = f32_to_bf16(swiglu(acc[ib][0][e], acc[ib][1][e]));
+                    else C[static_cast<int64_t>(row) * p.N + cn] = f32_to_bf16(acc[ib][cb][e]);
+                }
+        }
     }
 }
 
@@ -2106,10 +2179,10 @@ __device__ __forceinline__ void mma_tile32(const W4Args& p, uint8_t* mm_lds, int
 template <int BPS, bool GBIG, bool GR, bool SWI, int L, bool SK = false, int RB = 4, bool F32 = false, bool PK = false,
           bool W32 = false>
 __global__ __launch_bounds__(L >= 3 ? 512 : 256, L == 3 ? 1 : 2) void w4_mma_kernel(W4Args p) {
-    static_assert(!W32 || (BPS == 4 && L == 1 && RB == 4 && !F32), "the 32x32x16 tile: bf16 64 x 256 tiles");
+    static_assert(!W32 || (BPS == 4 && L == 1 && RB == 4), "the 32x32x16 tile: 64 x 256 tiles");
     extern __shared__ __attribute__((aligned(1024))) uint8_t mm_lds[];
     auto tile = [&](int bx, int by, int bz, int k0, int k1, int slot) {
-        if constexpr (W32) mma_tile32<GBIG, GR, SWI, PK, SK>(p, mm_lds, bx, by, bz, k0, k1, slot);
+        if constexpr (W32) mma_tile32<GBIG, GR, SWI, PK, SK, F32>(p, mm_lds, bx, by, bz, k0, k1, slot);
         else mma_tile<BPS, GBIG, GR, SWI, L, SK, RB, F32, PK>(p, mm_lds, bx, by, bz, k0, k1, slot);
     };
     if constexpr (!PK) {
@@ -2420,7 +2493,9 @@ void launch_gemv_waves(const W4Args& a, dim3 grid, int W, int bps, hipStream_t s
 // G >= 128 only (one scale group per K tile segment); smaller groups would
 // need four times the activation-sum registers and spill.
 // LDS of the 32x32x16 tile: two activation buffers and two tiles' row sums
+// (bf16 activations; fp32 for the reference interface)
 constexpr size_t kMma32Lds = 2 * 64 * kW4TileK * 2 + 2 * 64 * 4;
+constexpr size_t kMma32F32Lds = 2 * 64 * kW4TileK * 4 + 2 * 64 * 4;
 // the 32x32x16 form of the 64 x 256 bf16 tile (LHQ_W4_W32=0 in a tuning
 // build keeps the 16x16x32 form)
 bool use_w32() {
@@ -2512,6 +2587,18 @@ int launch_mma_f32_rb(const W4Args& a, hipStream_t s, const char* who) {
     const int64_t tiles = ceil_div64(a.M, 16 * RB);
     LHQ_SUPPORTED(tiles <= 65535, "%s: %lld row tiles exceed the grid limit", who, static_cast<long long>(tiles));
     const dim3 grid(ceil_div(a.Nt, WN * MM_CT), static_cast<unsigned>(tiles), 1);
+    if constexpr (L == 1 && RB == 4) {
+        if (use_w32()) {
+            if (a.gmul) {
+                allow_cu_lds<&w4_mma_kernel<4, true, false, false, 1, false, 4, true, false, true>>();
+                w4_mma_kernel<4, true, false, false, 1, false, 4, true, false, true><<<grid, 256, kMma32F32Lds, s>>>(a);
+            } else {
+                allow_cu_lds<&w4_mma_kernel<4, false, false, false, 1, false, 4, true, false, true>>();
+                w4_mma_kernel<4, false, false, false, 1, false, 4, true, false, true><<<grid, 256, kMma32F32Lds, s>>>(a);
+            }
+            return check_launch(who);
+        }
+    }
     if (a.gmul) {
         allow_cu_lds<&w4_mma_kernel<4, true, false, false, L, false, RB, true>>();
         w4_mma_kernel<4, true, false, false, L, false, RB, true><<<grid, 64 * NW, lds, s>>>(a);
@@ -3054,6 +3141,18 @@ void launch_split_f32_rb(const W4Args& a, unsigned splits, hipStream_t s) {
     constexpr int UPW = 4 * RB / (NW / NK), PS = UPW >= 4 ? 1 : 4 / UPW;
     constexpr size_t lds = 2 * a_bytes + static_cast<size_t>(NK) * RB * PS * 64 * 16;  // tiles, partial sums
     const dim3 grid(ceil_div(a.Nt, WN * MM_CT), ceil_div(a.M, 16 * RB), splits);
+    if constexpr (L == 1 && RB == 4) {
+        if (use_w32()) {
+            if (a.gmul) {
+                allow_cu_lds<&w4_mma_kernel<4, true, false, false, 1, true, 4, true, false, true>>();
+                w4_mma_kernel<4, true, false, false, 1, true, 4, true, false, true><<<grid, 256, kMma32F32Lds, s>>>(a);
+            } else {
+                allow_cu_lds<&w4_mma_kernel<4, false, false, false, 1, true, 4, true, false, true>>();
+                w4_mma_kernel<4, false, false, false, 1, true, 4, true, false, true><<<grid, 256, kMma32F32Lds, s>>>(a);
+            }
+            return;
+        }
+    }
     if (a.gmul) {
         allow_cu_lds<&w4_mma_kernel<4, true, false, false, L, true, RB, true>>();
         w4_mma_kernel<4, true, false, false, L, true, RB, true><<<grid, 64 * NW, lds, s>>>(a);
