@@ -2475,9 +2475,17 @@ void launch_gemv_bps(const W4Args& a, dim3 grid, int bps, hipStream_t s) {
 template <bool F32A, bool ASYM, bool F32C, int T, int NPW, int MR>
 void launch_i8_mr(const W4Args& a, dim3 grid, int S, size_t lds, hipStream_t s) {
     lds = std::max(lds, static_cast<size_t>(S) * T * MR * 64 * sizeof(float));  // the reduction reuses it
-    if (a.G == 64) w4_decode_i8_kernel<F32A, ASYM, F32C, T, NPW, 2, false, MR><<<grid, 64 * S, lds, s>>>(a);
-    else if (a.gmul) w4_decode_i8_kernel<F32A, ASYM, F32C, T, NPW, 4, true, MR><<<grid, 64 * S, lds, s>>>(a);
-    else w4_decode_i8_kernel<F32A, ASYM, F32C, T, NPW, 4, false, MR><<<grid, 64 * S, lds, s>>>(a);
+    const bool big = lds > 64 * 1024;  // one workgroup per CU (the launch checks the grid)
+    if (a.G == 64) {
+        if (big) allow_cu_lds<&w4_decode_i8_kernel<F32A, ASYM, F32C, T, NPW, 2, false, MR>>();
+        w4_decode_i8_kernel<F32A, ASYM, F32C, T, NPW, 2, false, MR><<<grid, 64 * S, lds, s>>>(a);
+    } else if (a.gmul) {
+        if (big) allow_cu_lds<&w4_decode_i8_kernel<F32A, ASYM, F32C, T, NPW, 4, true, MR>>();
+        w4_decode_i8_kernel<F32A, ASYM, F32C, T, NPW, 4, true, MR><<<grid, 64 * S, lds, s>>>(a);
+    } else {
+        if (big) allow_cu_lds<&w4_decode_i8_kernel<F32A, ASYM, F32C, T, NPW, 4, false, MR>>();
+        w4_decode_i8_kernel<F32A, ASYM, F32C, T, NPW, 4, false, MR><<<grid, 64 * S, lds, s>>>(a);
+    }
 }
 
 template <bool F32A, bool ASYM, bool F32C, int T, bool GR, bool SWI = false>
@@ -2672,14 +2680,19 @@ int launch_w4(W4Args a, int batch, hipStream_t s, int mblocks = -1) {
     // N=11008), G = 64 or a multiple of 128, digit planes and block table
     // within the LDS budget (LHQ_W4_I8=-1 disables).
     const size_t i8_lds = static_cast<size_t>(a.Kt) * (3 * kW4TileK + 16);
+    // Up to 64 KiB of digit planes always; up to 96 KiB (K up to 31,488) with
+    // two column tiles per wave where the workgroups then fit one per CU
+    // (K=28672, N=8192: 256 workgroups)
+    const bool i8_big = i8_lds > static_cast<size_t>(kDecodeMaxLds) && i8_lds <= static_cast<size_t>(kDecodeBigLds) &&
+                        static_cast<int64_t>(ceil_div(a.Nt, 2)) * batch <= device_cus();
     if (!GR && mblocks == 1 && a.M == 1 && env_i8 >= 0 && (a.G == 64 || a.G % kW4TileK == 0) &&
-        i8_lds <= static_cast<size_t>(kDecodeMaxLds)) {
+        (i8_lds <= static_cast<size_t>(kDecodeMaxLds) || i8_big)) {
         // one column tile per wave: measured at K=8192, N=28672 (1792 column
         // tiles) 21.7 us against 22.4 us with two; with fp32 activations and
         // output 21.3 against 22.6 us (N=11008: 7.5 against 8.6 us), and
         // 26.3 us with eight waves per workgroup instead of four
-        int T = 1;
-        if (env_dt == 1 || env_dt == 2) T = env_dt;
+        int T = i8_big ? 2 : 1;
+        if (!i8_big && (env_dt == 1 || env_dt == 2)) T = env_dt;
         const int smax = (T == 1) ? 16 : 8;  // the kernel's launch bounds
         const int64_t cols = static_cast<int64_t>(ceil_div(a.Nt, T)) * batch;
         // and at most 32 K tiles per wave (K = 20480, N = 8192: 8 waves

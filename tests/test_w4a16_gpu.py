@@ -48,6 +48,7 @@ def _sym_case(oracle, ops, M, K, N, G, seed, alpha=1.0, beta=0.0):
     (2, 96, 40, 32),         # K not a multiple of the 128-wide tile
     (7, 4160, 72, 64),
     (16, 28672, 64, 128),    # activations too large to stage: generic kernel
+    (1, 28672, 512, 128),    # integer decode with 88 KiB of digit planes, two column tiles per wave
 ])
 def test_w4a16_f32_matches_oracle(oracle, ops, M, K, N, G):
     got, want = _sym_case(oracle, ops, M, K, N, G, seed=100 + M + K // 64)
