@@ -3051,10 +3051,21 @@ TilePlan plan_thin(const W4Args& a, int64_t ws_cap) {
     // splits; 5 splits, 560 workgroups, 63.4-65.3); N = 14336 34.6-35.2 /
     // 33.0-33.4 (8); K = 4096, N = 28672 34.4-34.7 / 32.0-33.1 (4); K =
     // 28672, N = 28672 179.9-181.1 / 148.3-150.0 (4); 48 rows, K = 8192,
-    // N = 28672 53.3-53.7 / 46.4-48.4 (4).
-    if (env_s == 0 && t.RB == 4 && !(a.Kt >= 128 && S * wgs <= cus)) {
-        const int two = static_cast<int>(std::min<int64_t>(2 * cus / wgs, a.Kt / 8));
-        S = std::max(S, two);
+    // N = 28672 53.3-53.7 / 46.4-48.4 (4).  Where one workgroup per CU
+    // leaves at most 12 K tiles per split, the grid stays at one per CU
+    // (at most one round, none of the CUs running two): M = 64, K = 8192,
+    // N = 10240 (40 column groups) 28.4-29.9 us with 8 splits (320
+    // workgroups), 29.6 with 11, 26.0 with 6; N = 8192 22.7 with 8 (one per
+    // CU), 28.4 with 16.  32-row blocks take the same rule (M = 32, K =
+    // 8192, N = 28672: 3 splits, 336 workgroups, 42.9 us; 4 splits 36.2).
+    if (env_s == 0 && t.RB >= 2 && !(a.Kt >= 128 && S * wgs <= cus)) {
+        const int one = static_cast<int>(std::min<int64_t>(std::max<int64_t>(1, cus / wgs), a.Kt / kSplitMinKt));
+        if (ceil_div(a.Kt, std::max(one, 1)) <= 12) {
+            S = std::max(one, 1);
+        } else {
+            const int two = static_cast<int>(std::min<int64_t>(2 * cus / wgs, a.Kt / 8));
+            S = std::max(S, two);
+        }
     }
     if (env_s >= 1) S = std::min(env_s, a.Kt);
     const int64_t per_split = static_cast<int64_t>(a.M) * a.N * 4;
