@@ -159,8 +159,9 @@ int lhq_gemm_w4a16(const float* A, const uint8_t* qweight, const float* scales,
                    void* stream);
 /* lhq_gemm_w4a16 with a caller workspace (no reference counterpart: the
  * reference's CPU loop needs no partial sums; the lh:: drop-in of
- * gemm_w4a16_groupwise passes one).  At 2..64 rows (group_size a multiple
- * of 128, K % 128 == 0) K is split across workgroups: each split writes fp32
+ * gemm_w4a16_groupwise passes one).  At 2..64 rows, and at 65..512 rows
+ * where the unsplit grid fills at most half the GPU (group_size a multiple
+ * of 128, K % 128 == 0), K is split across workgroups: each split writes fp32
  * partial sums to `workspace`, and a second kernel adds them in split order
  * and applies alpha / beta as lhq_gemm_w4a16 does (deterministic).  The
  * split count is the most the workspace allows, up to
@@ -180,7 +181,8 @@ int lhq_gemm_w4a16_bf16(const uint16_t* A, const uint8_t* qweight, const uint16_
                         int group_size, void* stream);
 /* lhq_gemm_w4a16_bf16 with a caller workspace (no reference counterpart:
  * the reference's CPU loop needs no partial sums).  Where the output grid
- * cannot fill the GPU (2 <= M <= 64 rows, group_size a multiple of 128,
+ * cannot fill the GPU (2 <= M <= 64 rows, or up to 512 rows where the
+ * unsplit grid fills at most half the GPU; group_size a multiple of 128,
  * and weights large enough for the tile kernel), K is split across
  * workgroups: each split writes fp32 partial sums to `workspace` and they
  * are added in split order into C (deterministic).  The split count is

@@ -2986,9 +2986,24 @@ struct TilePlan {
 };
 
 constexpr int kSplitMinKt = 4;  // K tiles per split at least
+constexpr int kThinMaxRows = 512;  // rows a split launch takes at most
+
+// Above 64 rows the split count is capped so that the partial sums (S M N
+// fp32, written and read back) are no larger than the weights' codes
+// (K N / 2 bytes), i.e. 8 S M <= K: measured (us, unsplit / split, bf16)
+// M = 128, K = N = 8192 (8 splits) 50.4 / 33.6; M = 256, K = 8192, N =
+// 4096 (4) 50.8 / 33.0; M = 128, K = 28672, N = 8192 (4) 155 / 83.6; but
+// M = 512, K = N = 4096 (4 splits, partial sums four times the codes)
+// 32.2 / 33.0.
+int cap_split_rows(const W4Args& a, int S, int env_s) {
+    if (a.M <= 64 || env_s >= 1) return S;
+    return static_cast<int>(std::min<int64_t>(S, a.K / (int64_t{8} * a.M)));
+}
 
 // ws_cap: the workspace bytes available (-1: as much as the plan wants).
-// A split applies to 2..64 rows where the tile kernel runs (G >= 128), and
+// A split applies to 2..64 rows where the tile kernel runs (G >= 128) (and
+// to 65..512 rows of 64-row blocks whose grid fills at most half the CUs,
+// cap_split_rows), and
 // where the ordinary launch would be the tile kernel or the weights are
 // large enough (K * N >= 32 Mi) that the 16-row kernel loses to it: measured
 // at M = 32, (K, N) = (4096, 4096) 9.2 us on the 16-row kernel against 12.5
@@ -3006,7 +3021,9 @@ TilePlan plan_thin(const W4Args& a, int64_t ws_cap) {
     const int env_thin = tuning_knob("LHQ_W4_THIN", -1);   // 0: never split
     const int env_s = tuning_knob("LHQ_W4_THIN_S", 0);     // force the split count
     const int env_l = tuning_knob("LHQ_W4_THIN_L", 0);     // force the layout (1..4)
-    if (env_thin == 0 || a.M < 2 || a.M > 64) return t;
+    // (more than 64 rows: 64-row blocks, split only where the unsplit grid
+    // fills at most half the CUs; the rule below)
+    if (env_thin == 0 || a.M < 2 || a.M > tuning_knob("LHQ_W4_THIN_MMAX", kThinMaxRows)) return t;
     if (a.G < kW4TileK || a.K % kW4TileK != 0 || static_cast<int64_t>(a.M) * a.K >= (int64_t{1} << 31)) return t;
     const bool tile = mma_applies(a, a.M, a.M);
     if (!tile && static_cast<int64_t>(a.K) * a.N < (int64_t{32} << 20)) return t;
@@ -3068,6 +3085,7 @@ TilePlan plan_thin(const W4Args& a, int64_t ws_cap) {
         }
     }
     if (env_s >= 1) S = std::min(env_s, a.Kt);
+    S = cap_split_rows(a, S, env_s);
     const int64_t per_split = static_cast<int64_t>(a.M) * a.N * 4;
     if (ws_cap >= 0) S = static_cast<int>(std::min<int64_t>(S, std::max<int64_t>(1, ws_cap / per_split)));
     // splits of equal length: no split ends up empty
@@ -3188,6 +3206,9 @@ void launch_split_f32_rb(const W4Args& a, unsigned splits, hipStream_t s) {
 
 // ws_cap: the workspace bytes available (-1: as much as the plan wants).
 // 16-, 32- or 64-row blocks (RB = 1, 2, 4) on 256-column workgroups (L = 1)
+// (65..512 rows: 64-row blocks where the unsplit grid fills at most half
+// the CUs, cap_split_rows; M = 128, K = N = 8192: 142 / 50.3 us, M = 256
+// 146 / 85.3, M = 256, K = 28672 499 / 241)
 // and S splits that bring the grid to about two workgroups per CU, each
 // walking at least 4 K tiles.  Measured on MI355X (us, lhq_gemm_w4a16 /
 // this split): M = 16, K = 8192, N = 28672 48.6 / 36.4; M = 16, K = 28672,
@@ -3205,7 +3226,7 @@ TilePlan plan_thin_f32(const W4Args& a, int64_t ws_cap) {
     const int env_on = tuning_knob("LHQ_W4_F32_SPLIT", -1);  // 0: never split, 1: split wherever allowed
     const int env_s = tuning_knob("LHQ_W4_F32_SPLIT_S", 0);  // force the split count
     const int env_l = tuning_knob("LHQ_W4_F32_SPLIT_L", 0);  // force the layout (1..3)
-    if (env_on == 0 || a.M < 2 || a.M > 64) return t;
+    if (env_on == 0 || a.M < 2 || a.M > tuning_knob("LHQ_W4_THIN_MMAX", kThinMaxRows)) return t;
     if (a.G < kW4TileK || a.K % kW4TileK != 0 || static_cast<int64_t>(a.M) * a.K >= (int64_t{1} << 31)) return t;
     if (env_on != 1 && a.M <= 16 && static_cast<int64_t>(a.K) * a.N < (int64_t{32} << 20)) return t;
     t.RB = a.M <= 16 ? 1 : a.M <= 32 ? 2 : 4;
@@ -3218,9 +3239,13 @@ TilePlan plan_thin_f32(const W4Args& a, int64_t ws_cap) {
     const int WN = t.L == 1 ? 4 : 2, per_cu = t.L >= 3 ? 1 : 2;
     const int64_t wgs = static_cast<int64_t>(ceil_div(a.Nt, WN * MM_CT)) * ceil_div(a.M, 16 * t.RB);
     const int cus = std::max(device_cus(), 1);
+    // more than 64 rows: only where the unsplit grid fills at most half the
+    // CUs
+    if (env_s == 0 && a.M > 64 && 2 * wgs > cus) return t;
     // about one round of the resident workgroups, at least 4 K tiles each
     int S = static_cast<int>(std::min<int64_t>(std::max<int64_t>(1, per_cu * cus / wgs), a.Kt / kSplitMinKt));
     if (env_s >= 1) S = std::min(env_s, a.Kt);
+    S = cap_split_rows(a, S, env_s);
     const int64_t per_split = static_cast<int64_t>(a.M) * a.N * 4;
     if (ws_cap >= 0) S = static_cast<int>(std::min<int64_t>(S, std::max<int64_t>(1, ws_cap / per_split)));
     const int kps = ceil_div(a.Kt, std::max(S, 1));

@@ -101,7 +101,8 @@ def test_workspace_queries_on_the_host(L):
     ask for nothing, whatever the device."""
     f32 = L.cdll.lhq_gemm_w4a16_workspace_bytes
     assert f32(1, 28672, 8192, 128) == 0       # one row
-    assert f32(65, 8192, 8192, 128) == 0       # beyond 64 rows
+    assert f32(4096, 8192, 8192, 128) == 0     # a full grid
+    assert f32(513, 8192, 1024, 128) == 0      # beyond 512 rows
     assert f32(16, 4096, 4096, 128) == 0       # 2..16 rows with K * N < 32 Mi
     assert f32(32, 8192, 8192, 64) == 0        # G < 128
     assert f32(16, 8192, 8192, 48) == 0        # a group size the GEMMs reject

@@ -3,7 +3,9 @@ gemm_w4a16_groupwise, gemm_quant.hpp:47-57 / gemm_quant.cpp:54-82) vs the
 CPU oracle.
 
 At 2..64 rows (group size a multiple of 128, K % 128 == 0; at 2..16 rows
-only where K * N >= 32 Mi) K is split across workgroups: each split writes
+only where K * N >= 32 Mi), and at 65..512 rows where the unsplit grid fills
+at most half the GPU (with at most K / (8 M) splits), K is split across
+workgroups: each split writes
 fp32 partial sums to the workspace, and a second kernel adds them in split
 order and applies alpha / beta as the reference does (beta == 0 never reads
 C).  Checked: 16-, 32- and 64-row blocks with ragged M and N, split
@@ -65,6 +67,9 @@ def _run(ops, A, w, C0, alpha, beta, ws_bytes, fill=None):
     (33, 1152, 512, 128, 1.0, 0.0),        # 64-row blocks, 33 live rows, 9 K tiles
     (48, 4096, 1024, 128, 1.0, 1.0),
     (64, 8192, 512, 128, 0.5, 0.0),        # config 5 K
+    (80, 8192, 1024, 128, 1.0, 0.0),       # 65..512 rows: two row tiles, 16 live rows in the second
+    (200, 4096, 1536, 256, 0.5, 1.0),      # four row tiles, G = 256, alpha / beta, 2 splits (K / (8 M))
+    (130, 16384, 520, 128, 1.0, 0.0),      # ragged N, odd K tiles per split
 ])
 def test_f32_splitk_matches_oracle(oracle, ops, M, K, N, G, alpha, beta):
     A, w, C0, want = _case(oracle, ops, M, K, N, G, seed=2100 + M + K // 128, alpha=alpha, beta=beta)
@@ -105,7 +110,8 @@ def test_f32_splitk_workspace_bytes_rules(ops):
     def f(M, K, N, G):
         return _ws_bytes(ops, M, K, N, G)
     assert f(1, 8192, 28672, 128) == 0       # one row: no split
-    assert f(65, 8192, 8192, 128) == 0       # beyond 64 rows
+    assert f(513, 8192, 1024, 128) == 0      # beyond 512 rows
+    assert f(4096, 8192, 8192, 128) == 0     # a full grid
     assert f(0, 8192, 8192, 128) == 0
     assert f(16, 4096, 4096, 128) == 0       # 2..16 rows with K * N < 32 Mi
     assert f(2, 4096, 4096, 128) == 0
@@ -118,6 +124,9 @@ def test_f32_splitk_workspace_bytes_rules(ops):
     if torch.cuda.get_device_properties(0).multi_processor_count == 256:
         assert f(16, 8192, 28672, 128) == 4 * 16 * 28672 * 4
         assert f(64, 8192, 8192, 128) == 16 * 64 * 8192 * 4   # 32 groups, 16 splits of 4 K tiles
+        assert f(128, 8192, 8192, 128) == 8 * 128 * 8192 * 4  # 64 workgroups unsplit, 8 splits (K / (8 M))
+        assert f(512, 8192, 8192, 128) == 0   # 256 workgroups unsplit: more than half the CUs
+        assert f(512, 4096, 4096, 128) == 0   # K / (8 M) = 1
 
 
 def test_f32_splitk_in_a_captured_hip_graph(oracle, ops):

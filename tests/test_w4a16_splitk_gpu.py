@@ -1,7 +1,9 @@
 """W4A16 with a caller workspace (lhq_gemm_w4a16_bf16_ws) vs the CPU oracle.
 
-At 2..64 rows the tile kernel's output grid cannot fill the GPU, so K is
-split across workgroups: each split writes fp32 partial sums to the
+At 2..64 rows the tile kernel's output grid cannot fill the GPU, nor at
+65..512 rows where it fills at most half the CUs (there with at most
+K / (8 M) splits), so K is split across workgroups: each split writes fp32
+partial sums to the
 workspace and a second kernel adds them in split order.  Checked here: the
 three row-block forms (16, 32 and 64 rows per wave; 16-row blocks, and 32-
 or 64-row blocks at K >= 16384, with K in two halves inside the workgroup),
@@ -55,6 +57,9 @@ def _case(oracle, ops, M, K, N, G, seed):
     (64, 4096, 4104, 128),    # ragged N at 64 rows
     (24, 16384, 2064, 128),   # K >= 16384: 32-row blocks, K halves in the workgroup, odd K tiles per split
     (64, 16384, 1040, 128),   # K >= 16384: 64-row blocks, K halves in the workgroup, ragged N
+    (100, 8192, 2048, 128),   # 65..512 rows: two row tiles, 36 live rows in the second, K / (8 M) splits
+    (256, 8192, 4104, 128),   # four row tiles, ragged N
+    (72, 16384, 1024, 256),   # K halves in the workgroup, G = 256
 ])
 def test_splitk_matches_oracle(oracle, ops, M, K, N, G):
     A, w, want = _case(oracle, ops, M, K, N, G, seed=700 + M + N)
@@ -111,6 +116,10 @@ def test_splitk_workspace_bytes_rules(ops):
     assert f(64, 8192, 14336, 128) == 8 * 64 * 14336 * 4  # two workgroups per CU, 8 K tiles each
     assert f(64, 8192, 28672, 128) == 4 * 64 * 28672 * 4  # 448 workgroups, not 560
     assert f(64, 8192, 57344, 128) == 0      # more than half a CU's worth of column groups
+    assert f(128, 8192, 8192, 128) == 8 * 128 * 8192 * 4  # 64 workgroups unsplit: 8 splits (K / (8 M))
+    assert f(512, 8192, 8192, 128) == 0      # 256 workgroups unsplit: more than half the CUs
+    assert f(512, 4096, 4096, 128) == 0      # K / (8 M) = 1
+    assert f(513, 8192, 1024, 128) == 0      # beyond 512 rows
 
 
 @pytest.mark.parametrize("M,K,N,G", [(4, 4096, 4096, 128), (64, 4160, 1024, 64)])
