@@ -160,7 +160,7 @@ int lhq_gemm_w4a16(const float* A, const uint8_t* qweight, const float* scales,
 /* lhq_gemm_w4a16 with a caller workspace (no reference counterpart: the
  * reference's CPU loop needs no partial sums; the lh:: drop-in of
  * gemm_w4a16_groupwise passes one).  At 2..64 rows, and at 65..512 rows
- * where the unsplit grid fills at most half the GPU (group_size a multiple
+ * where the unsplit grid leaves a CU idle (group_size a multiple
  * of 128, K % 128 == 0), K is split across workgroups: each split writes fp32
  * partial sums to `workspace`, and a second kernel adds them in split order
  * and applies alpha / beta as lhq_gemm_w4a16 does (deterministic).  The

@@ -3239,9 +3239,11 @@ TilePlan plan_thin_f32(const W4Args& a, int64_t ws_cap) {
     const int WN = t.L == 1 ? 4 : 2, per_cu = t.L >= 3 ? 1 : 2;
     const int64_t wgs = static_cast<int64_t>(ceil_div(a.Nt, WN * MM_CT)) * ceil_div(a.M, 16 * t.RB);
     const int cus = std::max(device_cus(), 1);
-    // more than 64 rows: only where the unsplit grid fills at most half the
-    // CUs
-    if (env_s == 0 && a.M > 64 && 2 * wgs > cus) return t;
+    // more than 64 rows: only where the unsplit grid leaves a CU without a
+    // workgroup (M = 128, K = 8192, N = 28672, 224 workgroups: 154-162 us
+    // unsplit, 139-140 with 2 splits; the bf16 form gains nothing there and
+    // splits only grids of at most half the CUs)
+    if (env_s == 0 && a.M > 64 && wgs > cus) return t;
     // about one round of the resident workgroups, at least 4 K tiles each
     int S = static_cast<int>(std::min<int64_t>(std::max<int64_t>(1, per_cu * cus / wgs), a.Kt / kSplitMinKt));
     if (env_s >= 1) S = std::min(env_s, a.Kt);

@@ -3,8 +3,8 @@ gemm_w4a16_groupwise, gemm_quant.hpp:47-57 / gemm_quant.cpp:54-82) vs the
 CPU oracle.
 
 At 2..64 rows (group size a multiple of 128, K % 128 == 0; at 2..16 rows
-only where K * N >= 32 Mi), and at 65..512 rows where the unsplit grid fills
-at most half the GPU (with at most K / (8 M) splits), K is split across
+only where K * N >= 32 Mi), and at 65..512 rows where the unsplit grid
+leaves a CU idle (with at most K / (8 M) splits), K is split across
 workgroups: each split writes
 fp32 partial sums to the workspace, and a second kernel adds them in split
 order and applies alpha / beta as the reference does (beta == 0 never reads
@@ -125,7 +125,8 @@ def test_f32_splitk_workspace_bytes_rules(ops):
         assert f(16, 8192, 28672, 128) == 4 * 16 * 28672 * 4
         assert f(64, 8192, 8192, 128) == 16 * 64 * 8192 * 4   # 32 groups, 16 splits of 4 K tiles
         assert f(128, 8192, 8192, 128) == 8 * 128 * 8192 * 4  # 64 workgroups unsplit, 8 splits (K / (8 M))
-        assert f(512, 8192, 8192, 128) == 0   # 256 workgroups unsplit: more than half the CUs
+        assert f(512, 8192, 8192, 128) == 2 * 512 * 8192 * 4  # 256 workgroups unsplit: 2 splits
+        assert f(1024, 8192, 8192, 128) == 0  # 512 workgroups unsplit
         assert f(512, 4096, 4096, 128) == 0   # K / (8 M) = 1
 
 
