@@ -1133,6 +1133,126 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm8_skinny_kernel(Gemm8Args p
     }
 }
 
+// ---------------------------------------------------------------------------
+// Mid-size int8 kernel (W8A8 with 16 < M <= kMidMaxM: batched decode).
+// There the 256x256 tile kernel runs ceil(N/256) workgroups -- 56 at N =
+// 14336, under a quarter of the CUs -- each walking all of K, and the rows
+// past M are MFMA work for nothing.  Here a 64 W-thread workgroup owns an
+// output block of RB 16-row blocks by T 16-column tiles and its W waves
+// split K; per 64-deep k step a lane loads 16 contiguous k bytes of each of
+// its T B^T columns and RB A rows (1 KiB loads per wave), and RB * T
+// v_mfma_i32_16x16x64_i8 accumulate the blocks (rows past M read row M-1,
+// their outputs are not stored; k past K reads the row's last 16 bytes, B^T
+// is zero there).  BATCH k steps are loaded before they are consumed.
+// Waves 1.. hand their int32 blocks to wave 0 through LDS, which adds them
+// (integer addition: the reference's accumulator exactly) and writes the
+// skinny kernel's epilogue.
+// ---------------------------------------------------------------------------
+constexpr int kMidMaxM = 32;
+
+// RB 16-row blocks by T 16-column tiles per workgroup, W waves splitting K,
+// BATCH k steps loaded before they are consumed, MINW workgroups per CU in
+// the register budget
+template <int EPI, int RB = 4, int T = 4, int W = 4, int BATCH = 4, int MINW = 2>
+__global__ __launch_bounds__(64 * W, MINW) void gemm8_mid_kernel(Gemm8Args p) {
+    static_assert((W - 1) * RB * T * 64 * 16 <= 60 * 1024, "reduction area");
+    __shared__ i32x4_t red[W - 1][RB * T][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n0 = blockIdx.x * 16 * T, m0 = blockIdx.y * 16 * RB;
+    const int kl = 16 * (lane >> 4);  // this lane's 16 k within a 64-deep step
+    const int steps = p.Kp / 64;
+    const int per = (steps + W - 1) / W;
+    const int s0 = min(wave * per, steps), s1 = min(s0 + per, steps);
+    const uint8_t* a_row[RB];
+    const uint8_t* b_col[T];
+    // rows past M read row M-1; columns n0 + 16 t + (lane & 15) < Np (B^T
+    // rows are zero-padded to a multiple of 256 >= ceil(N / (16 T)) * 16 T)
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+        a_row[i] = p.A + static_cast<size_t>(min(m0 + 16 * i + (lane & 15), p.M - 1)) * p.K;
+#pragma unroll
+    for (int t = 0; t < T; ++t) b_col[t] = p.Bt + static_cast<size_t>(n0 + 16 * t + (lane & 15)) * p.Kp;
+
+    i32x4_t acc[RB][T];
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[i][t] = i32x4_t{0, 0, 0, 0};
+    for (int sb = s0; sb < s1; sb += BATCH) {
+        u32x4_t a[BATCH][RB], b[BATCH][T];
+#pragma unroll
+        for (int u = 0; u < BATCH; ++u) {
+            // steps past this wave's range re-read its last one (discarded)
+            const int k = min(sb + u, s1 - 1) * 64 + kl;
+#pragma unroll
+            for (int i = 0; i < RB; ++i) a[u][i] = *reinterpret_cast<const u32x4_t*>(a_row[i] + min(k, p.K - 16));
+#pragma unroll
+            for (int t = 0; t < T; ++t) b[u][t] = *reinterpret_cast<const u32x4_t*>(b_col[t] + k);
+        }
+#pragma unroll
+        for (int u = 0; u < BATCH; ++u)
+            if (sb + u < s1)
+#pragma unroll
+                for (int i = 0; i < RB; ++i)
+#pragma unroll
+                    for (int t = 0; t < T; ++t) acc[i][t] = mfma_i8_16x16x64(a[u][i], b[u][t], acc[i][t]);
+    }
+    if (wave > 0) {
+#pragma unroll
+        for (int i = 0; i < RB; ++i)
+#pragma unroll
+            for (int t = 0; t < T; ++t) red[wave - 1][i * T + t][lane] = acc[i][t];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int w = 0; w < W - 1; ++w)
+#pragma unroll
+        for (int i = 0; i < RB; ++i)
+#pragma unroll
+            for (int t = 0; t < T; ++t) acc[i][t] += red[w][i * T + t][lane];
+
+    // D element j of block (i, t) in lane l: row m0 + 16 i + 4 (l >> 4) + j,
+    // column n0 + 16 t + (l & 15)
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        const int c = n0 + 16 * t + (lane & 15);
+        if (c >= p.N) continue;
+        float bs = 0.0f;
+        if constexpr (EPI != EPI_I32) bs = p.Bs[c];
+#pragma unroll
+        for (int i = 0; i < RB; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int r = m0 + 16 * i + 4 * (lane >> 4) + j;
+                if (r >= p.M) continue;
+                const size_t o = static_cast<size_t>(r) * p.N + c;
+                if constexpr (EPI == EPI_I32) {
+                    static_cast<int32_t*>(p.C)[o] = acc[i][t][j];
+                } else {
+                    float f = p.alpha * p.As[r];  // gemm_quant.cpp:44-46, left to right
+                    f = f * bs;
+                    f = f * static_cast<float>(acc[i][t][j]);
+                    if constexpr (EPI == EPI_F32) {
+                        // apply_beta (gemm_quant.cpp:12-21), then C += rescaled
+                        float* Cp = static_cast<float*>(p.C);
+                        const float base = (p.beta == 0.0f) ? 0.0f : (p.beta == 1.0f) ? Cp[o] : Cp[o] * p.beta;
+                        Cp[o] = base + f;
+                    } else {
+                        static_cast<uint16_t*>(p.C)[o] = f32_to_bf16(0.0f + f);
+                    }
+                }
+            }
+    }
+}
+
+template <int EPI, int RB, int T, int W, int BATCH, int MINW>
+void launch_mid(const Gemm8Args& p, void* stream) {
+    const dim3 grid(ceil_div(p.N, 16 * T), ceil_div(p.M, 16 * RB));
+    gemm8_mid_kernel<EPI, RB, T, W, BATCH, MINW><<<grid, 64 * W, 0, as_stream(stream)>>>(p);
+}
+
 int env_int(const char* name, int dflt) { return tuning_knob(name, dflt); }
 
 // Compute units of the current device (one persistent workgroup each).
@@ -1159,6 +1279,14 @@ int launch_dma(const Gemm8Args& p, int tiles, void* stream, const char* who) {
     // (256 accumulator registers per wave, ~130 KiB of LDS).
     static const int persist = env_int("LHQ_GEMM8_PERSIST", 1);
     static const int cus = device_cus();
+    // bf16 tiles filling at most half the CUs: every workgroup a 256 x 128
+    // half tile (the persistent loop with no whole round), twice the
+    // workgroups
+    static const int halves = env_int("LHQ_GEMM8_HALVES", 1);
+    if (EPI == EPI_BF16 && halves && cus > 0 && 2 * tiles <= cus) {
+        gemm8_dma_kernel<EPI, STAGES, M16><<<2 * tiles, NTHREADS, lds, as_stream(stream)>>>(p);
+        return check_launch(who);
+    }
     const int G = cus;
     const int rem = G > 0 ? tiles % G : 0;
     if (EPI == EPI_BF16 && persist && G > 0 && G % 8 == 0 && tiles > G && rem != 0 && 2 * rem <= G) {
@@ -1215,6 +1343,28 @@ int launch_gemm8(const uint8_t* A, const uint8_t* Bt, const float* As, const flo
     if constexpr (OP == OP_I8) {
         if (use_skinny && M <= 16) {
             gemm8_skinny_kernel<EPI><<<ceil_div(N, 16), 64 * SK_WAVES, 0, as_stream(stream)>>>(p);
+            return check_launch(who);
+        }
+        static const int mid_max = env_int("LHQ_GEMM8_MID", kMidMaxM);  // largest M for the mid-size kernel
+        if (M <= mid_max) {
+#ifdef LHQ_TUNING_KNOBS
+            static const int mid_form = env_int("LHQ_GEMM8_MID_FORM", 0);
+            switch (mid_form) {
+                case 1: launch_mid<EPI, 4, 2, 4, 4, 2>(p, stream); return check_launch(who);
+                case 2: launch_mid<EPI, 2, 4, 4, 4, 2>(p, stream); return check_launch(who);
+                case 3: launch_mid<EPI, 2, 2, 8, 4, 2>(p, stream); return check_launch(who);
+                case 4: launch_mid<EPI, 2, 4, 8, 2, 1>(p, stream); return check_launch(who);
+                case 5: launch_mid<EPI, 4, 1, 4, 8, 2>(p, stream); return check_launch(who);
+                case 6: launch_mid<EPI, 2, 2, 4, 8, 2>(p, stream); return check_launch(who);
+                default: break;
+            }
+#endif
+            // 32 x 32 blocks, eight k steps per batch: M = 17 19.5-19.7 us,
+            // M = 32 23.2 (K = 4096, N = 14336), against 24.5 / 26.3 for 64 x
+            // 64 blocks and 42.6 / 43.4 on whole tiles.  From 33 rows the tile
+            // kernel's half tiles match or beat 64 x 64 blocks (M = 48: 29.4
+            // here; M = 65 on half tiles 29.9, M = 64 here 32.4)
+            launch_mid<EPI, 2, 2, 4, 8, 2>(p, stream);
             return check_launch(who);
         }
 #ifdef LHQ_TUNING_KNOBS

@@ -31,7 +31,9 @@ def _quantized(oracle, M, K, N, seed, lo=-1.0, hi=1.0):
 SHAPES = [(32, 64, 48), (1, 4096, 4096), (255, 256, 257), (256, 512, 256), (300, 1024, 520),
           (16, 208, 100), (7, 4096, 1000), (2, 48, 17),  # skinny kernel (M <= 16)
           (513, 128, 1000), (4, 16, 4),
-          (300, 1040, 520)]  # K % 128 != 0 over several stages: the tile's clamped A loads meet zero-padded B
+          (300, 1040, 520),  # K % 128 != 0 over several stages: the tile's clamped A loads meet zero-padded B
+          # mid-size kernel (16 < M <= 32, 32 x 32 blocks), then whole or half tiles
+          (17, 4096, 1000), (24, 64, 70), (33, 1040, 130), (128, 2048, 2064), (100, 64, 70)]
 
 
 @pytest.mark.parametrize("M,K,N", SHAPES)
@@ -71,7 +73,10 @@ def test_w8a8_f32_bitexact(oracle, ops, M, K, N, alpha, beta):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
-@pytest.mark.parametrize("M,K,N", [(64, 512, 384), (512, 1024, 512)])
+@pytest.mark.parametrize("M,K,N", [(64, 512, 384), (512, 1024, 512),
+                                   (20, 4096, 14336),   # mid-size kernel, 32 x 32 blocks
+                                   (96, 1024, 3000),    # 12 tiles: every workgroup a 256 x 128 half tile
+                                   (200, 2048, 3000)])  # (and 200 live rows of 256)
 def test_w8a8_bf16_bitexact(oracle, ops, M, K, N):
     X = D.to_bf16_bits(oracle, D.with_outliers(D.normal((M, K), 1.0, 11), 0.001, 20.0, 12))
     Aq, As = oracle.q8_quantize_per_row_bf16(X)
