@@ -910,8 +910,16 @@ __global__ __launch_bounds__(NTHREADS) void gemm8_dma_kernel(Gemm8Args p) {
     typename std::conditional<M16, i32x4_t[8][8], i32x16_t[4][4]>::type acc;
     if constexpr (EPI != EPI_BF16) {
         // fp32 / int32 outputs keep one tile per workgroup: their epilogues
-        // need more registers than a persistent loop leaves without spills
+        // need more registers than a persistent loop leaves without spills.
+        // A launch of twice the tiles: every workgroup one 256 x 128 half
+        // tile
         int tm, tn;
+        if (G == 2 * total) {
+            tile_of_id(b >> 1, p, tm, tn);
+            if constexpr (M16) dma_tile_m16<EPI, 2>(p, ds_lds, tm * BM, tn * BN + (b & 1) * (BN / 2), acc);
+            else dma_tile<EPI, STAGES, 2>(p, ds_lds, tm * BM, tn * BN + (b & 1) * (BN / 2), acc);
+            return;
+        }
         tile_of(b, p, tm, tn);
         if constexpr (M16) dma_tile_m16<EPI, 4>(p, ds_lds, tm * BM, tn * BN, acc);
         else dma_tile<EPI, STAGES, 4>(p, ds_lds, tm * BM, tn * BN, acc);
@@ -1279,11 +1287,10 @@ int launch_dma(const Gemm8Args& p, int tiles, void* stream, const char* who) {
     // (256 accumulator registers per wave, ~130 KiB of LDS).
     static const int persist = env_int("LHQ_GEMM8_PERSIST", 1);
     static const int cus = device_cus();
-    // bf16 tiles filling at most half the CUs: every workgroup a 256 x 128
-    // half tile (the persistent loop with no whole round), twice the
-    // workgroups
+    // tiles filling at most half the CUs: every workgroup a 256 x 128 half
+    // tile, twice the workgroups
     static const int halves = env_int("LHQ_GEMM8_HALVES", 1);
-    if (EPI == EPI_BF16 && halves && cus > 0 && 2 * tiles <= cus) {
+    if (halves && cus > 0 && 2 * tiles <= cus) {
         gemm8_dma_kernel<EPI, STAGES, M16><<<2 * tiles, NTHREADS, lds, as_stream(stream)>>>(p);
         return check_launch(who);
     }
