@@ -1157,14 +1157,21 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm8_skinny_kernel(Gemm8Args p
 // skinny kernel's epilogue.
 // ---------------------------------------------------------------------------
 constexpr int kMidMaxM = 32;
+constexpr int kMidMaxFp8M = 128;
 
 // RB 16-row blocks by T 16-column tiles per workgroup, W waves splitting K,
 // BATCH k steps loaded before they are consumed, MINW workgroups per CU in
 // the register budget
-template <int EPI, int RB = 4, int T = 4, int W = 4, int BATCH = 4, int MINW = 2>
+// OP_FP8 (gemm_fp8_e4m3, K % 128 == 0): fp32 accumulators, each 16-byte
+// operand feeding two v_mfma_f32_16x16x32_fp8_fp8 (its low and high 8
+// bytes), the waves' partial blocks added in wave order, and the tile
+// kernel's fp8 epilogue.
+template <int EPI, int RB = 4, int T = 4, int W = 4, int BATCH = 4, int MINW = 2, int OP = OP_I8>
 __global__ __launch_bounds__(64 * W, MINW) void gemm8_mid_kernel(Gemm8Args p) {
     static_assert((W - 1) * RB * T * 64 * 16 <= 60 * 1024, "reduction area");
-    __shared__ i32x4_t red[W - 1][RB * T][64];
+    static_assert(OP == OP_I8 || EPI == EPI_F32, "fp8: fp32 output");
+    using Acc = typename std::conditional<OP == OP_I8, i32x4_t, f32x4_t>::type;
+    __shared__ Acc red[W - 1][RB * T][64];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n0 = blockIdx.x * 16 * T, m0 = blockIdx.y * 16 * RB;
@@ -1182,11 +1189,11 @@ __global__ __launch_bounds__(64 * W, MINW) void gemm8_mid_kernel(Gemm8Args p) {
 #pragma unroll
     for (int t = 0; t < T; ++t) b_col[t] = p.Bt + static_cast<size_t>(n0 + 16 * t + (lane & 15)) * p.Kp;
 
-    i32x4_t acc[RB][T];
+    Acc acc[RB][T];
 #pragma unroll
     for (int i = 0; i < RB; ++i)
 #pragma unroll
-        for (int t = 0; t < T; ++t) acc[i][t] = i32x4_t{0, 0, 0, 0};
+        for (int t = 0; t < T; ++t) acc[i][t] = Acc{};
     for (int sb = s0; sb < s1; sb += BATCH) {
         u32x4_t a[BATCH][RB], b[BATCH][T];
 #pragma unroll
@@ -1204,7 +1211,18 @@ __global__ __launch_bounds__(64 * W, MINW) void gemm8_mid_kernel(Gemm8Args p) {
 #pragma unroll
                 for (int i = 0; i < RB; ++i)
 #pragma unroll
-                    for (int t = 0; t < T; ++t) acc[i][t] = mfma_i8_16x16x64(a[u][i], b[u][t], acc[i][t]);
+                    for (int t = 0; t < T; ++t) {
+                        if constexpr (OP == OP_I8) {
+                            acc[i][t] = mfma_i8_16x16x64(a[u][i], b[u][t], acc[i][t]);
+                        } else {
+                            // k 16 g .. + 7 of the step, then + 8 .. + 15, in
+                            // every lane group g (A and B alike)
+                            acc[i][t] = mfma_fp8_16x16x32(u32x2_t{a[u][i][0], a[u][i][1]},
+                                                          u32x2_t{b[u][t][0], b[u][t][1]}, acc[i][t]);
+                            acc[i][t] = mfma_fp8_16x16x32(u32x2_t{a[u][i][2], a[u][i][3]},
+                                                          u32x2_t{b[u][t][2], b[u][t][3]}, acc[i][t]);
+                        }
+                    }
     }
     if (wave > 0) {
 #pragma unroll
@@ -1223,6 +1241,28 @@ __global__ __launch_bounds__(64 * W, MINW) void gemm8_mid_kernel(Gemm8Args p) {
 
     // D element j of block (i, t) in lane l: row m0 + 16 i + 4 (l >> 4) + j,
     // column n0 + 16 t + (l & 15)
+    if constexpr (OP == OP_FP8) {
+        float combined = p.alpha * p.As[0];  // gemm_quant.cpp:98
+        combined = combined * p.Bs[0];
+        float* Cp = static_cast<float*>(p.C);
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const int c = n0 + 16 * t + (lane & 15);
+            if (c >= p.N) continue;
+#pragma unroll
+            for (int i = 0; i < RB; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int r = m0 + 16 * i + 4 * (lane >> 4) + j;
+                    if (r >= p.M) continue;
+                    const size_t o = static_cast<size_t>(r) * p.N + c;
+                    // apply_beta (gemm_quant.cpp:12-21), then C += rescaled
+                    const float base = (p.beta == 0.0f) ? 0.0f : (p.beta == 1.0f) ? Cp[o] : Cp[o] * p.beta;
+                    Cp[o] = base + combined * acc[i][t][j];
+                }
+        }
+        return;
+    }
 #pragma unroll
     for (int t = 0; t < T; ++t) {
         const int c = n0 + 16 * t + (lane & 15);
@@ -1255,10 +1295,10 @@ __global__ __launch_bounds__(64 * W, MINW) void gemm8_mid_kernel(Gemm8Args p) {
     }
 }
 
-template <int EPI, int RB, int T, int W, int BATCH, int MINW>
+template <int EPI, int RB, int T, int W, int BATCH, int MINW, int OP = OP_I8>
 void launch_mid(const Gemm8Args& p, void* stream) {
     const dim3 grid(ceil_div(p.N, 16 * T), ceil_div(p.M, 16 * RB));
-    gemm8_mid_kernel<EPI, RB, T, W, BATCH, MINW><<<grid, 64 * W, 0, as_stream(stream)>>>(p);
+    gemm8_mid_kernel<EPI, RB, T, W, BATCH, MINW, OP><<<grid, 64 * W, 0, as_stream(stream)>>>(p);
 }
 
 int env_int(const char* name, int dflt) { return tuning_knob(name, dflt); }
@@ -1345,6 +1385,18 @@ int launch_gemm8(const uint8_t* A, const uint8_t* Bt, const float* As, const flo
     static const int use_dma = env_int("LHQ_GEMM8_DMA", 1);
     static const int use_skinny = env_int("LHQ_GEMM8_SKINNY", 1);
     if constexpr (OP == OP_FP8) {
+        // up to 128 rows (K % 128 == 0): the mid-size kernel, 32 x 32 blocks
+        // up to 32 rows, then 64 x 64 (the fp8 tile has no half tiles).
+        // K = 4096, N = 14336 (us, whole tiles / here): M = 1 40.9 / 15.9,
+        // M = 17 42.1 / 19.2, M = 32 44.2 / 22.9, M = 64 48.9 / 34.9, M = 128
+        // 55.4 / 46.9; a 16 x 16 block on 8 waves at M <= 16 measured 15.0 /
+        // 18.1 / 21.0 at M = 1 / 8 / 16 against 15.9 / 17.6 / 18.9
+        static const int fp8_mid_max = env_int("LHQ_GEMM8_FP8_MID", kMidMaxFp8M);
+        if (M <= fp8_mid_max && K % BK == 0) {
+            if (M <= 32) launch_mid<EPI_F32, 2, 2, 4, 8, 2, OP_FP8>(p, stream);
+            else launch_mid<EPI_F32, 4, 4, 4, 4, 2, OP_FP8>(p, stream);
+            return check_launch(who);
+        }
         if (use_dma && K % BK == 0) return launch_fp8_dma<DS_STAGES>(p, tiles, stream, who);
     }
     if constexpr (OP == OP_I8) {
