@@ -679,7 +679,7 @@ def bench_w8_gemv(ops, steps, warmup, seed=0, K=4096, N=4096, min_rotate_bytes=2
     p50, p90 = t_gemv.chunk_percentiles(steps)
     us_step = ms_step * 1e3 / steps
     us_gemv = ms_gemv * 1e3 / steps
-    res = {"leg": "w8_gemv_config1", "M": M, "K": K, "N": N, "kernel": "gemm8_skinny_kernel",
+    res = {"leg": "w8_gemv_config1", "M": M, "K": K, "N": N, "kernel": "gemm8_mid_kernel (16-row blocks)",
            "weights": "int8 per output channel (column) scales, prepacked once", "weight_sets": nsets,
            "rotate_bytes": nsets * K * N, "gemv_bytes": gemv_bytes,
            "us_per_step_quant_plus_gemv": round(us_step, 3), "us_per_gemv": round(us_gemv, 3),

@@ -1062,90 +1062,10 @@ __global__ __launch_bounds__(NTHREADS) void gemm8_fp8_dma_kernel(Gemm8Args p) {
 }
 
 // ---------------------------------------------------------------------------
-// Skinny int8 kernel (W8A8 with M <= 16, e.g. the M = 1 GEMV of config 1).
-// The 256x256 tile kernel would spend 255/256 of its MFMA work and all but
-// N/256 of its workgroups on nothing there.  Here a 256-thread workgroup
-// owns one 16-column tile and its eight waves split K; per 64-deep k step a
-// lane loads 16 contiguous k bytes of its column from the prepacked B^T (one
-// 1 KiB coalesced load per wave) and 16 of its row of A, and one
-// v_mfma_i32_16x16x64_i8 accumulates the 16 x 16 block (rows past M read
-// row M-1, their outputs are not stored).  The eight int32 partial blocks
-// are summed through LDS -- integer addition, so the result is the
-// reference's accumulator exactly -- and the epilogue is the tile kernel's.
-// ---------------------------------------------------------------------------
-constexpr int SK_WAVES = 8;
-constexpr int SK_BATCH = 8;  // k steps loaded before they are consumed
-
-template <int EPI>
-__global__ __launch_bounds__(64 * SK_WAVES) void gemm8_skinny_kernel(Gemm8Args p) {
-    __shared__ i32x4_t red[SK_WAVES][64];
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int n0 = blockIdx.x * 16;
-    const int col = n0 + (lane & 15);          // < Np: B^T rows are zero-padded to a multiple of 256
-    const int row = min(lane & 15, p.M - 1);   // the A row this lane feeds
-    const int kl = 16 * (lane >> 4);           // this lane's 16 k within a 64-deep step
-    const int steps = p.Kp / 64;
-    const int per = (steps + SK_WAVES - 1) / SK_WAVES;
-    const int s0 = min(wave * per, steps), s1 = min(s0 + per, steps);
-    const uint8_t* a_row = p.A + static_cast<size_t>(row) * p.K;
-    const uint8_t* b_col = p.Bt + static_cast<size_t>(col) * p.Kp;
-
-    i32x4_t acc = {0, 0, 0, 0};
-    for (int sb = s0; sb < s1; sb += SK_BATCH) {
-        u32x4_t a[SK_BATCH], b[SK_BATCH];
-#pragma unroll
-        for (int u = 0; u < SK_BATCH; ++u) {
-            // steps past this wave's range re-read its last one (discarded);
-            // k past K reads the row's last 16 bytes (B^T is zero there)
-            const int k = min(sb + u, s1 - 1) * 64 + kl;
-            a[u] = *reinterpret_cast<const u32x4_t*>(a_row + min(k, p.K - 16));
-            b[u] = *reinterpret_cast<const u32x4_t*>(b_col + k);
-        }
-#pragma unroll
-        for (int u = 0; u < SK_BATCH; ++u)
-            if (sb + u < s1) acc = mfma_i8_16x16x64(a[u], b[u], acc);
-    }
-    red[wave][lane] = acc;
-    __syncthreads();
-    if (wave != 0) return;
-    i32x4_t sum = red[0][lane];
-#pragma unroll
-    for (int w = 1; w < SK_WAVES; ++w) sum += red[w][lane];
-
-    // D element j of lane l: row 4*(l >> 4) + j, column n0 + (l & 15)
-    const int c = n0 + (lane & 15);
-    if (c >= p.N) return;
-    float bs = 0.0f;
-    if constexpr (EPI != EPI_I32) bs = p.Bs[c];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int r = 4 * (lane >> 4) + j;
-        if (r >= p.M) continue;
-        const size_t o = static_cast<size_t>(r) * p.N + c;
-        if constexpr (EPI == EPI_I32) {
-            static_cast<int32_t*>(p.C)[o] = sum[j];
-        } else {
-            float f = p.alpha * p.As[r];  // gemm_quant.cpp:44-46, left to right
-            f = f * bs;
-            f = f * static_cast<float>(sum[j]);
-            if constexpr (EPI == EPI_F32) {
-                // apply_beta (gemm_quant.cpp:12-21), then C += rescaled
-                float* Cp = static_cast<float*>(p.C);
-                const float base = (p.beta == 0.0f) ? 0.0f : (p.beta == 1.0f) ? Cp[o] : Cp[o] * p.beta;
-                Cp[o] = base + f;
-            } else {
-                static_cast<uint16_t*>(p.C)[o] = f32_to_bf16(0.0f + f);
-            }
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Mid-size int8 kernel (W8A8 with 16 < M <= kMidMaxM: batched decode).
-// There the 256x256 tile kernel runs ceil(N/256) workgroups -- 56 at N =
-// 14336, under a quarter of the CUs -- each walking all of K, and the rows
-// past M are MFMA work for nothing.  Here a 64 W-thread workgroup owns an
+// Small- and mid-size int8 kernel (W8A8 with M <= kMidMaxM: the M = 1 GEMV
+// of config 1 and batched decode).  There the 256x256 tile kernel runs
+// ceil(N/256) workgroups -- 56 at N = 14336, under a quarter of the CUs --
+// each walking all of K, and the rows past M are MFMA work for nothing.  Here a 64 W-thread workgroup owns an
 // output block of RB 16-row blocks by T 16-column tiles and its W waves
 // split K; per 64-deep k step a lane loads 16 contiguous k bytes of each of
 // its T B^T columns and RB A rows (1 KiB loads per wave), and RB * T
@@ -1154,7 +1074,8 @@ __global__ __launch_bounds__(64 * SK_WAVES) void gemm8_skinny_kernel(Gemm8Args p
 // is zero there).  BATCH k steps are loaded before they are consumed.
 // Waves 1.. hand their int32 blocks to wave 0 through LDS, which adds them
 // (integer addition: the reference's accumulator exactly) and writes the
-// skinny kernel's epilogue.
+// reference's epilogue (C += ((alpha * a_s) * b_s) * acc, no fused
+// multiply-add).
 // ---------------------------------------------------------------------------
 constexpr int kMidMaxM = 32;
 constexpr int kMidMaxFp8M = 128;
@@ -1383,7 +1304,7 @@ int launch_gemm8(const uint8_t* A, const uint8_t* Bt, const float* As, const flo
     // padding), else the register-staged kernel, which zeroes the K padding
     // of A before it reaches the MFMA
     static const int use_dma = env_int("LHQ_GEMM8_DMA", 1);
-    static const int use_skinny = env_int("LHQ_GEMM8_SKINNY", 1);
+    static const int use_small = env_int("LHQ_GEMM8_SKINNY", 1);
     if constexpr (OP == OP_FP8) {
         // up to 128 rows (K % 128 == 0): the mid-size kernel, 32 x 32 blocks
         // up to 32 rows, then 64 x 64 (the fp8 tile has no half tiles).
@@ -1400,12 +1321,18 @@ int launch_gemm8(const uint8_t* A, const uint8_t* Bt, const float* As, const flo
         if (use_dma && K % BK == 0) return launch_fp8_dma<DS_STAGES>(p, tiles, stream, who);
     }
     if constexpr (OP == OP_I8) {
-        if (use_skinny && M <= 16) {
-            gemm8_skinny_kernel<EPI><<<ceil_div(N, 16), 64 * SK_WAVES, 0, as_stream(stream)>>>(p);
+        // up to 16 rows: 16-row blocks of one 16-column tile, four waves
+        // each loading its whole K range (16 steps at K = 4096) at once.
+        // Measured against eight waves of eight steps (us, K = 4096): M = 1,
+        // N = 4096 (config 1) 6.45 -> 6.05; N = 14336: M = 1 14.8 -> 13.7,
+        // M = 8 17.8 -> 15.7, M = 16 20.5 -> 18.3 (16 waves of four steps
+        // 6.25 at config 1; two tiles on eight waves 7.74)
+        if (use_small && M <= 16) {
+            launch_mid<EPI, 1, 1, 4, 16, 2>(p, stream);
             return check_launch(who);
         }
         static const int mid_max = env_int("LHQ_GEMM8_MID", kMidMaxM);  // largest M for the mid-size kernel
-        if (M <= mid_max) {
+        if (use_small && M <= mid_max) {
 #ifdef LHQ_TUNING_KNOBS
             static const int mid_form = env_int("LHQ_GEMM8_MID_FORM", 0);
             switch (mid_form) {

@@ -29,7 +29,7 @@ def _quantized(oracle, M, K, N, seed, lo=-1.0, hi=1.0):
 
 
 SHAPES = [(32, 64, 48), (1, 4096, 4096), (255, 256, 257), (256, 512, 256), (300, 1024, 520),
-          (16, 208, 100), (7, 4096, 1000), (2, 48, 17),  # skinny kernel (M <= 16)
+          (16, 208, 100), (7, 4096, 1000), (2, 48, 17),  # small-size kernel (M <= 16, 16-row blocks)
           (513, 128, 1000), (4, 16, 4),
           (300, 1040, 520),  # K % 128 != 0 over several stages: the tile's clamped A loads meet zero-padded B
           # mid-size kernel (16 < M <= 32, 32 x 32 blocks), then whole or half tiles
