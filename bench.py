@@ -621,6 +621,78 @@ def bench_w8a8(ops, M, K, N, steps, warmup, seed=0):
     return res
 
 
+def bench_8bit_small_m(ops, steps, warmup, seed=0, K=4096, N=14336, ms=(1, 17, 32, 64, 128, 256, 512), nsets=6):
+    """W8A8 (bf16 output, and the reference's fp32 output with alpha = 1,
+    beta = 0) and FP8 e4m3 at batched-decode row counts, timed over `nsets`
+    rotating weight sets (6 x 58.7 MB at K=4096, N=14336, beyond the Infinity
+    Cache); random int8 / e4m3 operands.  Bytes: K*N weight codes + M*K
+    activations + 4 (M + N) scales + the output."""
+    import numpy as np
+    import torch
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed)
+    L = ops.lib().cdll
+    Bt8, Bs8, Bt_f8 = [], [], []
+    for _ in range(nsets):
+        W = torch.randn((K, N), generator=gen, device="cuda") * 0.02
+        Bq = ops.empty((K, N), np.int8)
+        Bs = ops.empty((N,), np.float32)
+        ops.lib().call("lhq_q8_quantize_per_col", W.data_ptr(), Bq.data_ptr(), Bs.data_ptr(), K, N, ops.stream())
+        Bt8.append(ops.prepack_b8(Bq, K, N))
+        Bs8.append(Bs)
+        del W, Bq
+        # e4m3 codes below 0x70 (finite, |v| < 256), either sign
+        f8 = torch.randint(0, 0x70, (K, N), dtype=torch.uint8, device="cuda", generator=gen)
+        f8 |= (torch.randint(0, 2, (K, N), dtype=torch.uint8, device="cuda", generator=gen) << 7)
+        Bt_f8.append(ops.prepack_b8(f8, K, N))
+        del f8
+    sa = torch.tensor([0.01], device="cuda")
+    sb = torch.tensor([0.02], device="cuda")
+    rows = []
+    for M in ms:
+        Aq = torch.randint(-127, 128, (M, K), dtype=torch.int8, device="cuda", generator=gen)
+        As = torch.rand((M,), device="cuda", generator=gen) * 0.01
+        A8 = torch.randint(0, 0x70, (M, K), dtype=torch.uint8, device="cuda", generator=gen)
+        Cb = ops.empty((M, N), np.int16)
+        Cf = torch.zeros((M, N), device="cuda")
+
+        def w8_bf16(i):
+            j = i % nsets
+            st = L.lhq_gemm_w8a8_bf16(Aq.data_ptr(), Bt8[j].data_ptr(), As.data_ptr(), Bs8[j].data_ptr(),
+                                      Cb.data_ptr(), M, N, K, ops.stream())
+            if st:
+                raise RuntimeError(ops.lib().last_error())
+
+        def w8_f32(i):
+            j = i % nsets
+            st = L.lhq_gemm_w8a8(Aq.data_ptr(), Bt8[j].data_ptr(), As.data_ptr(), Bs8[j].data_ptr(), Cf.data_ptr(),
+                                 M, N, K, 1.0, 0.0, ops.stream())
+            if st:
+                raise RuntimeError(ops.lib().last_error())
+
+        def fp8(i):
+            j = i % nsets
+            st = L.lhq_gemm_fp8_e4m3(A8.data_ptr(), Bt_f8[j].data_ptr(), sa.data_ptr(), sb.data_ptr(), Cf.data_ptr(),
+                                     M, N, K, 1.0, 0.0, ops.stream())
+            if st:
+                raise RuntimeError(ops.lib().last_error())
+
+        row = {"M": M, "K": K, "N": N}
+        for name, fn, ob in (("w8a8_bf16", w8_bf16, 2), ("w8a8_f32", w8_f32, 4), ("fp8_f32", fp8, 4)):
+            ms_, _ = GraphTimer(fn, nsets, chunk=nsets * 8).time(steps, warmup)
+            us = ms_ * 1e3 / steps
+            byts = K * N + M * K + 4 * (M + N) + M * N * ob
+            row[name] = {"us": round(us, 2), "gbs": round(byts / (us * 1e-6) / 1e9, 1),
+                         "hbm_frac": round(byts / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                         "tops": round(2.0 * M * K * N / (us * 1e-6) / 1e12, 1)}
+        rows.append(row)
+        del Aq, As, A8, Cb, Cf
+    del Bt8, Bs8, Bt_f8
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return rows
+
+
 def bench_w8_gemv(ops, steps, warmup, seed=0, K=4096, N=4096, min_rotate_bytes=2 * INFINITY_CACHE_BYTES + (1 << 26)):
     """Config 1: the W8 per-output-channel int8 GEMV through the reference's
     gemm_quant path (gemm_quant.cpp:29-49 at M=1).  One step is the
@@ -1000,7 +1072,7 @@ def main() -> int:
                     help="also run a 1 GiB device copy (PMC calibration kernel)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the W4A16 prefill and MoE legs")
     ap.add_argument("--only", choices=["w4a16", "w8a8", "prefill", "moe", "fp8", "configs", "mfma", "f32", "w8gemv",
-                                      "thin", "grouped"],
+                                      "thin", "grouped", "smallm"],
                     default=None,
                     help="run one leg only (profiling); prints that leg's summary, not the bench line")
     ap.add_argument("--moe-tokens", type=int, default=512,
@@ -1052,6 +1124,12 @@ def main() -> int:
         log(f"moe grouped W4A16 (config 4): {r['us_per_call']:.1f} us  {r['tflops']:.0f} TFLOPS "
             f"({100 * r['mfma_frac']:.1f}% of bf16 peak)")
         print(json.dumps({"leg": "moe_grouped_w4a16", **r}), flush=True)
+        return 0
+    if args.only == "smallm":
+        for r in bench_8bit_small_m(ops, 240, 24):
+            log(f"8-bit GEMMs M={r['M']} K={r['K']} N={r['N']}: W8A8 bf16 {r['w8a8_bf16']['us']:.1f} us, "
+                f"fp32 {r['w8a8_f32']['us']:.1f} us, FP8 {r['fp8_f32']['us']:.1f} us")
+            print(json.dumps({"leg": "8bit_small_m", **r}), flush=True)
         return 0
     if args.only == "w8gemv":
         r = bench_w8_gemv(ops, 500, 50)
