@@ -962,16 +962,19 @@ __global__ __launch_bounds__(NTHREADS) void gemm8_dma_kernel(Gemm8Args p) {
 // byte could be the NaN code, and NaN times the zero padding of B is NaN).
 // Rows past M read row M-1; those rows are never stored.
 // ---------------------------------------------------------------------------
-template <int STAGES>
+// JB: 32-column blocks per wave (4: a 256x256 tile; 2: a 256x128 half tile,
+// with JB B DMAs per wave and stage instead of 4).
+template <int STAGES, int JB = 4>
 __device__ __forceinline__ void dma_tile_fp8(const Gemm8Args& p, uint8_t* ds_lds, int m0, int n0,
                                              f32x16_t (&acc)[4][4]) {
-    constexpr int DPS = 8;  // DMAs per wave per stage: 4 of A, 4 of B
+    constexpr int DPS = 4 + JB;  // DMAs per wave per stage: 4 of A, JB of B
+    static_assert(JB == 4 || JB == 2, "whole or half tiles");
     static_assert(STAGES >= 3 && DPS * (STAGES - 2) <= 63, "vmcnt range");
     auto stage_buf = [&](int u) { return ds_lds + u * 2 * DS_OP_BYTES; };
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
-    uint32_t a_row[4], b_src[4];
+    uint32_t a_row[4], b_src[JB];
     int kca[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -979,19 +982,29 @@ __device__ __forceinline__ void dma_tile_fp8(const Gemm8Args& p, uint8_t* ds_lds
         const int r = c >> 2;
         kca[i] = ((c & 3) ^ ((r >> 2) & 3)) * 16;
         a_row[i] = static_cast<uint32_t>(min(m0 + r, p.M - 1)) * static_cast<uint32_t>(p.K);
-        b_src[i] = static_cast<uint32_t>(n0 + r) * static_cast<uint32_t>(p.Kp) + static_cast<uint32_t>(kca[i]);
+    }
+    // B rows n0 .. n0 + 64 JB - 1 (< Np: a half tile is the first or second
+    // half of a whole one)
+#pragma unroll
+    for (int i = 0; i < JB; ++i) {
+        const int c = (JB * wave + i) * 64 + lane;
+        const int r = c >> 2;
+        b_src[i] = static_cast<uint32_t>(n0 + r) * static_cast<uint32_t>(p.Kp) +
+                   static_cast<uint32_t>(((c & 3) ^ ((r >> 2) & 3)) * 16);
     }
     const int nk = p.Kp / DS_BK;
-    // DMA d of stage s (clamped to the last stage) into buf: A and B alternate
+    // DMA d of stage s (clamped to the last stage) into buf: A and B
+    // alternate while both last, then the rest of A
     auto dma = [&](uint8_t* buf, int s, int d) {
         const uint32_t k0 = static_cast<uint32_t>(min(s, nk - 1) * DS_BK);
-        const int i = d >> 1;
-        if (!(d & 1))
+        const bool is_b = d < 2 * JB && (d & 1);
+        const int i = d < 2 * JB ? d >> 1 : d - JB;
+        if (!is_b)
             __builtin_amdgcn_global_load_lds(p.A + (a_row[i] + k0 + static_cast<uint32_t>(kca[i])),
                                              (LHQ_LDS_AS void*)(buf + (4 * wave + i) * 1024), 16, 0, 0);
         else
             __builtin_amdgcn_global_load_lds(p.Bt + (b_src[i] + k0),
-                                             (LHQ_LDS_AS void*)(buf + DS_OP_BYTES + (4 * wave + i) * 1024), 16, 0,
+                                             (LHQ_LDS_AS void*)(buf + DS_OP_BYTES + (JB * wave + i) * 1024), 16, 0,
                                              0);
     };
 #pragma unroll
@@ -1001,8 +1014,8 @@ __device__ __forceinline__ void dma_tile_fp8(const Gemm8Args& p, uint8_t* ds_lds
 
     const int swz = ((lane & 31) >> 2) & 3;
     const int a_base = (wm * 128 + (lane & 31)) * DS_BK;
-    const int b_base = DS_OP_BYTES + (wn * 128 + (lane & 31)) * DS_BK;
-    u32x4_t f[8][2];  // [A blocks 0..3, B blocks 0..3][k half]
+    const int b_base = DS_OP_BYTES + (wn * 32 * JB + (lane & 31)) * DS_BK;
+    u32x4_t f[4 + JB][2];  // [A blocks 0..3, B blocks 0..JB-1][k half]
     auto read = [&](const uint8_t* buf, int x) {
         const int base = x < 4 ? a_base + x * 32 * DS_BK : b_base + (x - 4) * 32 * DS_BK;
 #pragma unroll
@@ -1016,14 +1029,14 @@ __device__ __forceinline__ void dma_tile_fp8(const Gemm8Args& p, uint8_t* ds_lds
     auto step = [&](uint8_t* cur, const uint8_t* next, int s) {
         rendezvous();
 #pragma unroll
-        for (int t = 0; t < 16; ++t) {
-            const int i = t >> 2, j = t & 3;
+        for (int t = 0; t < 4 * JB; ++t) {
+            const int i = t / JB, j = t % JB;
             acc[i][j] = mfma_fp8_32x32x64(f[4 + j][0], f[4 + j][1], f[i][0], f[i][1], acc[i][j]);
-            if (t < 8) dma(cur, s + STAGES, t);
-            if (j == 3 && i < 3) read(next, i);  // A block i is done
+            if (t < DPS) dma(cur, s + STAGES, t);
+            if (j == JB - 1 && i < 3) read(next, i);  // A block i is done
             if (i == 3) {
-                read(next, 4 + j);               // B block j is done
-                if (j == 3) read(next, 3);
+                read(next, 4 + j);                    // B block j is done
+                if (j == JB - 1) read(next, 3);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -1034,7 +1047,7 @@ __device__ __forceinline__ void dma_tile_fp8(const Gemm8Args& p, uint8_t* ds_lds
         for (int d = 0; d < DPS; ++d) dma(stage_buf(u), u, d);
     asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(DPS * (STAGES - 1)) : "memory");
 #pragma unroll
-    for (int x = 0; x < 8; ++x) read(stage_buf(0), x);
+    for (int x = 0; x < 4 + JB; ++x) read(stage_buf(0), x);
     for (int s = 0; s < nk; s += STAGES) {
 #pragma unroll
         for (int u = 0; u < STAGES; ++u)
@@ -1046,18 +1059,26 @@ __device__ __forceinline__ void dma_tile_fp8(const Gemm8Args& p, uint8_t* ds_lds
     __syncthreads();
     uint8_t* const area = ds_lds + wave * 32 * STAGED_PITCH;
     static_assert(4 * 32 * STAGED_PITCH <= STAGES * 2 * DS_OP_BYTES, "epilogue staging fits the stages");
-    if (m0 + BM <= p.M && n0 + BN <= p.N && p.N % 8 == 0 && p.c_vec)
-        gemm8_store_staged<EPI_F32, false, 4, true>(p, acc, m0, n0, wm, wn, lane, nullptr, area);
+    if (m0 + BM <= p.M && n0 + 64 * JB <= p.N && p.N % 8 == 0 && p.c_vec)
+        gemm8_store_staged<EPI_F32, false, JB, true>(p, acc, m0, n0, wm, wn, lane, nullptr, area);
     else
-        gemm8_store_staged<EPI_F32, true, 4, true>(p, acc, m0, n0, wm, wn, lane, nullptr, area);
+        gemm8_store_staged<EPI_F32, true, JB, true>(p, acc, m0, n0, wm, wn, lane, nullptr, area);
 }
 
+// One tile per workgroup; a launch of twice the tiles: every workgroup one
+// 256 x 128 half tile.
 template <int STAGES>
 __global__ __launch_bounds__(NTHREADS) void gemm8_fp8_dma_kernel(Gemm8Args p) {
     extern __shared__ __attribute__((aligned(1024))) uint8_t ds_lds[];
-    int tm, tn;
-    tile_of(blockIdx.x, p, tm, tn);
+    const int total = p.tiles_m * p.tiles_n;
     f32x16_t acc[4][4];
+    int tm, tn;
+    if (static_cast<int>(gridDim.x) == 2 * total) {
+        tile_of_id(blockIdx.x >> 1, p, tm, tn);
+        dma_tile_fp8<STAGES, 2>(p, ds_lds, tm * BM, tn * BN + (blockIdx.x & 1) * (BN / 2), acc);
+        return;
+    }
+    tile_of(blockIdx.x, p, tm, tn);
     dma_tile_fp8<STAGES>(p, ds_lds, tm * BM, tn * BN, acc);
 }
 
@@ -1078,7 +1099,7 @@ __global__ __launch_bounds__(NTHREADS) void gemm8_fp8_dma_kernel(Gemm8Args p) {
 // multiply-add).
 // ---------------------------------------------------------------------------
 constexpr int kMidMaxM = 32;
-constexpr int kMidMaxFp8M = 128;
+constexpr int kMidMaxFp8M = 32;
 
 // RB 16-row blocks by T 16-column tiles per workgroup, W waves splitting K,
 // BATCH k steps loaded before they are consumed, MINW workgroups per CU in
@@ -1273,7 +1294,11 @@ int launch_fp8_dma(const Gemm8Args& p, int tiles, void* stream, const char* who)
                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     if (attr != hipSuccess)
         return set_error(LHQ_ERR_HIP, "%s: dynamic LDS attribute: %s", who, hipGetErrorString(attr));
-    gemm8_fp8_dma_kernel<STAGES><<<tiles, NTHREADS, lds, as_stream(stream)>>>(p);
+    // tiles filling at most half the CUs: every workgroup a half tile
+    static const int halves = env_int("LHQ_GEMM8_HALVES", 1);
+    static const int cus = device_cus();
+    const int wgs = (halves && cus > 0 && 2 * tiles <= cus) ? 2 * tiles : tiles;
+    gemm8_fp8_dma_kernel<STAGES><<<wgs, NTHREADS, lds, as_stream(stream)>>>(p);
     return check_launch(who);
 }
 
@@ -1306,16 +1331,16 @@ int launch_gemm8(const uint8_t* A, const uint8_t* Bt, const float* As, const flo
     static const int use_dma = env_int("LHQ_GEMM8_DMA", 1);
     static const int use_small = env_int("LHQ_GEMM8_SKINNY", 1);
     if constexpr (OP == OP_FP8) {
-        // up to 128 rows (K % 128 == 0): the mid-size kernel, 32 x 32 blocks
-        // up to 32 rows, then 64 x 64 (the fp8 tile has no half tiles).
+        // up to 32 rows (K % 128 == 0): the mid-size kernel's 32 x 32 blocks.
         // K = 4096, N = 14336 (us, whole tiles / here): M = 1 40.9 / 15.9,
-        // M = 17 42.1 / 19.2, M = 32 44.2 / 22.9, M = 64 48.9 / 34.9, M = 128
-        // 55.4 / 46.9; a 16 x 16 block on 8 waves at M <= 16 measured 15.0 /
-        // 18.1 / 21.0 at M = 1 / 8 / 16 against 15.9 / 17.6 / 18.9
+        // M = 17 42.1 / 19.2, M = 32 44.2 / 22.9; a 16 x 16 block on 8 waves
+        // at M <= 16 measured 15.0 / 18.1 / 21.0 at M = 1 / 8 / 16 against
+        // 15.9 / 17.6 / 18.9.  Above, the tile kernel (half tiles where the
+        // tiles fill at most half the CUs); 64 x 64 blocks here took 34.7 /
+        // 46.4 us at M = 64 / 128
         static const int fp8_mid_max = env_int("LHQ_GEMM8_FP8_MID", kMidMaxFp8M);
         if (M <= fp8_mid_max && K % BK == 0) {
-            if (M <= 32) launch_mid<EPI_F32, 2, 2, 4, 8, 2, OP_FP8>(p, stream);
-            else launch_mid<EPI_F32, 4, 4, 4, 4, 2, OP_FP8>(p, stream);
+            launch_mid<EPI_F32, 2, 2, 4, 8, 2, OP_FP8>(p, stream);
             return check_launch(who);
         }
         if (use_dma && K % BK == 0) return launch_fp8_dma<DS_STAGES>(p, tiles, stream, who);
