@@ -18,7 +18,11 @@
 // the fp32 epilogue repeats the reference's multiply order with no fused
 // multiply-add, so the fp32 output is bit-exact too.  Workgroups are mapped
 // XCD-aware: consecutive tiles of one group of tile rows land on one XCD so
-// its L2 sees the A rows and B columns they share.
+// its L2 sees the A rows and B columns they share.  Where the tiles fill at
+// most half the CUs, every workgroup takes a 256x128 half tile instead; up to
+// 32 rows gemm8_mid_kernel runs 16x16 MFMA blocks straight from global
+// memory with K split across its waves (the M = 1 GEMV of config 1 and
+// batched decode).
 #include <cstdlib>
 #include <type_traits>
 
