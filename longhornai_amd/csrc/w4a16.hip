@@ -833,11 +833,18 @@ __device__ __forceinline__ uint32_t row8_sum(uint32_t x) {
     return x + dpp<0x141>(x);
 }
 
-template <bool F32A, bool ASYM, bool F32C, int T, int NPW, int BPS, bool GBIG, int MR>
+// GR (bf16, asymmetric weights): a ragged group table; grid.y walks the
+// groups' rows one at a time (resolve_group_rows with one-row blocks), each
+// workgroup staging its row and streaming its group's weight tiles; SWI:
+// the SwiGLU epilogue over the gate / up tile pair of the workgroup (T = 2).
+template <bool F32A, bool ASYM, bool F32C, int T, int NPW, int BPS, bool GBIG, int MR, bool GR = false,
+          bool SWI = false>
 __global__ __launch_bounds__(T == 1 ? 1024 : 512) void w4_decode_i8_kernel(W4Args p) {
     static_assert(BPS == 2 || BPS == 4, "scale segments of 64 or 128 k");
     static_assert(NPW == 4 || NPW == 8, "passes start at multiples of NPW tiles");
     static_assert(MR == 1 || MR == 4, "one row or all four");
+    static_assert(!GR || (MR == 1 && !F32A && ASYM && !F32C), "grouped: one bf16 row per workgroup");
+    static_assert(!SWI || (GR && T == 2), "SwiGLU: the gate / up pair of a grouped workgroup");
     constexpr int SEGS = 4 / BPS;
     constexpr int NZW = (BPS < 4) ? (NPW * SEGS + 7) / 8 : (GBIG ? NPW : 1);
     extern __shared__ __attribute__((aligned(16))) uint8_t q_lds[];
@@ -845,8 +852,19 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512) void w4_decode_i8_kernel(W4Arg
     const int S = blockDim.x >> 6;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int z = blockIdx.z;
-    const int Ml = min(p.M, 4);
+    const int z = GR ? 0 : blockIdx.z;
+    int m0 = 0;  // the group row of a grouped workgroup
+    const uint8_t* qw = p.qw;
+    const void* scales = p.scales;
+    const uint32_t* zeros = p.zeros;
+    if constexpr (GR) {
+        int e, m_end;
+        if (!resolve_group_rows(p, blockIdx.y, 1, e, m0, m_end)) return;  // uniform per workgroup
+        qw = p.qws[e];
+        scales = p.scs[e];
+        zeros = p.zss[e];
+    }
+    const int Ml = GR ? 1 : min(p.M, 4);
     const int col = lane & 15;
     const int Kp = p.Kt * kW4TileK;
     uint8_t* const dig = q_lds;
@@ -858,9 +876,9 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512) void w4_decode_i8_kernel(W4Arg
 #pragma unroll
     for (int t = 0; t < T; ++t) {
         const int64_t nt = min(static_cast<int>(blockIdx.x) * T + t, p.Nt - 1);
-        qwb[t] = p.qw + z * p.qw_bs + nt * p.Kt * kW4TileBytes;
-        scb[t] = static_cast<const char*>(p.scales) + (z * p.s_bs + nt * p.NG * 16) * (ASYM ? 2 : 4);
-        zwb[t] = ASYM ? reinterpret_cast<const char*>(p.zeros + z * p.z_bs + nt * p.NG8 * 16) : nullptr;
+        qwb[t] = qw + z * p.qw_bs + nt * p.Kt * kW4TileBytes;
+        scb[t] = static_cast<const char*>(scales) + (z * p.s_bs + nt * p.NG * 16) * (ASYM ? 2 : 4);
+        zwb[t] = ASYM ? reinterpret_cast<const char*>(zeros + z * p.z_bs + nt * p.NG8 * 16) : nullptr;
     }
     const uint32_t s_col = static_cast<uint32_t>(col * (ASYM ? 2 : 4));
 
@@ -902,7 +920,7 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512) void w4_decode_i8_kernel(W4Arg
     const int span = S * NPW;
     const int rc = Kp >> 3;  // 8-element chunks per padded row; 16 per K tile
     const int chunks = Ml * rc;
-    const char* A = static_cast<const char*>(p.A) + z * p.a_bs * (F32A ? 4 : 2);
+    const char* A = static_cast<const char*>(p.A) + (z * p.a_bs + static_cast<int64_t>(m0) * p.K) * (F32A ? 4 : 2);
     constexpr int B = 4;  // chunks per thread per batch
     u32x4_t av[B], av2[B];
     auto stage_load = [&](int c0) {
@@ -1104,6 +1122,22 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512) void w4_decode_i8_kernel(W4Arg
 #pragma unroll
         for (int j = 0; j < MR; ++j) red[((wave * T + t) * MR + j) * 64 + lane] = acc[t][j];
     __syncthreads();
+    if constexpr (SWI) {
+        // tiles 2j (gate) and 2j + 1 (up) -> act column tile j = blockIdx.x
+        for (int c = threadIdx.x; c < 16; c += 64 * S) {
+            float g = 0.0f, u = 0.0f;
+            for (int w2 = 0; w2 < S; ++w2) {
+                const float* gp = red + (w2 * T + 0) * 64 + c;
+                const float* up = red + (w2 * T + 1) * 64 + c;
+                g += gp[0] + gp[16] + gp[32];
+                u += up[0] + up[16] + up[32];
+            }
+            const int cn = static_cast<int>(blockIdx.x) * kW4TileN + c;
+            if (cn < p.N)
+                static_cast<uint16_t*>(p.C)[static_cast<int64_t>(m0) * p.N + cn] = f32_to_bf16(swiglu(g, u));
+        }
+        return;
+    }
     for (int idx = threadIdx.x; idx < T * MR * 16; idx += 64 * S) {
         const int t = idx / (MR * 16), j = (idx / 16) % MR, c = idx & 15;
         float sum = 0.0f;
@@ -1113,8 +1147,8 @@ __global__ __launch_bounds__(T == 1 ? 1024 : 512) void w4_decode_i8_kernel(W4Arg
         }
         const int ntt = static_cast<int>(blockIdx.x) * T + t;
         const int cn = ntt * kW4TileN + c;
-        if (j < p.M && cn < p.N && ntt < p.Nt)
-            w4_store<F32C>(p, z * p.c_bs + static_cast<int64_t>(j) * p.N + cn, sum);
+        if (j < (GR ? 1 : p.M) && cn < p.N && ntt < p.Nt)
+            w4_store<F32C>(p, z * p.c_bs + static_cast<int64_t>(m0 + j) * p.N + cn, sum);
     }
 }
 
@@ -2488,6 +2522,13 @@ void launch_i8_mr(const W4Args& a, dim3 grid, int S, size_t lds, hipStream_t s) 
     }
 }
 
+// The grouped integer decode (one row per workgroup, G = 128).
+template <int T, bool SWI>
+void launch_i8_grouped(const W4Args& a, dim3 grid, int S, size_t lds, hipStream_t s) {
+    lds = std::max(lds, static_cast<size_t>(S) * T * 64 * sizeof(float));  // the reduction reuses it
+    w4_decode_i8_kernel<false, true, false, T, 4, 4, false, 1, true, SWI><<<grid, 64 * S, lds, s>>>(a);
+}
+
 template <bool F32A, bool ASYM, bool F32C, int T, bool GR, bool SWI = false>
 void launch_gemv_waves(const W4Args& a, dim3 grid, int W, int bps, hipStream_t s) {
     switch (W) {
@@ -2750,6 +2791,34 @@ int launch_w4(W4Args a, int batch, hipStream_t s, int mblocks = -1) {
     // keeps a workgroup's LDS small enough for three per CU at K = 4096
     // while a group of up to four rows still streams its weights once.
     if constexpr (GR && !F32A && ASYM && !F32C) {
+        // At most max(2, groups / 2) rows in all: the integer decode, one row
+        // per workgroup, each streaming its group's weights, so rows * (one
+        // group's weights) are read however the rows spread.  The bf16 form
+        // below streams a group's weights once per block of rb rows.
+        // Measured, 8 experts of Mixtral shapes, gate/up + down: 1 token
+        // (2 rows) 23.1 + 11.9 us against 27.4 + 15.0; 2 tokens 42.7 + 21.9
+        // against 48.3 + 26.1; 4 tokens (8 rows) 76.9 + 39.9 against
+        // 72.5 + 44.9.
+        static const int env_gi8 = env_int("LHQ_W4_GI8");
+        static const int env_gmax = tuning_knob("LHQ_W4_GI8_MMAX", 0);
+        const int gi8_mmax = (env_gmax >= 1) ? env_gmax : std::max(2, a.num_groups / 2);
+        const size_t gi8_lds = static_cast<size_t>(a.Kt) * (3 * kW4TileK + 16);
+        if (env_gi8 >= 0 && env_dec >= 0 && a.M <= gi8_mmax && a.G == kW4TileK && gi8_lds <= static_cast<size_t>(kDecodeMaxLds)) {
+            const int T = (SWI || a.Nt >= 1024) ? 2 : 1;
+            const int smax = (T == 1) ? 16 : 8;
+            const int64_t cols = static_cast<int64_t>(ceil_div(a.Nt, T)) * a.M;
+            // as the bf16 grouped decode, at most 16 K tiles per wave
+            int S = 4;
+            while (S < smax && (cols * S < 2048 || a.Kt > 16 * S)) S *= 2;
+            S = max(1, min(S, ceil_div(a.Kt, 4)));
+            if (env_ds >= 1 && env_ds <= smax) S = env_ds;
+            // one-row blocks: exactly a.M of them, however the rows spread
+            dim3 grid(ceil_div(a.Nt, T), static_cast<unsigned>(a.M), 1);
+            if constexpr (SWI) launch_i8_grouped<2, true>(a, grid, S, gi8_lds, s);
+            else if (T == 1) launch_i8_grouped<1, false>(a, grid, S, gi8_lds, s);
+            else launch_i8_grouped<2, false>(a, grid, S, gi8_lds, s);
+            return check_launch("w4a16 grouped decode (int8 MFMA)");
+        }
         static const int env_grb = env_int("LHQ_W4_GRB");
         const int64_t row_bytes = static_cast<int64_t>(a.Kt) * kW4TileK * 2;
         const int rb_max = static_cast<int>(std::min<int64_t>(16, kDecodeMaxLds / row_bytes));

@@ -344,11 +344,13 @@ def test_w4a16_bf16_batched(oracle, ops, M):
         assert rel_frobenius(got[b], wants[b]) <= TOL_BF16
 
 
-def _grouped(oracle, ops, T, E, topk, K, N, G, seed, empty_expert=None):
+def _grouped(oracle, ops, T, E, topk, K, N, G, seed, empty_expert=None, one_expert=None):
     import torch
     ids = D.moe_routing(T, E, topk, seed)
     if empty_expert is not None:
         ids[ids == empty_expert] = (empty_expert + 1) % E
+    if one_expert is not None:  # every row on one expert (top-1 routing)
+        ids[:] = one_expert
     off, tok, _ = oracle.moe_dispatch_table(ids, E)
     X = D.to_bf16_bits(oracle, D.normal((T, K), 1.0, seed + 1))
     A = X[tok]  # dispatched rows, expert-major, token order kept (moe.cpp:124-139)
@@ -387,8 +389,12 @@ def test_w4a16_grouped_many_groups(oracle, ops, T, E, topk, K, N):
 
 
 @pytest.mark.parametrize("T,E,topk,K,N,G", [
-    (1, 8, 2, 4096, 256, 128),    # one token over 8 experts
-    (2, 4, 1, 256, 16400, 128),   # two column tiles per workgroup, N % 16 != 0
+    (1, 8, 2, 4096, 256, 128),    # one token over 8 experts (up to 2 rows, G = 128: the integer form)
+    (2, 4, 1, 256, 16400, 128),   # two column tiles per workgroup, N % 16 != 0 (2 rows, maybe in one group)
+    (1, 8, 2, 14336, 520, 128),   # the MoE down projection's K, N % 16 != 0
+    (1, 8, 1, 2048, 4096, 128),   # one row
+    (2, 8, 2, 4096, 300, 128),    # 4 rows over 8 groups (the integer form up to groups / 2 rows)
+    (3, 8, 2, 1024, 64, 128),     # 6 rows over 8 groups: the bf16 form
     (8, 8, 1, 512, 200, 64),      # G = 64
     (3, 4, 1, 1024, 96, 256),     # G = 256
     (6, 12, 2, 384, 48, 32),      # G = 32, 3 K tiles
@@ -397,9 +403,20 @@ def test_w4a16_grouped_many_groups(oracle, ops, T, E, topk, K, N):
 ])
 def test_w4a16_grouped_decode(oracle, ops, T, E, topk, K, N, G):
     """At most one row per group on average: the grouped decode kernel, each
-    group's rows staged in LDS in blocks of up to 4."""
+    group's rows staged in LDS in blocks of up to 4, or, up to max(2, groups / 2)
+    rows in all with G = 128, the integer-MFMA decode with one row per workgroup."""
     got, want, off = _grouped(oracle, ops, T=T, E=E, topk=topk, K=K, N=N, G=G, seed=50 + T)
     assert off[-1] == T * topk <= E
+    assert rel_frobenius(got, want) <= TOL_BF16
+
+
+@pytest.mark.parametrize("T,K,N", [(4, 4096, 300), (2, 14336, 64)])
+def test_w4a16_grouped_decode_rows_on_one_group(oracle, ops, T, K, N):
+    """All rows on one group, at most groups / 2 rows: the integer-MFMA
+    grouped decode streams that group's weights once per row."""
+    got, want, off = _grouped(oracle, ops, T=T, E=8, topk=1, K=K, N=N, G=128, seed=70 + T,
+                              one_expert=5)
+    assert off[5] == 0 and off[6] == T and off[-1] == T
     assert rel_frobenius(got, want) <= TOL_BF16
 
 
