@@ -344,7 +344,8 @@ def test_w4a16_bf16_batched(oracle, ops, M):
         assert rel_frobenius(got[b], wants[b]) <= TOL_BF16
 
 
-def _grouped(oracle, ops, T, E, topk, K, N, G, seed, empty_expert=None, one_expert=None):
+def _grouped(oracle, ops, T, E, topk, K, N, G, seed, empty_expert=None, one_expert=None,
+             bad_tokens=()):
     import torch
     ids = D.moe_routing(T, E, topk, seed)
     if empty_expert is not None:
@@ -352,7 +353,10 @@ def _grouped(oracle, ops, T, E, topk, K, N, G, seed, empty_expert=None, one_expe
     if one_expert is not None:  # every row on one expert (top-1 routing)
         ids[:] = one_expert
     off, tok, _ = oracle.moe_dispatch_table(ids, E)
-    X = D.to_bf16_bits(oracle, D.normal((T, K), 1.0, seed + 1))
+    xf = D.normal((T, K), 1.0, seed + 1)
+    for i, t in enumerate(bad_tokens):  # +Inf, -Inf, NaN in turn
+        xf[t, (37 * i + 11) % K] = (np.inf, -np.inf, np.nan)[i % 3]
+    X = D.to_bf16_bits(oracle, xf)
     A = X[tok]  # dispatched rows, expert-major, token order kept (moe.cpp:124-139)
     P_, S_, Z_ = [], [], []
     for e in range(E):
@@ -558,6 +562,24 @@ def test_w4a16_bf16_nonfinite_rows_are_nan(oracle, ops, M, K, N):
     if len(good):
         want[good] = oracle.gemm_w4a16_asym(np.ascontiguousarray(A[good]), p, s, z, N, G)
     _check_nonfinite(got, want, bad, TOL_BF16)
+
+
+@pytest.mark.parametrize("T,E,topk,K,N,bad", [
+    (2, 8, 2, 4096, 300, (1,)),        # 4 rows: the grouped integer decode
+    (3, 8, 2, 1024, 64, (0, 2)),       # 6 rows: the bf16 grouped decode
+    (64, 8, 2, 256, 1000, (3, 40, 63)),  # the 16-row kernel
+    (300, 4, 1, 256, 256, (0, 150, 299)),  # the tile kernel (~75 rows per group)
+])
+def test_w4a16_grouped_nonfinite_rows_are_nan(oracle, ops, T, E, topk, K, N, bad):
+    """The grouped launches: every dispatched row of a token holding +Inf,
+    -Inf or NaN is NaN in every column, the other rows as without them."""
+    seed = 90 + T
+    got, want, off = _grouped(oracle, ops, T=T, E=E, topk=topk, K=K, N=N, G=128, seed=seed,
+                              bad_tokens=bad)
+    _, tok, _ = oracle.moe_dispatch_table(D.moe_routing(T, E, topk, seed), E)
+    rows = np.flatnonzero(np.isin(tok, bad))
+    assert len(rows) == len(bad) * topk
+    _check_nonfinite(got, want, rows, TOL_BF16)
 
 
 @pytest.mark.parametrize("M,K,N", [(1, 4096, 2048), (16, 4096, 1024), (64, 1024, 512)])
