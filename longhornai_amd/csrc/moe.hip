@@ -137,6 +137,89 @@ __global__ __launch_bounds__(256) void moe_gather_kernel(const uint8_t* __restri
     }
 }
 
+// Dispatch in one launch for at most kSmallSlots slots (decode-sized
+// batches), where the two launches above cost more than their work.  Grid
+// (T, row chunks) as the gather.  Every workgroup holds all S ids in LDS and
+// finds the positions of its token's slots itself: slot s of expert e goes to
+// position #{valid s' : (e', s') < (e, s)} in (expert, slot) order, which is
+// offsets[e] + the earlier slots of e -- the placement of the two-launch path
+// (moe.cpp:111-139).  Then it copies its chunk of the token's row to each of
+// those positions.  Chunk 0 of each token writes its slot_pos / token_idx /
+// slot_idx entries; workgroup (0, 0) writes offsets[0..E] (histogram, then a
+// block scan) and the unplaced tail of token_idx / slot_idx.
+constexpr int kSmallSlots = 256;
+
+template <int VB>
+__global__ __launch_bounds__(kSmallSlots) void moe_dispatch_small_kernel(
+    const int32_t* __restrict__ ids, int S, int topk, int E, int32_t* __restrict__ offsets,
+    int32_t* __restrict__ token_idx, int32_t* __restrict__ slot_idx, int32_t* __restrict__ slot_pos,
+    const uint8_t* __restrict__ hidden, uint8_t* __restrict__ out, int64_t row_bytes) {
+    using V = typename VecOf<VB>::T;
+    __shared__ int32_t sid[kSmallSlots];    // expert of each slot, -1 where dropped
+    __shared__ int32_t spos[kMaxTopK];      // positions of this token's slots
+    __shared__ int32_t cnt[kMaxExperts];    // workgroup (0, 0): slots per expert
+    __shared__ int32_t wsum[kSmallSlots / 64];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int t = blockIdx.x;
+    const int my = tid < S ? ids[tid] : -1;
+    const bool valid = tid < S && my >= 0 && my < E;
+    sid[tid] = valid ? my : -1;
+    if (tid < topk) spos[tid] = 0;
+    __syncthreads();
+
+    for (int k = 0; k < topk; ++k) {
+        const int s = t * topk + k;
+        const int e = sid[s];  // the same in every lane
+        if (e < 0) continue;
+        const uint64_t b = __ballot(valid && (my < e || (my == e && tid < s)));
+        if (lane == 0 && b) atomicAdd(&spos[k], __popcll(b));
+    }
+    __syncthreads();
+
+    const int64_t off = (static_cast<int64_t>(blockIdx.y) * kSmallSlots + tid) * VB;
+    if (off < row_bytes) {
+        const V v = *reinterpret_cast<const V*>(hidden + static_cast<int64_t>(t) * row_bytes + off);
+        for (int k = 0; k < topk; ++k)
+            if (sid[t * topk + k] >= 0) *reinterpret_cast<V*>(out + static_cast<int64_t>(spos[k]) * row_bytes + off) = v;
+    }
+    if (blockIdx.y == 0 && tid < topk) {
+        const int s = t * topk + tid;
+        const bool ok = sid[s] >= 0;
+        slot_pos[s] = ok ? spos[tid] : -1;
+        if (ok) {
+            token_idx[spos[tid]] = t;
+            slot_idx[spos[tid]] = tid;
+        }
+    }
+    if (blockIdx.x != 0 || blockIdx.y != 0) return;  // (uniform over the workgroup)
+
+    for (int e = tid; e < kMaxExperts; e += kSmallSlots) cnt[e] = 0;
+    __syncthreads();
+    if (valid) atomicAdd(&cnt[my], 1);
+    __syncthreads();
+    // exclusive scan of cnt[0..E): thread i owns experts 2i and 2i+1
+    const int a = 2 * tid < E ? cnt[2 * tid] : 0;
+    const int b = 2 * tid + 1 < E ? cnt[2 * tid + 1] : 0;
+    int x = a + b;
+    for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(x, d);
+        if (lane >= d) x += y;
+    }
+    if (lane == 63) wsum[wave] = x;
+    __syncthreads();
+    for (int w = 0; w < wave; ++w) x += wsum[w];
+    const int excl = x - a - b;
+    if (2 * tid < E) offsets[2 * tid] = excl;
+    if (2 * tid + 1 < E) offsets[2 * tid + 1] = excl + a;
+    const int placed = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    if (tid == 0) offsets[E] = placed;
+    for (int s = placed + tid; s < S; s += kSmallSlots) {
+        token_idx[s] = -1;
+        slot_idx[s] = -1;
+    }
+}
+
 // slot_pos from token_idx / slot_idx (the inverse of the dispatch layout):
 // fill with -1, then one store per dispatched slot.
 __global__ void moe_fill_kernel(int32_t* p, int64_t n, int32_t v) {
@@ -305,18 +388,32 @@ int dispatch(const char* who, const void* hidden, int elem, const int32_t* ids, 
                 "%s: null pointer", who);
     hipStream_t s = as_stream(stream);
     const int S = T * topk;
-    moe_rank_kernel<<<1, kRankThreads, 0, s>>>(ids, S, topk, E, offsets, token_idx, slot_idx, slot_pos);
-    if (int st = check_launch(who)) return st;
-    if (T == 0) return LHQ_OK;
     const int64_t row_bytes = static_cast<int64_t>(H) * elem;
     const int vb = (row_bytes % 16 == 0 && aligned(hidden, 16) && aligned(out, 16)) ? 16
                    : (row_bytes % 4 == 0 && aligned(hidden, 4) && aligned(out, 4)) ? 4
                                                                                    : 2;
     const int64_t chunks = ceil_div64(row_bytes / vb, 256);
-    LHQ_SUPPORTED(chunks <= 65535, "%s: hidden_dim=%d too large", who, H);
+    LHQ_SUPPORTED(T == 0 || chunks <= 65535, "%s: hidden_dim=%d too large", who, H);
     const dim3 grid(static_cast<unsigned>(T), static_cast<unsigned>(chunks));
     const uint8_t* h = static_cast<const uint8_t*>(hidden);
     uint8_t* o = static_cast<uint8_t*>(out);
+    // one launch for decode-sized batches (T = 1, top-2 of 8, H = 4096 bf16:
+    // 4.5 us for the two launches)
+    if (S >= 1 && S <= kSmallSlots && topk <= kMaxTopK) {
+        if (vb == 16)
+            moe_dispatch_small_kernel<16><<<grid, kSmallSlots, 0, s>>>(ids, S, topk, E, offsets, token_idx, slot_idx,
+                                                                     slot_pos, h, o, row_bytes);
+        else if (vb == 4)
+            moe_dispatch_small_kernel<4><<<grid, kSmallSlots, 0, s>>>(ids, S, topk, E, offsets, token_idx, slot_idx,
+                                                                    slot_pos, h, o, row_bytes);
+        else
+            moe_dispatch_small_kernel<2><<<grid, kSmallSlots, 0, s>>>(ids, S, topk, E, offsets, token_idx, slot_idx,
+                                                                    slot_pos, h, o, row_bytes);
+        return check_launch(who);
+    }
+    moe_rank_kernel<<<1, kRankThreads, 0, s>>>(ids, S, topk, E, offsets, token_idx, slot_idx, slot_pos);
+    if (int st = check_launch(who)) return st;
+    if (T == 0) return LHQ_OK;
     if (vb == 16) moe_gather_kernel<16><<<grid, 256, 0, s>>>(h, slot_pos, o, row_bytes, topk);
     else if (vb == 4) moe_gather_kernel<4><<<grid, 256, 0, s>>>(h, slot_pos, o, row_bytes, topk);
     else moe_gather_kernel<2><<<grid, 256, 0, s>>>(h, slot_pos, o, row_bytes, topk);

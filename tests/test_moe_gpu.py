@@ -60,6 +60,14 @@ DISPATCH_CASES = [
     (300, 16, 3, 64, "dropped"),
     (257, 32, 2, 40, "skewed"),
     (0, 4, 2, 8, "uniform"),
+    # up to 256 slots: the one-launch form
+    (1, 8, 2, 4096, "uniform"),   # one decode token
+    (2, 8, 2, 4096, "skewed"),
+    (40, 16, 3, 64, "dropped"),
+    (64, 8, 4, 32, "repeat"),     # exactly 256 slots
+    (128, 512, 2, 6, "uniform"),  # 256 slots over the most experts
+    (86, 3, 3, 40, "repeat"),     # 258 slots: the two launches
+    (2, 100, 70, 8, "repeat"),    # top-70 (past the combine's 64): the two launches
 ]
 
 
