@@ -2804,11 +2804,14 @@ int launch_w4(W4Args a, int batch, hipStream_t s, int mblocks = -1) {
         const int gi8_mmax = (env_gmax >= 1) ? env_gmax : std::max(2, a.num_groups / 2);
         const size_t gi8_lds = static_cast<size_t>(a.Kt) * (3 * kW4TileK + 16);
         if (env_gi8 >= 0 && env_dec >= 0 && a.M <= gi8_mmax && a.G == kW4TileK && gi8_lds <= static_cast<size_t>(kDecodeMaxLds)) {
-            const int T = (SWI || a.Nt >= 1024) ? 2 : 1;
+            static const int env_gt = tuning_knob("LHQ_W4_GI8_T", 0);
+            const int T = (SWI || (env_gt == 0 ? a.Nt >= 1024 : env_gt == 2)) ? 2 : 1;
             const int smax = (T == 1) ? 16 : 8;
             const int64_t cols = static_cast<int64_t>(ceil_div(a.Nt, T)) * a.M;
-            // as the bf16 grouped decode, at most 16 K tiles per wave
-            int S = 4;
+            // at most 16 K tiles per wave, as the bf16 grouped decode, from
+            // 2 waves (gate/up at one token, K = 4096: 21.0-21.5 us with 2
+            // waves, 22.4 with 4)
+            int S = 2;
             while (S < smax && (cols * S < 2048 || a.Kt > 16 * S)) S *= 2;
             S = max(1, min(S, ceil_div(a.Kt, 4)));
             if (env_ds >= 1 && env_ds <= smax) S = env_ds;
