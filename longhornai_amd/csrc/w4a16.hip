@@ -2740,6 +2740,11 @@ int launch_w4(W4Args a, int batch, hipStream_t s, int mblocks = -1) {
         // 17.5 us against 18.3 with 4)
         int S = 4;
         while (S < smax && (cols * S < 2048 || a.Kt > 32 * S)) S *= 2;
+        // two waves where K is at most 32 tiles and two still give 7 waves
+        // per CU (us, 4 waves -> 2: K=4096, N=28672 12.8 -> 12.1; N=14336
+        // 8.2 -> 7.8; K=2048, N=16384 6.3 -> 5.5; fewer columns lose:
+        // K=4096, N=11008 6.8 -> 7.2, N=8192 5.5 -> 6.9)
+        if (a.Kt <= 32 && cols * 2 >= int64_t{7} * device_cus()) S = 2;
         S = max(1, min(S, ceil_div(a.Kt, 4)));
         if (env_ds >= 1 && env_ds <= smax) S = env_ds;
         dim3 grid(ceil_div(a.Nt, T), 1, batch);

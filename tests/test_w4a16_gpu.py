@@ -270,7 +270,8 @@ def test_w4a16_bf16_ragged_k(oracle, ops, M, K, N, G):
 # whole block, with one and two column tiles per wave (Nt < 1024 and >= 1024,
 # odd Nt), G = 64 (also with a ragged last K tile), 128 and 256.
 INT8_DECODE_CASES = [
-    (1, 4096, 16400, 128),
+    (1, 4096, 16400, 128),  # K <= 32 tiles with >= 896 column tiles: two waves per workgroup
+    (1, 4096, 14336, 128),  # 896 column tiles: the two-wave rule's edge on 256 CUs
     (1, 1024, 272, 64),
     (1, 4160, 72, 64),
     (1, 2048, 16400, 256),
