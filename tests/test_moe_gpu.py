@@ -251,6 +251,7 @@ def _swiglu_case(oracle, ops, T, E, K, H, I, G, seed, kind="uniform"):
     (1, 8, 2, 4096, 256, 128, "uniform"),   # one token, two experts (the integer-MFMA form)
     (1, 8, 2, 2048, 1000, 128, "uniform"),  # ... I % 16 != 0
     (2, 8, 2, 2048, 300, 128, "skewed"),    # 4 rows, two on expert 0 (integer form)
+    (2, 8, 2, 1024, 72, 128, "dropped"),    # integer form, row capacity past offsets[E]
     (5, 8, 1, 512, 72, 64, "uniform"),      # G = 64, I % 16 != 0
     (10, 16, 1, 384, 48, 32, "skewed"),     # 7 rows of one expert: two row blocks; G = 32
     (6, 12, 2, 1024, 40, 256, "dropped"),   # G = 256, ids outside [0, E) dropped
