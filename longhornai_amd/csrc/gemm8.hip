@@ -1343,6 +1343,14 @@ int launch_gemm8(const uint8_t* A, const uint8_t* Bt, const float* As, const flo
         // tiles fill at most half the CUs); 64 x 64 blocks here took 34.7 /
         // 46.4 us at M = 64 / 128
         static const int fp8_mid_max = env_int("LHQ_GEMM8_FP8_MID", kMidMaxFp8M);
+        // up to 16 rows the int8 form below: 16-row blocks of one 16-column
+        // tile, four waves each loading its whole K range at once (us, K =
+        // 4096, N = 14336, 32 x 32 blocks -> this: M = 1 15.9 -> 13.2-13.7,
+        // M = 4 16.8 -> 14.7-15.0, M = 8 17.4 -> 15.9, M = 16 18.8 -> 18.9)
+        if (M <= 16 && M <= fp8_mid_max && K % BK == 0) {
+            launch_mid<EPI_F32, 1, 1, 4, 16, 2, OP_FP8>(p, stream);
+            return check_launch(who);
+        }
         if (M <= fp8_mid_max && K % BK == 0) {
             launch_mid<EPI_F32, 2, 2, 4, 8, 2, OP_FP8>(p, stream);
             return check_launch(who);

@@ -157,14 +157,17 @@ def test_fp8_matches_oracle(oracle, ops, M, K, N, alpha, beta):
     (129, 128, 64),     # two k stages, fewer than the pipeline's buffers (one tile: two half tiles,
                         # the second wholly past N)
     (2048, 256, 4200),  # 136 tiles: whole 256 x 256 tiles (half tiles only where they fill at most half the CUs)
-    # up to 128 rows: the mid-size kernel (32 x 32 blocks up to 32 rows, then 64 x 64)
-    (1, 4096, 1000), (17, 1024, 520), (32, 128, 64), (100, 2048, 1000), (128, 4096, 256),
+    # up to 16 rows: the mid-size kernel's 16-row blocks (four waves over K)
+    (1, 4096, 1000), (5, 128, 1000), (8, 1024, 520), (16, 2048, 72),
+    # then 32 x 32 blocks up to 32 rows, then half tiles
+    (17, 1024, 520), (32, 128, 64), (100, 2048, 1000), (128, 4096, 256),
 ])
 @pytest.mark.parametrize("alpha,beta", [(1.0, 0.0), (0.5, 2.0)])
 def test_fp8_dma_path(oracle, ops, M, K, N, alpha, beta):
     """K % 128 == 0 runs the mid-size kernel (16x16x32 fp8 MFMAs, K split across
-    waves) up to 128 rows and the LDS-DMA kernel on the 32x32x64 f8f6f4 MFMA
-    above (256 x 128 half tiles where the tiles fill at most half the CUs).  A NaN code in A (0x7f) and in B (0xff) make exactly their row /
+    waves; 16-row blocks up to 16 rows, 32 x 32 blocks up to 32) and the LDS-DMA
+    kernel on the 32x32x64 f8f6f4 MFMA above (256 x 128 half tiles where the
+    tiles fill at most half the CUs).  A NaN code in A (0x7f) and in B (0xff) make exactly their row /
     column NaN, as in the reference's fp32 loop."""
     A = D.normal((M, K), 1.0, 70 + M)
     B = D.normal((K, N), 0.05, 71 + N)
